@@ -1,0 +1,348 @@
+#!/usr/bin/env python3
+"""Benchmark of the HIP device on one MI355X; prints ONE JSON line.
+
+Headline workload: the fused broadcast chain
+  z = tanh((x + bias) * scale) * sigmoid(x) - 0.1 * x * x
+with x (8192, 4096), bias (4096,), scale (8192, 1), fp32, seed 1. A step builds
+the lazy graph and realizes it (one fused kernel). value = algorithmic HBM bytes
+per step / step time (GB/s); inputs are resident in HBM before the timed region
+and rotate over 3 copies (3 x 128 MiB > the 256 MB Infinity Cache).
+
+roofline: the same kernel timed with HIP events on the library's stream over
+back-to-back launches of pre-built graphs. cpu_baseline: the CPU oracle
+(restatement of Ormi's CPU backend, one core) on a bounded row sample.
+"extra" carries the other configs (C1, C3, C4, C5), each with its own roofline.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+FP32_PEAK_TFLOPS = 157.3
+METRIC = json.loads((ROOT / "BASELINE.json").read_text())["metric"]
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+class Events:
+    """HIP events on libormi_hip's stream (the null stream every launch uses)."""
+
+    def __init__(self):
+        self.lib = ctypes.CDLL(str(ROOT / "ormi_amd" / "lib" / "libormi_hip.so"))
+        self.lib.ormi_hip_event_create.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.lib.ormi_hip_event_record.argtypes = [ctypes.c_void_p]
+        self.lib.ormi_hip_event_elapsed_ms.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(ctypes.c_float)]
+        self.lib.ormi_hip_synchronize.argtypes = []
+
+    def new(self):
+        e = ctypes.c_void_p()
+        assert self.lib.ormi_hip_event_create(ctypes.byref(e)) == 0
+        return e
+
+    def record(self, e):
+        assert self.lib.ormi_hip_event_record(e) == 0
+
+    def elapsed_ms(self, a, b) -> float:
+        ms = ctypes.c_float()
+        assert self.lib.ormi_hip_event_elapsed_ms(a, b, ctypes.byref(ms)) == 0
+        return ms.value
+
+    def sync(self):
+        assert self.lib.ormi_hip_synchronize() == 0
+
+
+def timed_launches(ev: Events, make, n: int) -> float:
+    """Average ms per realize over n back-to-back realizations of pre-built graphs."""
+    graphs = [make(i) for i in range(n)]
+    ev.sync()
+    a, b = ev.new(), ev.new()
+    ev.record(a)
+    for g in graphs:
+        g.realize()
+    ev.record(b)
+    return ev.elapsed_ms(a, b) / n
+
+
+# ------------------------------------------------------------------ workloads
+def c2_arrays(rows=8192, cols=4096, seed=1):
+    rng = np.random.default_rng(seed)
+    x = rng.normal(0, 1, (rows, cols)).astype(np.float32)
+    bias = rng.normal(0, 0.1, (cols,)).astype(np.float32)
+    scale = rng.uniform(0.5, 1.5, (rows, 1)).astype(np.float32)
+    return x, bias, scale
+
+
+def c2_graph(X, B, S):
+    return ((X + B) * S).tanh() * X.sigmoid() - 0.1 * X * X
+
+
+def c2_bytes(rows=8192, cols=4096):
+    return 4 * (rows * cols * 2 + cols + rows)  # read x, bias, scale; write z
+
+
+def cpu_baseline_c2(target_s: float = 10.0) -> dict:
+    """Oracle on one core: per-node execute_graph (what Ormi's CPU backend does on
+    .numpy()) over a row sample of the C2 workload, repeated to ~target_s."""
+    import oracle
+    from ormi_amd import Tensor
+
+    oracle.load()
+    rows, cols = 1024, 4096
+    x, bias, scale = c2_arrays(8192, cols)
+    x, scale = x[:rows], scale[:rows]
+    X, B, S = Tensor(x, "cpu"), Tensor(bias, "cpu"), Tensor(scale, "cpu")
+    t0 = time.perf_counter()
+    c2_graph(X, B, S).numpy()
+    one = time.perf_counter() - t0
+    reps = max(1, min(20, int(target_s / max(one, 1e-3))))
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        c2_graph(X, B, S).realize()
+    per = (time.perf_counter() - t0) / reps
+    # The fused tape (execute_jit on the whole chain), the favourable CPU case.
+    from ormi_amd import ormi_backend as ob
+
+    t0 = time.perf_counter()
+    z = c2_graph(X, B, S)
+    ob.execute_jit(z._node)
+    fused = time.perf_counter() - t0
+    gbs = c2_bytes(rows, cols) / per / 1e9
+    return {
+        "value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+        "sample": f"C2 rows 0..{rows} of (8192,4096) (1/8 of the workload), per-node execute_graph, "
+                  f"{reps} reps, {per * 1e3:.1f} ms/rep; fused-tape execute_jit {fused * 1e3:.1f} ms "
+                  f"({c2_bytes(rows, cols) / fused / 1e9:.4f} GB/s); host {os.cpu_count()} cpus visible",
+    }
+
+
+def bench_c2(args, ev: Events) -> dict:
+    from ormi_amd import Tensor
+
+    log("C2: generating inputs")
+    x, bias, scale = c2_arrays()
+    sets = []
+    for k in range(3):
+        xs = x if k == 0 else np.ascontiguousarray(np.roll(x, k, axis=0))
+        sets.append((Tensor(xs, "hip"), Tensor(bias, "hip"), Tensor(scale, "hip")))
+    for i in range(args.warmup):
+        c2_graph(*sets[i % 3]).realize()
+    ev.sync()
+    log("C2: timed steps")
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        c2_graph(*sets[i % 3]).realize()
+    ev.sync()
+    step_s = (time.perf_counter() - t0) / args.steps
+    kernel_ms = timed_launches(ev, lambda i: c2_graph(*sets[i % 3]), max(args.steps, 20))
+    nbytes = c2_bytes()
+    return {
+        "step_s": step_s,
+        "value": nbytes / step_s / 1e9,
+        "roofline": {"bound": "hbm", "achieved": round(nbytes / (kernel_ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(nbytes / (kernel_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel_us": round(kernel_ms * 1e3, 2), "bytes_per_launch": nbytes},
+    }
+
+
+def bench_c3(ev: Events, n: int) -> dict:
+    from ormi_amd import Tensor
+
+    log("C3: generating inputs")
+    x = np.random.default_rng(2).normal(0, 2, (16384, 8192)).astype(np.float32)
+    X = [Tensor(x, "hip"), Tensor(np.ascontiguousarray(x[::-1]), "hip")]
+    M = [t.max(1, keepdims=True).realize() for t in X]
+    rows, cols = x.shape
+    inb = rows * cols * 4
+    work = {
+        "row_max": (lambda i: X[i % 2].max(1), inb + rows * 4),
+        "row_sumexp": (lambda i: (X[i % 2] - M[i % 2]).exp().sum(1), inb + rows * 4 + rows * 4),
+        "row_mean": (lambda i: X[i % 2].mean(1), inb + rows * 4),
+        "row_argmax": (lambda i: X[i % 2].argmax(1), inb + rows * 8),
+        "col_sum": (lambda i: X[i % 2].sum(0), inb + cols * 4),
+    }
+    out = {}
+    for name, (make, nbytes) in work.items():
+        make(0).realize()
+        ms = timed_launches(ev, make, n)
+        out[name] = {"us": round(ms * 1e3, 2), "GB/s": round(nbytes / ms / 1e6, 1),
+                     "frac_hbm": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4), "bytes": nbytes}
+    return out
+
+
+def bench_c1(ev: Events, n: int) -> dict:
+    from ormi_amd import Tensor
+
+    rng = np.random.default_rng(0)
+    a, b, c = (rng.uniform(-1, 1, (1024, 1024)).astype(np.float32) for _ in range(3))
+    A, B, C = (Tensor(v, "hip", requires_grad=True) for v in (a, b, c))
+
+    def fwd(i):
+        return ((A * B + C).relu() * 0.5).sum(1)
+
+    fwd(0).realize()
+    ms_f = timed_launches(ev, fwd, n)
+
+    def grads():
+        for t in (A, B, C):
+            t.zero_grad()
+        y = fwd(0)
+        y.sum().backward()
+        return [A.grad, B.grad, C.grad]
+
+    [g.realize() for g in grads()]
+    gs = [grads() for _ in range(n)]
+    ev.sync()
+    e0, e1 = ev.new(), ev.new()
+    ev.record(e0)
+    for trio in gs:
+        for g in trio:
+            g.realize()
+    ev.record(e1)
+    ms_b = ev.elapsed_ms(e0, e1) / n
+    fb, bb = 12587008, 50331648
+    return {"fwd_us": round(ms_f * 1e3, 2), "fwd_GB/s": round(fb / ms_f / 1e6, 1),
+            "bwd_us": round(ms_b * 1e3, 2), "bwd_GB/s": round(bb / ms_b / 1e6, 1),
+            "note": "fwd one fused reduce kernel (incl. the y.sum() realize of forward y in bwd); "
+                    "bwd three fused kernels (one per gradient root)"}
+
+
+def bench_c4(ev: Events, n: int) -> dict:
+    from ormi_amd import Tensor
+
+    log("C4: GEMMs")
+    rng = np.random.default_rng(3)
+    a = rng.normal(0, 1 / 64, (4096, 4096)).astype(np.float32)
+    b = rng.normal(0, 1 / 64, (4096, 4096)).astype(np.float32)
+    A, B = Tensor(a, "hip", dtype="bfloat16"), Tensor(b, "hip", dtype="bfloat16")
+    (A @ B).realize()
+    ms = timed_launches(ev, lambda i: A @ B, n)
+    flops = 2 * 4096 ** 3
+    out = {"bf16_4096": {"us": round(ms * 1e3, 2), "TFLOP/s": round(flops / ms / 1e9, 1),
+                         "frac_mfma": round(flops / ms / 1e9 / BF16_PEAK_TFLOPS, 4)}}
+    a32 = rng.normal(0, 1 / 64, (2048, 1024)).astype(np.float32)
+    b32 = rng.normal(0, 1 / 64, (1024, 4096)).astype(np.float32)
+    dc = rng.normal(0, 1, (2048, 4096)).astype(np.float32)
+    A32, B32, DC = Tensor(a32, "hip"), Tensor(b32, "hip"), Tensor(dc, "hip")
+    f32 = 2 * 2048 * 1024 * 4096
+    for name, make in (("fp32_fwd_NN", lambda i: A32 @ B32),
+                       ("fp32_dA_NT", lambda i: DC @ B32.transpose()),
+                       ("fp32_dB_TN", lambda i: A32.transpose() @ DC)):
+        make(0).realize()
+        ms = timed_launches(ev, make, n)
+        out[name] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(f32 / ms / 1e9, 1),
+                     "frac_mfma": round(f32 / ms / 1e9 / FP32_PEAK_TFLOPS, 4)}
+    return out
+
+
+def bench_c5(ev: Events, steps: int) -> dict:
+    from ormi_amd import Tensor
+    from ormi_amd.ormi_backend import Node
+
+    log("C5: MLP step")
+    rng = np.random.default_rng(4)
+    dims = [1024, 4096, 4096, 1024]
+    X = Tensor(rng.normal(0, 1, (1024, 1024)).astype(np.float32), "hip")
+    Y = Tensor(rng.normal(0, 1, (1024, 1024)).astype(np.float32), "hip")
+    W = [rng.uniform(-math.sqrt(6 / i), math.sqrt(6 / i), (i, o)).astype(np.float32) for i, o in zip(dims, dims[1:])]
+    ws = [Tensor(w, "hip", requires_grad=True) for w in W]
+
+    def step(ws):
+        h = X
+        for i, w in enumerate(ws):
+            h = h @ w
+            if i < len(ws) - 1:
+                h = h.gelu()
+        d = h - Y
+        loss = (d * d).sum() * (1.0 / (1024 * 1024))
+        loss.backward()
+        # New leaves each step so graphs do not chain across steps.
+        out = []
+        for w in ws:
+            u = (w - w.grad * 1e-3).realize()
+            out.append(Tensor(_node=Node(u._node.data, True, u._node.device), device="hip"))
+        return loss, out
+
+    loss0, ws = step(ws)
+    first = float(loss0.numpy())
+    ev.sync()
+    e0, e1 = ev.new(), ev.new()
+    ev.record(e0)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        loss, ws = step(ws)
+    ev.record(e1)
+    ms = ev.elapsed_ms(e0, e1) / steps
+    wall = (time.perf_counter() - t0) / steps
+    last = float(loss.numpy())
+    flops = 146028888064
+    return {"step_ms": round(ms, 3), "wall_ms": round(wall * 1e3, 3), "gemm_TFLOP/s": round(flops / ms / 1e9, 1),
+            "frac_fp32": round(flops / ms / 1e9 / FP32_PEAK_TFLOPS, 4), "loss_first": first, "loss_last": last}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-extra", action="store_true", help="only the headline workload")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
+              "multi-GPU sharding is described in DESIGN.md, not implemented.", file=sys.stderr)
+        sys.exit(2)
+
+    import ormi_amd
+
+    if not ormi_amd.ormi_backend.hip_available():
+        raise SystemExit("bench.py: HIP device unavailable (no GPU visible); refusing to report a number.")
+    ev = Events()
+    main_res = bench_c2(args, ev)
+    extra = {}
+    if not args.no_extra:
+        n = max(10, min(args.steps, 30))
+        extra["C1_fused_pointwise_rowsum_1024"] = bench_c1(ev, n)
+        extra["C3_reductions_16384x8192"] = bench_c3(ev, n)
+        extra["C4_gemm"] = bench_c4(ev, n)
+        extra["C5_mlp_step_ms"] = bench_c5(ev, max(3, min(args.steps // 10, 10)))
+    cpu = None if args.no_cpu else cpu_baseline_c2()
+    line = {
+        "metric": METRIC,
+        "value": round(main_res["value"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(main_res["step_s"] * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (numpy default_rng seeds from BASELINE.json configs)",
+        "config": {"workload": "C2 fused broadcast chain tanh((x+bias)*scale)*sigmoid(x)-0.1*x*x, "
+                               "x (8192,4096) fp32, bias (4096,), scale (8192,1), seed 1",
+                   "bytes_per_step": c2_bytes(), "parallelism": "single GPU"},
+        "roofline": main_res["roofline"],
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,153 @@
+/*
+ * ormi_hip.h — C ABI of libormi_hip.so, the MI355X (gfx950) device layer.
+ *
+ * The host C++ core (graph, autograd, fusion scheduler, hipRTC code generator)
+ * reaches the GPU only through these functions. No C++ or torch types cross
+ * this boundary: plain pointers, sizes and small POD descriptors.
+ *
+ * Conventions
+ *   - Every function returns ORMI_HIP_OK (0) on success or a nonzero ORMI_HIP_ERR_*
+ *     code; ormi_hip_last_error() then returns a message (thread-local).
+ *   - All device work is ordered on the device's null stream, as the reference
+ *     launches on the legacy default stream (csrc/backend/cuda/jit.cu:40).
+ *     Copies to the host synchronize (csrc/backend/cuda/allocator.cu:89-91).
+ *   - Device pointers belong to the caller. Compiled modules and kernel
+ *     handles belong to the library's cache and live until process exit.
+ *   - Memory entry points are thread-safe; launches are issued in call order.
+ */
+#ifndef ORMI_HIP_H
+#define ORMI_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ORMI_HIP_OK               0
+#define ORMI_HIP_ERR_RUNTIME      1  /* a HIP runtime call failed               */
+#define ORMI_HIP_ERR_NO_DEVICE    2  /* no usable GPU in this process           */
+#define ORMI_HIP_ERR_INVALID      3  /* bad argument (null, size, shape, dtype)  */
+#define ORMI_HIP_ERR_COMPILE      4  /* hipRTC rejected the source              */
+#define ORMI_HIP_ERR_UNSUPPORTED  5  /* valid request this build does not cover */
+
+/* Element type codes; the numbering is ormi::DType's. */
+#define ORMI_DTYPE_F32   0
+#define ORMI_DTYPE_I32   1
+#define ORMI_DTYPE_BOOL  2
+#define ORMI_DTYPE_BF16  3
+#define ORMI_DTYPE_F16   4
+#define ORMI_DTYPE_I64   5
+
+/* ---------------------------------------------------------------- device --
+ * Replaces the CUDA driver set-up in CUDAAllocator's constructor
+ * (reference csrc/backend/cuda/allocator.cu:20-25). ormi_hip_init fails with
+ * ORMI_HIP_ERR_NO_DEVICE when no GPU is visible, which makes the HIP device
+ * absent the same way a throwing CUDAAllocator constructor does
+ * (reference csrc/tests/test_utils.h:17-21). */
+int ormi_hip_device_count(int* count);
+int ormi_hip_init(int device);
+
+typedef struct ormi_hip_props {
+    char     name[64];         /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+    int      compute_units;    /* 256 on MI355X                              */
+    int      clock_khz;
+    int      lds_bytes_per_block;
+    size_t   total_mem_bytes;
+} ormi_hip_props;
+int ormi_hip_get_props(ormi_hip_props* out);
+
+/* Message for the last failing call on this thread ("" if none).
+ * Replaces the exceptions thrown by CUDA_SAFE_CALL / NVRTC_SAFE_CALL
+ * (reference csrc/utils/macros.h:8-19); the C++ side rethrows it as
+ * std::runtime_error("HIP Error: ..."). */
+const char* ormi_hip_last_error(void);
+
+/* ---------------------------------------------------------------- memory --
+ * Backs HIPAllocator : IAllocator (reference interface csrc/core/allocator.h:7-21,
+ * CUDA implementation csrc/backend/cuda/allocator.cu:36-95). */
+int ormi_hip_malloc(void** ptr, size_t bytes);                       /* cuMemAlloc   allocator.cu:47 */
+int ormi_hip_free(void* ptr);                                        /* cuMemFree    allocator.cu:30 */
+int ormi_hip_memset_d8(void* dst, unsigned char value, size_t count);/* cuMemsetD8   allocator.cu:58,81 */
+int ormi_hip_memset_d32(void* dst, uint32_t value, size_t count);    /* cuMemsetD32  allocator.cu:76 */
+/* Fill count elements of elem_bytes (1, 2, 4 or 8) with the pattern at value
+ * (a kernel, so it is safe inside stream capture). fill_n for every dtype. */
+int ormi_hip_fill(void* dst, const void* value, size_t elem_bytes, size_t count);
+int ormi_hip_memcpy_h2d(void* dst, const void* src, size_t bytes);   /* cuMemcpyHtoD allocator.cu:94 */
+int ormi_hip_memcpy_d2h(void* dst, const void* src, size_t bytes);   /* cuMemcpyDtoH allocator.cu:90 */
+int ormi_hip_memcpy_d2d(void* dst, const void* src, size_t bytes);   /* cuMemcpyDtoD allocator.cu:62 */
+int ormi_hip_synchronize(void);
+
+/* Contiguous element-type conversion dst[i] = (dst_dtype) src[i]. Float to
+ * bf16/fp16 rounds to nearest even. Used for bf16 leaves and casts. */
+int ormi_hip_convert(void* dst, int dst_dtype, const void* src, int src_dtype, size_t count);
+
+/* ------------------------------------------------------------- hipRTC JIT --
+ * Replaces compile_ptx + cuModuleLoadDataEx + cuModuleGetFunction + the
+ * per-call cuModuleUnload (reference csrc/backend/cuda/utils.cu:6-27,
+ * jit.cu:21-24,42-43). Compiles HIP source for the current device's gfx
+ * target and caches the code object by (source, options, kernel name):
+ * the same request returns the same handle without recompiling.
+ * On ORMI_HIP_ERR_COMPILE, ormi_hip_last_error() holds the compiler log. */
+int ormi_hip_rtc_compile(const char* source, const char* kernel_name,
+                         const char* const* options, int num_options,
+                         uint64_t* handle);
+
+/* Same as ormi_hip_rtc_compile but only produces the code object (no module
+ * load), so it runs without a GPU; target is a gfx name such as "gfx950".
+ * Writes the code object size to *code_bytes. Used to check generated
+ * source on a machine with no GPU. */
+int ormi_hip_rtc_compile_only(const char* source, const char* target,
+                              const char* const* options, int num_options,
+                              size_t* code_bytes);
+
+/* Launch a compiled kernel (reference cuLaunchKernel, jit.cu:40). args is the
+ * kernelParams array: one pointer per kernel parameter. */
+int ormi_hip_launch(uint64_t handle, const uint32_t grid[3], const uint32_t block[3],
+                    uint32_t lds_bytes, void** args);
+
+/* Number of distinct code objects compiled so far (cache misses). */
+int ormi_hip_rtc_cache_size(uint64_t* entries);
+
+/* ------------------------------------------------------------------ GEMM --
+ * Replaces cuda::matmul's cublasSgemmBatched call and its per-call pointer
+ * arrays (reference csrc/backend/cuda/kernels/blas/matmul.cu:19-112,
+ * interface cuda_matmul.cuh:6-12). Row-major semantics of the reference:
+ *   C[b][m][n] = sum_k A[b][m][k] * B[b][k][n]
+ * A[m][k] lives at a + m*a_stride_m + k*a_stride_k (elements); one of the two
+ * strides must be 1 (stride_k == 1: "N", stride_m == 1: "T", the reference's
+ * trans rule matmul.cu:47-52). Same for B with (stride_k, stride_n).
+ * C is written contiguous: C[b][m][n] at c + b*M*N + m*N + n, fp32.
+ * dtype: ORMI_DTYPE_F32 (fp32 MFMA), ORMI_DTYPE_BF16 or ORMI_DTYPE_F16
+ * (MFMA with fp32 accumulation). Batch index b decomposes row-major over
+ * batch_shape[0..batch_ndim); each operand's batch offset is
+ * sum(coord[i] * {a,b}_batch_stride[i]) — a stride of 0 broadcasts. */
+#define ORMI_GEMM_MAX_BATCH_DIMS 4
+typedef struct ormi_gemm_desc {
+    int         dtype;
+    int         M, N, K;
+    const void* a;
+    int64_t     a_stride_m, a_stride_k;
+    const void* b;
+    int64_t     b_stride_k, b_stride_n;
+    float*      c;
+    int         batch_ndim;
+    int         batch_shape[ORMI_GEMM_MAX_BATCH_DIMS];
+    int64_t     a_batch_stride[ORMI_GEMM_MAX_BATCH_DIMS];
+    int64_t     b_batch_stride[ORMI_GEMM_MAX_BATCH_DIMS];
+} ormi_gemm_desc;
+int ormi_hip_gemm(const ormi_gemm_desc* desc);
+
+/* ---------------------------------------------------------------- timing --
+ * HIP events on the library's stream, for measuring kernel time from
+ * outside (benchmarks). */
+int ormi_hip_event_create(void** event);
+int ormi_hip_event_record(void* event);
+int ormi_hip_event_elapsed_ms(void* start, void* end, float* ms);
+int ormi_hip_event_destroy(void* event);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ORMI_HIP_H */

@@ -1,0 +1,758 @@
+// hipRTC code generator for gfx950: fused element-wise maps, and row / column
+// reductions with a fused element-wise prologue.
+//
+// Replaces the reference's NVRTC source builder (csrc/backend/cuda/compiler.cu:53-112)
+// and its atomic sum kernel (csrc/backend/cuda/kernels/reduce/sum.cu:29-66). Unlike
+// those, sizes and strides are kernel arguments (never literals), so a kernel is
+// reused for every tensor with the same structure; the source only encodes the
+// tape, operand dtypes, which strides are 0 or 1, the vector width and the
+// index width.
+//
+// Index space. The kernel's logical shape is canonicalized first: size-1 dims are
+// dropped and neighbouring dims merged wherever every operand (and the output)
+// is linear across them. A reduction splits its dims into three groups, kept
+// dims before the last reduced one (O), reduced dims (R) and kept dims after it
+// (I), so out[o][i] = reduce_r f(o, r, i) with a contiguous output.
+//   * map:     each thread handles UNROLL groups of VEC (4) consecutive
+//              elements: 128-bit loads and stores, grid-stride over tiles
+//              sized for the chip's compute units.
+//   * row:     I empty. One wave64 per (row, part): lanes stride the row with
+//              128-bit loads, then a DPP/cross-lane wave reduction.
+//   * column:  I non-empty. 64 lanes along I (128-bit loads), 4 waves split R;
+//              the 4 partials are combined through LDS.
+// When O (or O x I) is too small to fill 256 CUs, R is split into parts whose
+// partial results go to a workspace, and a second kernel combines them in part
+// order (two-pass; deterministic, no atomics).
+#include <algorithm>
+#include <sstream>
+
+#include "backend/hip/hip_backend.h"
+
+namespace ormi::hip {
+    using ops::OpEnum;
+
+    static const char* kDeviceHeader =
+#include "ormi_device_text.inc"
+        ;
+
+    const std::vector<std::string>& rtc_options() {
+        static const std::vector<std::string> opts = {"-O3", "-std=c++17", "-ffp-contract=off",
+                                                      "-fhip-fp32-correctly-rounded-divide-sqrt"};
+        return opts;
+    }
+
+    FastDiv make_fastdiv(uint32_t d) {
+        if (d == 0) throw std::runtime_error("fastdiv by zero");
+        if (d > (1u << 31)) throw std::runtime_error("fastdiv divisor above 2^31");
+        uint32_t s = 0;
+        while ((1ull << s) < d) ++s;
+        const uint64_t m = ((1ull << 32) * ((1ull << s) - d)) / d + 1;
+        return FastDiv{d, (uint32_t)m, s};
+    }
+
+    namespace {
+        constexpr int kBlock = 256;
+        constexpr int kUnroll = 4;
+
+        const char* storage_type(DType t) {
+            switch (t) {
+                case DType::Float32: return "float";
+                case DType::BFloat16: case DType::Float16: return "unsigned short";
+                case DType::Int64: return "long long";
+                case DType::Int32: return "int";
+                case DType::Bool: return "unsigned char";
+            }
+            return "float";
+        }
+
+        size_t esize(DType t) { return dtype_size(t); }
+
+        bool vector_dtype(DType t) { return t == DType::Float32 || t == DType::BFloat16 || t == DType::Float16; }
+
+        std::string to_f32(DType t, const std::string& v) {
+            switch (t) {
+                case DType::Float32: return v;
+                case DType::BFloat16: return "ormi_bf16_to_f32(" + v + ")";
+                case DType::Float16: return "ormi_f16_to_f32(" + v + ")";
+                case DType::Bool: return "((" + v + ") ? 1.0f : 0.0f)";
+                default: return "((float)(" + v + "))";
+            }
+        }
+
+        std::string from_f32(DType t, const std::string& v) {
+            switch (t) {
+                case DType::Float32: return v;
+                case DType::BFloat16: return "ormi_f32_to_bf16(" + v + ")";
+                case DType::Float16: return "ormi_f32_to_f16(" + v + ")";
+                case DType::Int64: return "ormi_f32_to_i64(" + v + ")";
+                case DType::Int32: return "((int)ormi_f32_to_i64(" + v + "))";
+                case DType::Bool: return "((unsigned char)((" + v + ") != 0.0f))";
+            }
+            return v;
+        }
+
+        // Canonical index space: dims in kernel order with their group tag.
+        enum Group { G_O = 0, G_R = 1, G_I = 2, G_M = 3 };
+        struct Dim {
+            long long size;
+            Group group;
+        };
+        struct Canon {
+            std::vector<Dim> dims;
+            std::vector<std::vector<long long>> st;  // [leaf][dim]
+        };
+
+        // Drop size-1 dims, then merge dim d into d+1 when both are in the same
+        // group and every operand is linear across them. Output contiguity is
+        // preserved because groups keep the output's dim order.
+        void canonicalize(Canon& c, const std::vector<bool>& scalar) {
+            Canon out;
+            out.st.resize(c.st.size());
+            for (size_t d = 0; d < c.dims.size(); ++d) {
+                if (c.dims[d].size == 1) continue;
+                out.dims.push_back(c.dims[d]);
+                for (size_t L = 0; L < c.st.size(); ++L) out.st[L].push_back(c.st[L][d]);
+            }
+            bool merged = true;
+            while (merged) {
+                merged = false;
+                for (size_t d = 0; d + 1 < out.dims.size(); ++d) {
+                    if (out.dims[d].group != out.dims[d + 1].group) continue;
+                    bool ok = true;
+                    for (size_t L = 0; L < out.st.size() && ok; ++L)
+                        if (!scalar[L]) ok = out.st[L][d] == out.st[L][d + 1] * out.dims[d + 1].size;
+                    if (!ok) continue;
+                    out.dims[d].size *= out.dims[d + 1].size;
+                    out.dims.erase(out.dims.begin() + d + 1);
+                    for (auto& s : out.st) {
+                        s[d] = s[d + 1];
+                        s.erase(s.begin() + d + 1);
+                    }
+                    merged = true;
+                    break;
+                }
+            }
+            c = std::move(out);
+        }
+
+        struct ArgList {
+            std::vector<std::string> decls;
+            std::vector<uint64_t> vals;
+            void ptr(const std::string& decl, const void* p) {
+                decls.push_back(decl);
+                vals.push_back((uint64_t)(uintptr_t)p);
+            }
+            void i64(const std::string& name, long long v) {
+                decls.push_back("const long long " + name);
+                vals.push_back((uint64_t)v);
+            }
+        };
+
+        std::string hex_hash(const std::string& s) {
+            uint64_t h = 1469598103934665603ull;
+            for (unsigned char ch : s) {
+                h ^= ch;
+                h *= 1099511628211ull;
+            }
+            std::ostringstream o;
+            o << std::hex << h;
+            return o.str();
+        }
+
+        // Shared pieces of every generated kernel.
+        struct Gen {
+            const Expr& e;
+            Canon c;
+            std::vector<bool> scalar;
+            bool idx32 = true;
+            int vec = 1;
+            int vec_dim = -1;  // dim whose coordinate advances by VEC
+            ArgList args;
+            std::ostringstream body;
+
+            explicit Gen(const Expr& ex) : e(ex) {
+                for (const auto& L : e.leaves) scalar.push_back(L.scalar);
+            }
+
+            std::string idx() const { return idx32 ? "int" : "long long"; }
+
+            // Leaf L has a unit stride on the vector dim and can be read 4-wide.
+            bool leaf_vec_ok(size_t L, int d) const {
+                if (scalar[L]) return true;
+                const long long s = c.st[L][d];
+                if (s == 0) return true;
+                if (s != 1 || !vector_dtype(e.leaves[L].dtype)) return false;
+                for (size_t k = 0; k < c.dims.size(); ++k)
+                    if ((int)k != d && c.st[L][k] % 4 != 0) return false;
+                return ((uintptr_t)e.leaves[L].ptr % (4 * esize(e.leaves[L].dtype))) == 0;
+            }
+
+            void choose_vec(int d) {
+                vec = 1;
+                vec_dim = d;
+                if (d < 0 || c.dims[d].size % 4 != 0) return;
+                for (size_t L = 0; L < e.leaves.size(); ++L)
+                    if (!leaf_vec_ok(L, d)) return;
+                vec = 4;
+            }
+
+            void choose_idx(long long extra_extent) {
+                const long long lim = (1ll << 31) - 1;
+                long long numel = 1;
+                for (auto& d : c.dims) numel *= d.size;
+                idx32 = numel < lim && extra_extent < lim;
+                for (size_t L = 0; L < e.leaves.size() && idx32; ++L) {
+                    if (scalar[L]) continue;
+                    long long span = 0;
+                    for (size_t d = 0; d < c.dims.size(); ++d) span += (c.dims[d].size - 1) * std::llabs(c.st[L][d]);
+                    if (span >= lim) idx32 = false;
+                }
+            }
+
+            void declare_leaves() {
+                for (size_t L = 0; L < e.leaves.size(); ++L)
+                    args.ptr(std::string("const ") + storage_type(e.leaves[L].dtype) + "* __restrict__ L" + std::to_string(L),
+                             e.leaves[L].ptr);
+            }
+
+            // Size (in VEC groups for the vector dim) and fastdiv magic of each dim.
+            void declare_dims() {
+                for (size_t d = 0; d < c.dims.size(); ++d) {
+                    const long long n = (int)d == vec_dim ? c.dims[d].size / vec : c.dims[d].size;
+                    args.i64("D" + std::to_string(d), n);
+                    if (idx32) {
+                        const FastDiv f = make_fastdiv((uint32_t)n);
+                        args.i64("M" + std::to_string(d), (long long)((uint64_t)f.m | ((uint64_t)f.s << 32)));
+                    }
+                }
+            }
+
+            // Runtime strides for the dims where they are neither 0 nor 1.
+            void declare_strides() {
+                for (size_t L = 0; L < e.leaves.size(); ++L) {
+                    if (scalar[L]) continue;
+                    for (size_t d = 0; d < c.dims.size(); ++d) {
+                        const long long s = c.st[L][d];
+                        if (s != 0 && s != 1) args.i64("S" + std::to_string(L) + "_" + std::to_string(d), s);
+                    }
+                }
+            }
+
+            std::string stride_term(size_t L, size_t d) const {
+                const long long s = c.st[L][d];
+                const std::string cd = "c" + std::to_string(d);
+                if (s == 0) return "";
+                if (s == 1) return cd;
+                return cd + " * (" + idx() + ")S" + std::to_string(L) + "_" + std::to_string(d);
+            }
+
+            // Emit coordinates c<d> for `dims` (row-major) from index `var`.
+            void decompose(std::ostringstream& o, const std::string& ind, const std::string& var, const std::vector<int>& dims) {
+                if (dims.empty()) return;
+                const std::string t = idx();
+                o << ind << "{ " << t << " rem_ = " << var << ";\n";
+                for (size_t k = dims.size() - 1; k >= 1; --k) {
+                    const std::string d = std::to_string(dims[k]);
+                    if (idx32)
+                        o << ind << "  const int q_ = (int)ormi_fdiv((unsigned)rem_, (unsigned)M" << d << ", (unsigned)(M" << d
+                          << " >> 32));\n";
+                    else
+                        o << ind << "  const long long q_ = rem_ / D" << d << ";\n";
+                    o << ind << "  c" << d << " = rem_ - q_ * (" << t << ")D" << d << "; rem_ = q_;\n";
+                }
+                o << ind << "  c" << dims[0] << " = rem_; }\n";
+                for (int d : dims)
+                    if (d == vec_dim && vec > 1) o << ind << "c" << d << " *= " << vec << ";\n";
+            }
+
+            void declare_coords(std::ostringstream& o, const std::string& ind, const std::vector<int>& dims) {
+                for (int d : dims) o << ind << idx() << " c" << d << " = 0;\n";
+            }
+
+            // "off" expression of leaf L over `dims`, empty when all terms vanish.
+            std::string offset(size_t L, const std::vector<int>& dims) const {
+                std::string s;
+                for (int d : dims) {
+                    std::string t = stride_term(L, d);
+                    if (t.empty()) continue;
+                    s += s.empty() ? t : " + " + t;
+                }
+                return s;
+            }
+
+            // Load leaf L at element offset `off` into x<L><sfx>[0..vec).
+            void load_leaf(std::ostringstream& o, const std::string& ind, size_t L, const std::string& off, const std::string& dst) {
+                const DType dt = e.leaves[L].dtype;
+                const std::string p = "L" + std::to_string(L);
+                if (scalar[L]) return;  // hoisted
+                const bool unit = vec > 1 && c.st[L][vec_dim] == 1;
+                if (unit) {
+                    if (dt == DType::Float32) {
+                        o << ind << "{ const ormi_f4 v_ = *(const ormi_f4*)(" << p << " + (" << off << "));";
+                        for (int k = 0; k < vec; ++k) o << " " << dst << "[" << k << "] = v_[" << k << "];";
+                        o << " }\n";
+                    } else {
+                        o << ind << "{ const ormi_u16x4 v_ = *(const ormi_u16x4*)(" << p << " + (" << off << "));";
+                        for (int k = 0; k < vec; ++k) o << " " << dst << "[" << k << "] = " << to_f32(dt, "v_[" + std::to_string(k) + "]") << ";";
+                        o << " }\n";
+                    }
+                } else {
+                    o << ind << "{ const float v_ = " << to_f32(dt, p + "[" + off + "]") << ";";
+                    for (int k = 0; k < vec; ++k) o << " " << dst << "[" << k << "] = v_;";
+                    o << " }\n";
+                }
+            }
+
+            void hoist_scalars(std::ostringstream& o, const std::string& ind) {
+                for (size_t L = 0; L < e.leaves.size(); ++L)
+                    if (scalar[L])
+                        o << ind << "const float s" << L << " = " << to_f32(e.leaves[L].dtype, "L" + std::to_string(L) + "[0]") << ";\n";
+            }
+
+            // SSA evaluation for vector element k: leaf values come from
+            // x<L>[u][k] (or the hoisted scalar). Returns the root value name.
+            std::string eval(std::ostringstream& o, const std::string& ind, const std::string& u, const std::string& k) {
+                std::vector<std::string> name(e.leaves.size() + e.insts.size());
+                for (size_t L = 0; L < e.leaves.size(); ++L)
+                    name[L] = scalar[L] ? "s" + std::to_string(L) : "x" + std::to_string(L) + "[" + u + "][" + k + "]";
+                for (size_t i = 0; i < e.insts.size(); ++i) {
+                    const Inst& in = e.insts[i];
+                    const size_t id = e.leaves.size() + i;
+                    std::string expr;
+                    if (in.op == OpEnum::CAST) {
+                        if (in.cast == DType::BFloat16) expr = "ormi_round_bf16(" + name[in.a] + ")";
+                        else if (in.cast == DType::Float16) expr = "ormi_round_f16(" + name[in.a] + ")";
+                        else expr = name[in.a];
+                    } else {
+                        std::vector<std::string> operands{name[in.a]};
+                        if (in.b >= 0) operands.push_back(name[in.b]);
+                        expr = HIPLoweringRegistry::get(in.op)(operands);
+                    }
+                    name[id] = "t" + std::to_string(i);
+                    o << ind << "const float " << name[id] << " = " << expr << ";\n";
+                }
+                return name[e.root];
+            }
+
+            void declare_leaf_regs(std::ostringstream& o, const std::string& ind, int unroll) {
+                for (size_t L = 0; L < e.leaves.size(); ++L)
+                    if (!scalar[L]) o << ind << "float x" << L << "[" << unroll << "][" << vec << "];\n";
+            }
+
+            std::string finish(const std::string& kind, const std::string& kernel_body, KernelLaunch& k) {
+                std::ostringstream sig;
+                for (size_t i = 0; i < args.decls.size(); ++i) sig << (i ? ",\n    " : "    ") << args.decls[i];
+                const std::string tag = hex_hash(kernel_body + sig.str());
+                k.name = "ormi_" + kind + "_" + tag;
+                std::ostringstream src;
+                src << kDeviceHeader << "\n\nextern \"C\" __global__ __launch_bounds__(" << kBlock << ") void " << k.name << "(\n"
+                    << sig.str() << ") {\n" << kernel_body << "}\n";
+                k.args = args.vals;
+                return src.str();
+            }
+        };
+
+        std::vector<int> dims_of(const Canon& c, Group g) {
+            std::vector<int> v;
+            for (size_t d = 0; d < c.dims.size(); ++d)
+                if (c.dims[d].group == g) v.push_back((int)d);
+            return v;
+        }
+
+        long long group_size(const Canon& c, Group g) {
+            long long n = 1;
+            for (auto& d : c.dims)
+                if (d.group == g) n *= d.size;
+            return n;
+        }
+
+        std::string reduce_name(ReduceOp op) {
+            return op == ReduceOp::Sum ? "sum" : op == ReduceOp::Max ? "max" : "argmax";
+        }
+    }  // namespace
+
+    // ------------------------------------------------------------------ map --
+    KernelLaunch plan_map(const Expr& expr, const std::vector<int>& shape, void* out, DType out_dtype, int cu) {
+        Gen g(expr);
+        for (int s : shape) g.c.dims.push_back({(long long)s, G_M});
+        for (const auto& L : expr.leaves) g.c.st.push_back(L.st);
+        canonicalize(g.c, g.scalar);
+        if (g.c.dims.empty()) {
+            g.c.dims.push_back({1, G_M});
+            for (auto& s : g.c.st) s.push_back(0);
+        }
+        const int n = (int)g.c.dims.size();
+        g.choose_vec(n - 1);
+        if (!vector_dtype(out_dtype) || ((uintptr_t)out % 16) != 0) g.vec = 1;
+        long long numel = 1;
+        for (auto& d : g.c.dims) numel *= d.size;
+        const long long G = numel / g.vec;
+        const long long tiles = (G + kBlock * kUnroll - 1) / (kBlock * kUnroll);
+        const long long cap = (long long)std::max(cu, 1) * 16;
+        const long long grid = std::max(1LL, std::min(tiles, cap));
+        // The grid-stride cursor reaches G + grid * tile before the loop exits.
+        g.choose_idx(G + grid * kBlock * kUnroll);
+
+        KernelLaunch k;
+        g.args.ptr(std::string(storage_type(out_dtype)) + "* __restrict__ out", out);
+        g.declare_leaves();
+        g.args.i64("G", G);
+        g.declare_dims();
+        g.declare_strides();
+
+        std::vector<int> all;
+        for (int d = 0; d < n; ++d) all.push_back(d);
+        const std::string t = g.idx();
+        const int V = g.vec;
+        std::ostringstream& b = g.body;
+        g.hoist_scalars(b, "  ");
+        b << "  const " << t << " tile = " << kBlock * kUnroll << ";\n";
+        b << "  for (" << t << " base = (" << t << ")blockIdx.x * tile; base < (" << t << ")G; base += (" << t << ")gridDim.x * tile) {\n";
+        g.declare_leaf_regs(b, "    ", kUnroll);
+        b << "    " << t << " gi[" << kUnroll << "];\n";
+        b << "#pragma unroll\n    for (int u = 0; u < " << kUnroll << "; ++u) {\n";
+        b << "      const " << t << " gg = base + u * " << kBlock << " + (" << t << ")threadIdx.x;\n";
+        b << "      gi[u] = gg;\n";
+        b << "      const " << t << " gc = gg < (" << t << ")G ? gg : (" << t << ")G - 1;\n";
+        g.declare_coords(b, "      ", all);
+        g.decompose(b, "      ", "gc", all);
+        for (size_t L = 0; L < expr.leaves.size(); ++L) {
+            if (g.scalar[L]) continue;
+            std::string off = g.offset(L, all);
+            if (off.empty()) off = "0";
+            g.load_leaf(b, "      ", L, off, "x" + std::to_string(L) + "[u]");
+        }
+        b << "    }\n";
+        b << "#pragma unroll\n    for (int u = 0; u < " << kUnroll << "; ++u) {\n";
+        b << "      float res[" << V << "];\n";
+        b << "#pragma unroll\n      for (int k = 0; k < " << V << "; ++k) {\n";
+        const std::string root = g.eval(b, "        ", "u", "k");
+        b << "        res[k] = " << root << ";\n      }\n";
+        b << "      if (gi[u] < (" << t << ")G) {\n";
+        if (V == 4 && out_dtype == DType::Float32) {
+            b << "        *(ormi_f4*)(out + gi[u] * 4) = ormi_f4{res[0], res[1], res[2], res[3]};\n";
+        } else if (V == 4) {
+            b << "        *(ormi_u16x4*)(out + gi[u] * 4) = ormi_u16x4{" << from_f32(out_dtype, "res[0]") << ", "
+              << from_f32(out_dtype, "res[1]") << ", " << from_f32(out_dtype, "res[2]") << ", " << from_f32(out_dtype, "res[3]") << "};\n";
+        } else {
+            b << "        out[gi[u]] = " << from_f32(out_dtype, "res[0]") << ";\n";
+        }
+        b << "      }\n    }\n  }\n";
+
+        k.source = g.finish("map", b.str(), k);
+        k.grid[0] = (uint32_t)grid;
+        std::ostringstream plan;
+        plan << "map ndim=" << n << " vec=" << V << " idx=" << (g.idx32 ? 32 : 64) << " groups=" << G;
+        k.plan = plan.str();
+        return k;
+    }
+
+    // ------------------------------------------------------------- reduce --
+    ReducePlan plan_reduce(const Expr& expr, const std::vector<int>& in_shape, const std::vector<int>& axes_in, ReduceOp op,
+                           void* out, int cu) {
+        const int n = (int)in_shape.size();
+        std::vector<bool> red(n, axes_in.empty());
+        for (int a : axes_in) red[a] = true;
+        int last_red = -1;
+        for (int d = 0; d < n; ++d)
+            if (red[d]) last_red = d;
+
+        Gen g(expr);
+        // Kernel dim order: O dims, R dims, I dims (each in logical order).
+        std::vector<int> perm;
+        for (int d = 0; d < n; ++d) if (!red[d] && d < last_red) perm.push_back(d);
+        for (int d = 0; d < n; ++d) if (red[d]) perm.push_back(d);
+        for (int d = 0; d < n; ++d) if (!red[d] && d > last_red) perm.push_back(d);
+        for (int d : perm) g.c.dims.push_back({(long long)in_shape[d], red[d] ? G_R : (d < last_red ? G_O : G_I)});
+        for (const auto& L : expr.leaves) {
+            std::vector<long long> s;
+            for (int d : perm) s.push_back(L.st[d]);
+            g.c.st.push_back(s);
+        }
+        canonicalize(g.c, g.scalar);
+
+        const long long O = group_size(g.c, G_O), R = group_size(g.c, G_R), I = group_size(g.c, G_I);
+        if (R >= (1ll << 31)) throw std::runtime_error("HIP reduce: reduced extent above 2^31 elements.");
+        const std::vector<int> od = dims_of(g.c, G_O), rd = dims_of(g.c, G_R), id = dims_of(g.c, G_I);
+        const bool column = !id.empty();
+        g.choose_vec(column ? id.back() : (rd.empty() ? -1 : rd.back()));
+
+        ReducePlan plan;
+        KernelLaunch& k = plan.first;
+        const std::string name = reduce_name(op);
+        const bool is_sum = op == ReduceOp::Sum;
+        const int V = g.vec;
+        std::ostringstream& b = g.body;
+        std::ostringstream summary;
+
+        if (!column) {
+            // ---------------------------------------------------------- row --
+            const long long RG = R / V;
+            long long P = 1;
+            const long long target_waves = (long long)std::max(cu, 1) * 32;
+            if (O < target_waves / 2) P = std::max(1LL, std::min((target_waves + O - 1) / O, (RG + 255) / 256));
+            const long long CH = (RG + P - 1) / P;
+            P = (RG + CH - 1) / CH;  // drop empty parts
+            if (RG == 0) P = 1;
+            g.choose_idx(O * P * 64);
+            plan.two_pass = P > 1;
+            const std::string t = g.idx();
+
+            void* dst_v = plan.two_pass ? nullptr : out;  // bound later for two-pass
+            g.args.ptr("void* __restrict__ outp", dst_v);
+            g.args.ptr("int* __restrict__ outi", nullptr);
+            g.declare_leaves();
+            g.args.i64("NO", O);
+            g.args.i64("NP", P);
+            g.args.i64("RG", RG);
+            g.args.i64("CH", CH);
+            g.declare_dims();
+            g.declare_strides();
+
+            g.hoist_scalars(b, "  ");
+            b << "  const int lane = threadIdx.x & 63;\n";
+            b << "  const " << t << " wid = (" << t << ")blockIdx.x * 4 + (" << t << ")(threadIdx.x >> 6);\n";
+            b << "  if (wid >= (" << t << ")NO * (" << t << ")NP) return;\n";
+            b << "  const " << t << " o = wid / (" << t << ")NP, p = wid - o * (" << t << ")NP;\n";
+            g.declare_coords(b, "  ", od);
+            g.decompose(b, "  ", "o", od);
+            for (size_t L = 0; L < expr.leaves.size(); ++L) {
+                if (g.scalar[L]) continue;
+                std::string off = g.offset(L, od);
+                b << "  const " << t << " base" << L << " = " << (off.empty() ? "0" : off) << ";\n";
+            }
+            b << "  const " << t << " rg0 = p * (" << t << ")CH;\n";
+            b << "  const " << t << " rg1 = rg0 + (" << t << ")CH < (" << t << ")RG ? rg0 + (" << t << ")CH : (" << t << ")RG;\n";
+            if (is_sum) b << "  float acc[" << V << "] = {" << std::string(V > 1 ? "0.0f, 0.0f, 0.0f, 0.0f" : "0.0f") << "};\n";
+            else b << "  float bv = -__builtin_inff(); int bi = 0x7fffffff;\n";
+            // Body for UNR groups starting at rg, stepping 64.
+            auto emit_step = [&](int UNR, const std::string& ind) {
+                g.declare_leaf_regs(b, ind, UNR);
+                b << ind << "#pragma unroll\n" << ind << "for (int u = 0; u < " << UNR << "; ++u) {\n";
+                b << ind << "  const " << t << " rgu = rg + u * 64;\n";
+                g.declare_coords(b, ind + "  ", rd);
+                g.decompose(b, ind + "  ", "rgu", rd);
+                for (size_t L = 0; L < expr.leaves.size(); ++L) {
+                    if (g.scalar[L]) continue;
+                    std::string off = g.offset(L, rd);
+                    g.load_leaf(b, ind + "  ", L, "base" + std::to_string(L) + (off.empty() ? "" : " + " + off),
+                                "x" + std::to_string(L) + "[u]");
+                }
+                b << ind << "}\n";
+                b << ind << "#pragma unroll\n" << ind << "for (int u = 0; u < " << UNR << "; ++u) {\n";
+                b << ind << "#pragma unroll\n" << ind << "  for (int k = 0; k < " << V << "; ++k) {\n";
+                const std::string v = g.eval(b, ind + "    ", "u", "k");
+                if (is_sum) b << ind << "    acc[k] += " << v << ";\n";
+                else b << ind << "    ormi_am_take(bv, bi, " << v << ", (int)((rg + u * 64) * " << V << " + k));\n";
+                b << ind << "  }\n" << ind << "}\n";
+            };
+            b << "  " << t << " rg = rg0 + lane;\n";
+            b << "  for (; rg + " << 64 * (kUnroll - 1) << " < rg1; rg += " << 64 * kUnroll << ") {\n";
+            emit_step(kUnroll, "    ");
+            b << "  }\n";
+            b << "  for (; rg < rg1; rg += 64) {\n";
+            emit_step(1, "    ");
+            b << "  }\n";
+            if (is_sum) {
+                b << "  float s = " << (V > 1 ? "(acc[0] + acc[1]) + (acc[2] + acc[3])" : "acc[0]") << ";\n";
+                b << "  s = ormi_wave_sum(s);\n";
+                b << "  if (lane == 0) ((float*)outp)[wid] = s;\n";
+            } else {
+                b << "  ormi_wave_argmax(bv, bi);\n";
+                b << "  if (lane == 0) {\n";
+                if (op == ReduceOp::Argmax) b << "    if (NP == 1) ((long long*)outp)[wid] = (long long)bi; else { ((float*)outp)[wid] = bv; outi[wid] = bi; }\n";
+                else b << "    ((float*)outp)[wid] = bv; if (NP > 1) outi[wid] = bi;\n";
+                b << "  }\n";
+            }
+            k.source = g.finish("row" + name, b.str(), k);
+            const long long waves = O * P;
+            k.grid[0] = (uint32_t)std::max(1LL, (waves + 3) / 4);
+            summary << "row " << name << " O=" << O << " R=" << R << " vec=" << V << " parts=" << P << " idx=" << (g.idx32 ? 32 : 64);
+            k.plan = summary.str();
+            if (plan.two_pass) {
+                plan.workspace_bytes = (size_t)(O * P) * (sizeof(float) + sizeof(int));
+                // Second pass: one wave per output row over its P partials, in part order.
+                KernelLaunch& s2 = plan.second;
+                std::ostringstream sb;
+                sb << "  const int lane = threadIdx.x & 63;\n";
+                sb << "  const long long o = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);\n";
+                sb << "  if (o >= NO) return;\n";
+                sb << "  const float* pv = pvals + o * NP; const int* pi = pidx + o * NP;\n";
+                if (is_sum) {
+                    sb << "  float s = 0.0f;\n  for (long long q = lane; q < NP; q += 64) s += pv[q];\n";
+                    sb << "  s = ormi_wave_sum(s);\n  if (lane == 0) ((float*)outp)[o] = s;\n";
+                } else {
+                    sb << "  float bv = -__builtin_inff(); int bi = 0x7fffffff;\n";
+                    sb << "  for (long long q = lane; q < NP; q += 64) ormi_am_take(bv, bi, pv[q], pi[q]);\n";
+                    sb << "  ormi_wave_argmax(bv, bi);\n";
+                    if (op == ReduceOp::Argmax) sb << "  if (lane == 0) ((long long*)outp)[o] = (long long)bi;\n";
+                    else sb << "  if (lane == 0) ((float*)outp)[o] = bv;\n";
+                }
+                Gen g2(expr);
+                g2.args.ptr("void* __restrict__ outp", out);
+                g2.args.ptr("const float* __restrict__ pvals", nullptr);
+                g2.args.ptr("const int* __restrict__ pidx", nullptr);
+                g2.args.i64("NO", O);
+                g2.args.i64("NP", P);
+                s2.source = g2.finish("rowfin" + name, sb.str(), s2);
+                s2.grid[0] = (uint32_t)std::max(1LL, (O + 3) / 4);
+                s2.plan = "row-finish " + name;
+            }
+            return plan;
+        }
+
+        // ------------------------------------------------------------ column --
+        const long long IG = I / V;
+        const long long BI = (IG + 63) / 64;
+        long long P = 1;
+        const long long target_blocks = (long long)std::max(cu, 1) * 8;
+        if (BI * O < target_blocks) P = std::max(1LL, std::min((target_blocks + BI * O - 1) / (BI * O), (R + 63) / 64));
+        const long long CH = (R + P - 1) / P;
+        P = (R + CH - 1) / CH;
+        if (R == 0) P = 1;
+        g.choose_idx(O * I * P);
+        plan.two_pass = P > 1;
+        const std::string t = g.idx();
+
+        g.args.ptr("void* __restrict__ outp", plan.two_pass ? nullptr : out);
+        g.args.ptr("int* __restrict__ outi", nullptr);
+        g.declare_leaves();
+        g.args.i64("NO", O);
+        g.args.i64("NI", I);
+        g.args.i64("NIG", IG);
+        g.args.i64("NBI", BI);
+        g.args.i64("NR", R);
+        g.args.i64("CH", CH);
+        g.declare_dims();
+        g.declare_strides();
+
+        g.hoist_scalars(b, "  ");
+        b << "  __shared__ float sv[4][64][" << V << "];\n";
+        if (!is_sum) b << "  __shared__ int si[4][64][" << V << "];\n";
+        b << "  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;\n";
+        b << "  const " << t << " bid = (" << t << ")blockIdx.x;\n";
+        b << "  const " << t << " bi_ = bid % (" << t << ")NBI; const " << t << " rest = bid / (" << t << ")NBI;\n";
+        b << "  const " << t << " o = rest % (" << t << ")NO, p = rest / (" << t << ")NO;\n";
+        b << "  const " << t << " ig = bi_ * 64 + lane;\n";
+        b << "  const bool active = ig < (" << t << ")NIG;\n";
+        b << "  const " << t << " igc = active ? ig : (" << t << ")NIG - 1;\n";
+        std::vector<int> oi = od;
+        oi.insert(oi.end(), id.begin(), id.end());
+        g.declare_coords(b, "  ", oi);
+        g.decompose(b, "  ", "o", od);
+        g.decompose(b, "  ", "igc", id);
+        for (size_t L = 0; L < expr.leaves.size(); ++L) {
+            if (g.scalar[L]) continue;
+            std::string off = g.offset(L, oi);
+            b << "  const " << t << " base" << L << " = " << (off.empty() ? "0" : off) << ";\n";
+        }
+        b << "  const " << t << " r0 = p * (" << t << ")CH;\n";
+        b << "  const " << t << " r1 = r0 + (" << t << ")CH < (" << t << ")NR ? r0 + (" << t << ")CH : (" << t << ")NR;\n";
+        if (is_sum) b << "  float acc[" << V << "];\n#pragma unroll\n  for (int k = 0; k < " << V << "; ++k) acc[k] = 0.0f;\n";
+        else b << "  float bv[" << V << "]; int bx[" << V << "];\n#pragma unroll\n  for (int k = 0; k < " << V
+               << "; ++k) { bv[k] = -__builtin_inff(); bx[k] = 0x7fffffff; }\n";
+        auto emit_cstep = [&](int UNR, const std::string& ind) {
+            g.declare_leaf_regs(b, ind, UNR);
+            b << ind << "#pragma unroll\n" << ind << "for (int u = 0; u < " << UNR << "; ++u) {\n";
+            b << ind << "  const " << t << " ru = r + u * 4;\n";
+            g.declare_coords(b, ind + "  ", rd);
+            g.decompose(b, ind + "  ", "ru", rd);
+            for (size_t L = 0; L < expr.leaves.size(); ++L) {
+                if (g.scalar[L]) continue;
+                std::string off = g.offset(L, rd);
+                g.load_leaf(b, ind + "  ", L, "base" + std::to_string(L) + (off.empty() ? "" : " + " + off), "x" + std::to_string(L) + "[u]");
+            }
+            b << ind << "}\n";
+            b << ind << "#pragma unroll\n" << ind << "for (int u = 0; u < " << UNR << "; ++u) {\n";
+            b << ind << "#pragma unroll\n" << ind << "  for (int k = 0; k < " << V << "; ++k) {\n";
+            const std::string v = g.eval(b, ind + "    ", "u", "k");
+            if (is_sum) b << ind << "    acc[k] += " << v << ";\n";
+            else b << ind << "    ormi_am_take(bv[k], bx[k], " << v << ", (int)(r + u * 4));\n";
+            b << ind << "  }\n" << ind << "}\n";
+        };
+        b << "  " << t << " r = r0 + w;\n";
+        b << "  if (active) {\n";
+        b << "    for (; r + " << 4 * (kUnroll - 1) << " < r1; r += " << 4 * kUnroll << ") {\n";
+        emit_cstep(kUnroll, "      ");
+        b << "    }\n";
+        b << "    for (; r < r1; r += 4) {\n";
+        emit_cstep(1, "      ");
+        b << "    }\n  }\n";
+        b << "#pragma unroll\n  for (int k = 0; k < " << V << "; ++k) {";
+        if (is_sum) b << " sv[w][lane][k] = acc[k]; }\n";
+        else b << " sv[w][lane][k] = bv[k]; si[w][lane][k] = bx[k]; }\n";
+        b << "  __syncthreads();\n";
+        b << "  if (w == 0 && active) {\n";
+        b << "    const " << t << " e0 = (p * (" << t << ")NO + o) * (" << t << ")NI + ig * " << V << ";\n";
+        b << "#pragma unroll\n    for (int k = 0; k < " << V << "; ++k) {\n";
+        if (is_sum) {
+            b << "      const float s = ((sv[0][lane][k] + sv[1][lane][k]) + sv[2][lane][k]) + sv[3][lane][k];\n";
+            b << "      ((float*)outp)[e0 + k] = s;\n";
+        } else {
+            b << "      float v = sv[0][lane][k]; int x = si[0][lane][k];\n";
+            b << "      ormi_am_take(v, x, sv[1][lane][k], si[1][lane][k]);\n";
+            b << "      ormi_am_take(v, x, sv[2][lane][k], si[2][lane][k]);\n";
+            b << "      ormi_am_take(v, x, sv[3][lane][k], si[3][lane][k]);\n";
+            if (op == ReduceOp::Argmax) b << "      if (outi == nullptr) ((long long*)outp)[e0 + k] = (long long)x; else { ((float*)outp)[e0 + k] = v; outi[e0 + k] = x; }\n";
+            else b << "      ((float*)outp)[e0 + k] = v; if (outi != nullptr) outi[e0 + k] = x;\n";
+        }
+        b << "    }\n  }\n";
+        k.source = g.finish("col" + name, b.str(), k);
+        k.grid[0] = (uint32_t)std::max(1LL, BI * O * P);
+        summary << "column " << name << " O=" << O << " R=" << R << " I=" << I << " vec=" << V << " parts=" << P << " idx=" << (g.idx32 ? 32 : 64);
+        k.plan = summary.str();
+        if (plan.two_pass) {
+            // Partials are laid out [P][O*I]; the second pass walks them in part order.
+            plan.workspace_bytes = (size_t)(P * O * I) * (sizeof(float) + sizeof(int));
+            KernelLaunch& s2 = plan.second;
+            std::ostringstream sb;
+            sb << "  const long long e = (long long)blockIdx.x * 256 + threadIdx.x;\n";
+            sb << "  if (e >= NE) return;\n";
+            if (is_sum) {
+                sb << "  float s = 0.0f;\n  for (long long q = 0; q < NP; ++q) s += pvals[q * NE + e];\n";
+                sb << "  ((float*)outp)[e] = s;\n";
+            } else {
+                sb << "  float bv = -__builtin_inff(); int bi = 0x7fffffff;\n";
+                sb << "  for (long long q = 0; q < NP; ++q) ormi_am_take(bv, bi, pvals[q * NE + e], pidx[q * NE + e]);\n";
+                if (op == ReduceOp::Argmax) sb << "  ((long long*)outp)[e] = (long long)bi;\n";
+                else sb << "  ((float*)outp)[e] = bv;\n";
+            }
+            Gen g2(expr);
+            g2.args.ptr("void* __restrict__ outp", out);
+            g2.args.ptr("const float* __restrict__ pvals", nullptr);
+            g2.args.ptr("const int* __restrict__ pidx", nullptr);
+            g2.args.i64("NE", O * I);
+            g2.args.i64("NP", P);
+            s2.source = g2.finish("colfin" + name, sb.str(), s2);
+            s2.grid[0] = (uint32_t)std::max(1LL, (O * I + 255) / 256);
+            s2.plan = "column-finish " + name;
+        }
+        return plan;
+    }
+
+    // Point the split-reduction kernels at the workspace: values first, then
+    // indices. The first kernel's outp/outi are args 0 and 1; the second
+    // kernel's pvals/pidx are args 1 and 2.
+    void bind_workspace(ReducePlan& plan, void* ws) {
+        if (!plan.two_pass) return;
+        const size_t nvals = plan.workspace_bytes / (sizeof(float) + sizeof(int));
+        char* base = (char*)ws;
+        const uint64_t vals = (uint64_t)(uintptr_t)base;
+        const uint64_t idx = (uint64_t)(uintptr_t)(base + nvals * sizeof(float));
+        plan.first.args[0] = vals;
+        plan.first.args[1] = idx;
+        plan.second.args[1] = vals;
+        plan.second.args[2] = idx;
+    }
+
+    void launch(const KernelLaunch& k) {
+        std::vector<const char*> opts;
+        for (const auto& o : rtc_options()) opts.push_back(o.c_str());
+        uint64_t handle = 0;
+        ORMI_HIP_CHECK(ormi_hip_rtc_compile(k.source.c_str(), k.name.c_str(), opts.data(), (int)opts.size(), &handle));
+        std::vector<uint64_t> vals = k.args;
+        std::vector<void*> ptrs(vals.size());
+        for (size_t i = 0; i < vals.size(); ++i) ptrs[i] = &vals[i];
+        ORMI_HIP_CHECK(ormi_hip_launch(handle, k.grid, k.block, 0, ptrs.data()));
+    }
+}

@@ -1,0 +1,173 @@
+// Pointwise region discovery and the SSA tape the code generator consumes.
+// Follows the reference's tape construction (csrc/backend/cuda/compiler.cu:22-51:
+// dedup by Node*, realized nodes become leaves, MATMUL is never fused) but
+// walks the whole unrealized pointwise region instead of a single op, and
+// aligns each leaf to the kernel's shape the way the reference's CPU JIT
+// does (csrc/backend/cpu/jit.cpp:24-46: right-aligned, size-1 dims and
+// 1-element buffers read with stride 0).
+#include <mutex>
+#include <unordered_map>
+#include <unordered_set>
+
+#include "backend/hip/hip_backend.h"
+#include "runtime/runtime.h"
+
+namespace ormi::hip {
+    using ops::OpEnum;
+
+    static std::unordered_map<OpEnum, LoweringFunc>& lowering_table() {
+        static std::unordered_map<OpEnum, LoweringFunc> t;
+        return t;
+    }
+
+    void HIPLoweringRegistry::register_func(OpEnum op, LoweringFunc f) { lowering_table()[op] = std::move(f); }
+    bool HIPLoweringRegistry::has(OpEnum op) { return lowering_table().count(op) > 0; }
+    LoweringFunc HIPLoweringRegistry::get(OpEnum op) {
+        auto it = lowering_table().find(op);
+        if (it == lowering_table().end())
+            throw std::runtime_error(std::string("HIP JIT Compiler Error: No lowering rule registered for ") + ops::op_name(op));
+        return it->second;
+    }
+
+    namespace {
+        struct RegisterLowering {
+            RegisterLowering(OpEnum op, LoweringFunc f) { HIPLoweringRegistry::register_func(op, std::move(f)); }
+        };
+        using A = const std::vector<std::string>&;
+        RegisterLowering l_add(OpEnum::ADD, [](A v) { return "(" + v[0] + " + " + v[1] + ")"; });
+        RegisterLowering l_sub(OpEnum::SUB, [](A v) { return "(" + v[0] + " - " + v[1] + ")"; });
+        RegisterLowering l_mul(OpEnum::MUL, [](A v) { return "(" + v[0] + " * " + v[1] + ")"; });
+        RegisterLowering l_div(OpEnum::DIV, [](A v) { return "(" + v[0] + " / " + v[1] + ")"; });
+        RegisterLowering l_pow(OpEnum::POW, [](A v) { return "powf(" + v[0] + ", " + v[1] + ")"; });
+        RegisterLowering l_eq(OpEnum::EQ, [](A v) { return "ormi_eq(" + v[0] + ", " + v[1] + ")"; });
+        RegisterLowering l_neg(OpEnum::NEG, [](A v) { return "(-" + v[0] + ")"; });
+        RegisterLowering l_exp(OpEnum::EXP, [](A v) { return "expf(" + v[0] + ")"; });
+        RegisterLowering l_log(OpEnum::LOG, [](A v) { return "logf(" + v[0] + ")"; });
+        RegisterLowering l_sin(OpEnum::SIN, [](A v) { return "sinf(" + v[0] + ")"; });
+        RegisterLowering l_cos(OpEnum::COS, [](A v) { return "cosf(" + v[0] + ")"; });
+        RegisterLowering l_relu(OpEnum::RELU, [](A v) { return "ormi_relu(" + v[0] + ")"; });
+        RegisterLowering l_step(OpEnum::STEP, [](A v) { return "ormi_step(" + v[0] + ")"; });
+        RegisterLowering l_tanh(OpEnum::TANH, [](A v) { return "tanhf(" + v[0] + ")"; });
+        RegisterLowering l_tanhg(OpEnum::TANH_GRAD, [](A v) { return "ormi_tanh_grad(" + v[0] + ")"; });
+        RegisterLowering l_sig(OpEnum::SIGMOID, [](A v) { return "ormi_sigmoid(" + v[0] + ")"; });
+        RegisterLowering l_sigg(OpEnum::SIGMOID_GRAD, [](A v) { return "ormi_sigmoid_grad(" + v[0] + ")"; });
+        RegisterLowering l_gelu(OpEnum::GELU, [](A v) { return "ormi_gelu(" + v[0] + ")"; });
+        RegisterLowering l_gelug(OpEnum::GELU_GRAD, [](A v) { return "ormi_gelu_grad(" + v[0] + ")"; });
+    }
+
+    static bool cast_target_is_float(const Node& n) {
+        const DType t = std::get<CastAttrs>(n.attrs).dtype;
+        return t == DType::Float32 || t == DType::BFloat16 || t == DType::Float16;
+    }
+
+    bool fusible_root(const Node& n) {
+        if (n.is_realized() || !ops::is_pointwise(n.op)) return false;
+        return n.op == OpEnum::CAST || HIPLoweringRegistry::has(n.op);
+    }
+
+    bool fusible_interior(const Node& n) {
+        if (!fusible_root(n)) return false;
+        return n.op != OpEnum::CAST || cast_target_is_float(n);
+    }
+
+    std::vector<NodePtr> region_frontier(const NodePtr& root) {
+        std::vector<NodePtr> frontier;
+        std::unordered_set<Node*> seen{root.get()};
+        std::vector<NodePtr> stack{root};
+        while (!stack.empty()) {
+            NodePtr n = stack.back();
+            stack.pop_back();
+            for (const auto& p : n->parents) {
+                if (!seen.insert(p.get()).second) continue;
+                if (p->is_realized()) continue;
+                if (fusible_interior(*p)) stack.push_back(p);
+                else frontier.push_back(p);
+            }
+        }
+        return frontier;
+    }
+
+    static Leaf make_leaf(const NodePtr& n, const std::vector<int>& shape, bool plan_only) {
+        if (!n->data) throw std::runtime_error("HIP codegen: leaf is not realized.");
+        if (!plan_only && n->device.type != DeviceEnum::HIP) throw std::runtime_error("HIP codegen: operand lives on another device.");
+        Leaf L;
+        L.node = n;
+        L.ptr = n->data->ptr;
+        L.dtype = n->data->dtype;
+        const size_t ndim = shape.size();
+        L.st.assign(ndim, 0);
+        // Scalar rule of the reference (csrc/backend/cpu/jit.cpp:24): a leaf whose
+        // view is 0-d or whose buffer holds one element reads element 0.
+        L.scalar = n->view.shape.empty() || n->data->numel() == 1;
+        if (L.scalar) return L;
+        const auto& ls = n->view.shape;
+        const auto& lst = n->view.strides;
+        if (ls.size() > ndim) throw std::runtime_error("HIP codegen: operand has more dims than the kernel shape.");
+        const size_t off = ndim - ls.size();
+        for (size_t d = off; d < ndim; ++d) {
+            const int od = (int)(d - off);
+            if (ls[od] != 1) {
+                if (ls[od] != shape[d]) throw std::runtime_error("HIP codegen: operand shape does not broadcast to the kernel shape.");
+                L.st[d] = lst[od];
+            }
+        }
+        return L;
+    }
+
+    Expr build_expr(const NodePtr& root, const std::vector<int>& shape, bool plan_only) {
+        Expr e;
+        std::unordered_map<Node*, int> value_of;
+        std::vector<std::pair<NodePtr, int>> order;  // interior nodes in post-order
+        // Post-order DFS over the region: leaves get ids as first seen, interior
+        // nodes after all their operands.
+        struct Frame { NodePtr n; size_t next; };
+        std::vector<Frame> stack;
+        auto is_interior = [&](const NodePtr& n) { return n == root ? fusible_root(*n) : fusible_interior(*n); };
+        auto visit_leaf = [&](const NodePtr& n) {
+            const int id = (int)e.leaves.size();
+            e.leaves.push_back(make_leaf(n, shape, plan_only));
+            value_of[n.get()] = id;
+        };
+        if (!is_interior(root)) {
+            // A realized node (or a reduction input that is already a buffer):
+            // the tape is the identity on one leaf.
+            visit_leaf(root);
+            e.root = 0;
+            return e;
+        }
+        std::vector<NodePtr> interior_post;
+        std::unordered_set<Node*> on_stack{root.get()};
+        stack.push_back({root, 0});
+        while (!stack.empty()) {
+            Frame& f = stack.back();
+            if (f.next < f.n->parents.size()) {
+                NodePtr p = f.n->parents[f.next++];
+                if (value_of.count(p.get()) || on_stack.count(p.get())) continue;
+                if (!p->is_realized() && is_interior(p)) {
+                    on_stack.insert(p.get());
+                    stack.push_back({p, 0});
+                } else {
+                    if (!p->is_realized()) throw std::runtime_error("HIP codegen: region input was not realized first.");
+                    visit_leaf(p);
+                }
+            } else {
+                interior_post.push_back(f.n);
+                value_of[f.n.get()] = -1;  // assigned below
+                on_stack.erase(f.n.get());
+                stack.pop_back();
+            }
+        }
+        const int nleaves = (int)e.leaves.size();
+        for (size_t k = 0; k < interior_post.size(); ++k) value_of[interior_post[k].get()] = nleaves + (int)k;
+        for (const auto& n : interior_post) {
+            Inst in;
+            in.op = n->op;
+            in.a = value_of.at(n->parents[0].get());
+            if (ops::op_arity(n->op) == 2) in.b = value_of.at(n->parents[1].get());
+            if (n->op == OpEnum::CAST) in.cast = std::get<CastAttrs>(n->attrs).dtype;
+            e.insts.push_back(in);
+        }
+        e.root = value_of.at(root.get());
+        return e;
+    }
+}

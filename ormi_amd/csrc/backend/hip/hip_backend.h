@@ -1,0 +1,112 @@
+// HIP device backend (host side): allocator over the C ABI, fusion
+// scheduler, hipRTC code generator, reduction and matmul graph breakers.
+#pragma once
+#include <cstdint>
+#include <functional>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "core/node.h"
+#include "ormi_hip.h"
+
+#define ORMI_HIP_CHECK(call)                                                                    \
+    do {                                                                                        \
+        int rc_ = (call);                                                                       \
+        if (rc_ != ORMI_HIP_OK) throw std::runtime_error(std::string("HIP Error: ") + ormi_hip_last_error()); \
+    } while (0)
+
+namespace ormi::hip {
+    using NodePtr = std::shared_ptr<Node>;
+
+    // OpEnum -> HIP C expression over operand expressions (the reference's
+    // CUDALoweringRegistry shape, csrc/backend/cuda/lowering_registry.h:11-38).
+    using LoweringFunc = std::function<std::string(const std::vector<std::string>&)>;
+    class HIPLoweringRegistry {
+    public:
+        static void register_func(ops::OpEnum op, LoweringFunc f);
+        static LoweringFunc get(ops::OpEnum op);  // throws when op has no lowering
+        static bool has(ops::OpEnum op);
+    };
+
+    // ---------------------------------------------------------- fusion IR --
+    // A realized input of a fused kernel, with its strides aligned to the
+    // kernel's logical shape (0 on broadcast dims).
+    struct Leaf {
+        NodePtr node;  // keeps the buffer alive until the launch is queued
+        const void* ptr = nullptr;
+        DType dtype = DType::Float32;
+        bool scalar = false;  // 1-element buffer: read element 0 everywhere
+        std::vector<long long> st;
+    };
+
+    struct Inst {
+        ops::OpEnum op;
+        int a = -1, b = -1;          // operand value ids
+        DType cast = DType::Float32;  // CAST target
+    };
+
+    // Values 0..leaves-1 are leaves; value leaves.size()+k is insts[k].
+    struct Expr {
+        std::vector<Leaf> leaves;
+        std::vector<Inst> insts;
+        int root = -1;
+    };
+
+    bool fusible_interior(const Node& n);
+    bool fusible_root(const Node& n);
+    // Unrealized, non-fusible nodes the pointwise region rooted at root reads.
+    std::vector<NodePtr> region_frontier(const NodePtr& root);
+    // SSA tape of the region (every frontier node must be realized), leaves
+    // broadcast right-aligned to `shape`.
+    // plan_only accepts realized operands of any device (kernel planning for
+    // code generator tests; such an Expr is never launched).
+    Expr build_expr(const NodePtr& root, const std::vector<int>& shape, bool plan_only = false);
+
+    // --------------------------------------------------------- kernels --
+    struct FastDiv { uint32_t d, m, s; };
+    FastDiv make_fastdiv(uint32_t d);
+
+    enum class ReduceOp { Sum, Max, Argmax };
+
+    // A generated kernel: source, entry name, launch shape, packed arguments.
+    struct KernelLaunch {
+        std::string source;
+        std::string name;
+        uint32_t grid[3] = {1, 1, 1};
+        uint32_t block[3] = {256, 1, 1};
+        std::vector<uint64_t> args;  // every parameter is 8 bytes
+        std::string plan;            // human-readable summary (tests, debugging)
+    };
+
+    // Element-wise map of expr over `shape` into out (contiguous, out_dtype).
+    KernelLaunch plan_map(const Expr& expr, const std::vector<int>& shape, void* out, DType out_dtype, int compute_units);
+
+    // Reduction of expr (evaluated over in_shape) over `axes` (sorted; empty =
+    // all). out holds prod(kept dims) values, fp32 (Sum/Max) or int64 (Argmax).
+    // When the reduced range is split across work-groups, partial results go
+    // to workspace (sized by reduce_workspace_bytes) and a second kernel
+    // (second) finishes them.
+    struct ReducePlan {
+        KernelLaunch first;
+        bool two_pass = false;
+        KernelLaunch second;
+        size_t workspace_bytes = 0;
+    };
+    ReducePlan plan_reduce(const Expr& expr, const std::vector<int>& in_shape, const std::vector<int>& axes, ReduceOp op,
+                           void* out, int compute_units);
+    void bind_workspace(ReducePlan& plan, void* workspace);
+
+    // hipRTC options every generated kernel is compiled with.
+    const std::vector<std::string>& rtc_options();
+    // Compile (cached) and launch.
+    void launch(const KernelLaunch& k);
+
+    // ------------------------------------------------------- scheduler --
+    // Realize root on the HIP device: pointwise regions become one fused
+    // kernel, reductions fuse their pointwise producer as a prologue, views
+    // alias, matmuls call the MFMA GEMM.
+    void realize(const NodePtr& root);
+    int device_compute_units();
+}

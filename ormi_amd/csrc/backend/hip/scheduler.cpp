@@ -1,0 +1,265 @@
+// HIP device: allocator, fusion scheduler and graph breakers.
+//
+// Allocator: HIPAllocator implements the reference's IAllocator
+// (csrc/core/allocator.h:7-21) over libormi_hip, with the same exact-size
+// free-list pool as CUDAAllocator (csrc/backend/cuda/allocator.cu:36-55).
+//
+// Scheduler: the reference realizes every parent before compiling a node
+// (csrc/backend/runtime.cpp:16-18), so each op is its own kernel and every
+// intermediate round-trips through HBM. On the HIP device, realize(root):
+//   * view        -> realize the parent, alias its buffer (runtime.cpp:20-23);
+//   * pointwise   -> realize only the region's frontier (views, reductions,
+//                    matmuls, realized nodes), then ONE fused kernel writes
+//                    root; interior pointwise nodes stay unrealized and are
+//                    recomputed by any later kernel that reads them;
+//   * SUM/MAX/ARGMAX -> the producing pointwise region is fused into the
+//                    reduction as its prologue;
+//   * MATMUL      -> both operands realized, MFMA GEMM.
+// Reductions and MATMUL are registered as graph breakers for DeviceEnum::HIP
+// (the reference's plugin point, csrc/backend/graph_breakers.h:12-14).
+#include <mutex>
+#include <unordered_map>
+#include <vector>
+
+#include "backend/hip/hip_backend.h"
+#include "core/allocator.h"
+#include "core/memory.h"
+#include "runtime/graph_breakers.h"
+#include "runtime/runtime.h"
+
+namespace ormi {
+    class HIPAllocator : public IAllocator {
+        std::mutex mu_;
+        std::unordered_map<size_t, std::vector<void*>> free_blocks_;
+
+    public:
+        HIPAllocator() { ORMI_HIP_CHECK(ormi_hip_init(0)); }
+
+        void* allocate(size_t bytes) override {
+            {
+                std::lock_guard<std::mutex> lock(mu_);
+                auto it = free_blocks_.find(bytes);
+                if (it != free_blocks_.end() && !it->second.empty()) {
+                    void* p = it->second.back();
+                    it->second.pop_back();
+                    return p;
+                }
+            }
+            void* p = nullptr;
+            if (ormi_hip_malloc(&p, bytes) != ORMI_HIP_OK) {
+                // Out of memory: give cached blocks back to the device and retry once.
+                release_cached();
+                ORMI_HIP_CHECK(ormi_hip_malloc(&p, bytes));
+            }
+            return p;
+        }
+
+        void free(void* ptr, size_t bytes) override {
+            if (!ptr) return;
+            std::lock_guard<std::mutex> lock(mu_);
+            free_blocks_[bytes].push_back(ptr);
+        }
+
+        void release_cached() {
+            ormi_hip_synchronize();
+            std::lock_guard<std::mutex> lock(mu_);
+            for (auto& kv : free_blocks_)
+                for (void* p : kv.second) ormi_hip_free(p);
+            free_blocks_.clear();
+        }
+
+        void memset(void* ptr, int value, size_t bytes) override {
+            ORMI_HIP_CHECK(ormi_hip_memset_d8(ptr, (unsigned char)value, bytes));
+        }
+        void memcpy(void* dst, const void* src, size_t size) override { ORMI_HIP_CHECK(ormi_hip_memcpy_d2d(dst, src, size)); }
+        void fill_n(void* dst, const void* val, size_t elements, DType dtype) override {
+            ORMI_HIP_CHECK(ormi_hip_fill(dst, val, dtype_size(dtype), elements));
+        }
+        void copy_device_to_host(void* dst, const void* src, size_t bytes) override {
+            ORMI_HIP_CHECK(ormi_hip_memcpy_d2h(dst, src, bytes));
+        }
+        void copy_host_to_device(void* dst, const void* src, size_t bytes) override {
+            ORMI_HIP_CHECK(ormi_hip_memcpy_h2d(dst, src, bytes));
+        }
+        bool is_host_visible() const override { return false; }
+    };
+
+    // Constructed on first use; a constructor that throws (no GPU) leaves the
+    // HIP device unavailable, as a throwing CUDAAllocator does for CUDA.
+    static IAllocator* hip_allocator_instance() {
+        static HIPAllocator* inst = new HIPAllocator();  // outlives every Buffer
+        return inst;
+    }
+    static const bool hip_allocator_registered = (register_allocator(DeviceEnum::HIP, hip_allocator_instance), true);
+}
+
+namespace ormi::hip {
+    using ops::OpEnum;
+
+    int device_compute_units() {
+        static int cu = [] {
+            ormi_hip_props p{};
+            return ormi_hip_get_props(&p) == ORMI_HIP_OK && p.compute_units > 0 ? p.compute_units : 256;
+        }();
+        return cu;
+    }
+
+    static void run_map(const NodePtr& root) {
+        for (const auto& f : region_frontier(root)) realize(f);
+        const Expr e = build_expr(root, root->view.shape);
+        auto out = empty(root->view.shape, DeviceEnum::HIP, root->dtype);
+        root->data = out;
+        root->view.strides = calc_contiguous_strides(root->view.shape);
+        if (out->numel() == 0) return;
+        launch(plan_map(e, root->view.shape, out->ptr, root->dtype, device_compute_units()));
+    }
+
+    // Realize what a reduction reads: a pointwise producer stays unrealized
+    // (it becomes the prologue); anything else is realized.
+    static void prepare_input(const NodePtr& x) {
+        if (x->is_realized()) return;
+        if (fusible_root(*x)) {
+            for (const auto& f : region_frontier(x)) realize(f);
+        } else {
+            realize(x);
+        }
+    }
+
+    static void reduce_handler(const NodePtr& root, ReduceOp op) {
+        const NodePtr& x = root->parents[0];
+        prepare_input(x);
+        const auto& attrs = std::get<ReduceAttrs>(root->attrs);
+        const std::vector<int>& in_shape = x->view.shape;
+        const long long in_numel = shape_numel(in_shape);
+        const DType out_dtype = op == ReduceOp::Argmax ? DType::Int64 : DType::Float32;
+        auto out = empty(root->view.shape, DeviceEnum::HIP, out_dtype);
+        root->data = out;
+        root->view.strides = calc_contiguous_strides(root->view.shape);
+        if (out->numel() == 0) return;
+        if (in_numel == 0) {
+            if (op != ReduceOp::Sum) throw std::runtime_error("zero-size array to reduction operation maximum which has no identity");
+            const float zero = 0.0f;
+            ORMI_HIP_CHECK(ormi_hip_fill(out->ptr, &zero, 4, out->numel()));
+            return;
+        }
+        const Expr e = build_expr(x, in_shape);
+        ReducePlan plan = plan_reduce(e, in_shape, attrs.axes, op, out->ptr, device_compute_units());
+        std::shared_ptr<Buffer> ws;
+        if (plan.two_pass) {
+            ws = empty({(int)((plan.workspace_bytes + 3) / 4)}, DeviceEnum::HIP, DType::Float32);
+            bind_workspace(plan, ws->ptr);
+        }
+        launch(plan.first);
+        if (plan.two_pass) launch(plan.second);
+        // ws returns to the pool here; later work on the same stream is ordered
+        // after these kernels, so reuse is safe.
+    }
+
+    // Operand of a GEMM in the form ormi_hip_gemm takes: dtype f32/bf16/f16,
+    // realized. Other dtypes (and mixed pairs) are converted to f32 by a fused
+    // cast kernel.
+    static NodePtr gemm_operand(const NodePtr& x, DType want) {
+        realize(x);
+        if (x->data->dtype == want) return x;
+        auto c = std::make_shared<Node>(OpEnum::CAST, std::vector<NodePtr>{x}, x->device, CastAttrs{want});
+        realize(c);
+        return c;
+    }
+
+    // MATMUL on the HIP device (replaces cuda::matmul, csrc/backend/cuda/kernels/blas/
+    // matmul.cu:19-122): same shape rule, trans/ld derived from strides, batch
+    // dims broadcast with stride 0, contiguous fp32 output.
+    static void matmul_handler(const NodePtr& root) {
+        NodePtr A = root->parents[0], B = root->parents[1];
+        realize(A);
+        realize(B);
+        DType dt = A->data->dtype;
+        const bool same_float = dt == B->data->dtype && (dt == DType::Float32 || dt == DType::BFloat16 || dt == DType::Float16);
+        if (!same_float) dt = DType::Float32;
+        A = gemm_operand(A, dt);
+        B = gemm_operand(B, dt);
+
+        const auto& va = A->view;
+        const auto& vb = B->view;
+        const auto& vo = root->view;
+        const int na = (int)va.shape.size(), nb = (int)vb.shape.size(), no = (int)vo.shape.size();
+        auto out = empty(vo.shape, DeviceEnum::HIP, DType::Float32);
+        root->data = out;
+        root->view.strides = calc_contiguous_strides(vo.shape);
+        if (out->numel() == 0) return;
+
+        ormi_gemm_desc d{};
+        d.dtype = dt == DType::Float32 ? ORMI_DTYPE_F32 : dt == DType::BFloat16 ? ORMI_DTYPE_BF16 : ORMI_DTYPE_F16;
+        d.M = va.shape[na - 2];
+        d.K = va.shape[na - 1];
+        d.N = vb.shape[nb - 1];
+        d.a = A->data->ptr;
+        d.a_stride_m = va.strides[na - 2];
+        d.a_stride_k = va.strides[na - 1];
+        d.b = B->data->ptr;
+        d.b_stride_k = vb.strides[nb - 2];
+        d.b_stride_n = vb.strides[nb - 1];
+        d.c = (float*)out->ptr;
+        // Batch dims: drop extent-1 dims, then each operand's batch stride is its
+        // own stride where it has that dim with extent > 1, else 0 (broadcast).
+        std::vector<int> bshape;
+        std::vector<long long> abs, bbs;
+        for (int i = 0; i < no - 2; ++i) {
+            if (vo.shape[i] == 1) continue;
+            auto stride_of = [&](const TensorView& v, int nd) -> long long {
+                const int td = i - ((no - 2) - (nd - 2));
+                return (td >= 0 && v.shape[td] > 1) ? v.strides[td] : 0;
+            };
+            bshape.push_back(vo.shape[i]);
+            abs.push_back(stride_of(va, na));
+            bbs.push_back(stride_of(vb, nb));
+        }
+        // Merge batch dims while both operands stay linear (keeps within 4 dims).
+        for (size_t i = 0; i + 1 < bshape.size();) {
+            if (abs[i] == abs[i + 1] * bshape[i + 1] && bbs[i] == bbs[i + 1] * bshape[i + 1]) {
+                bshape[i] *= bshape[i + 1];
+                abs[i] = abs[i + 1];
+                bbs[i] = bbs[i + 1];
+                bshape.erase(bshape.begin() + i + 1);
+                abs.erase(abs.begin() + i + 1);
+                bbs.erase(bbs.begin() + i + 1);
+            } else {
+                ++i;
+            }
+        }
+        if (bshape.size() > ORMI_GEMM_MAX_BATCH_DIMS) throw std::runtime_error("HIP MATMUL: more than 4 non-mergeable batch dims.");
+        d.batch_ndim = (int)bshape.size();
+        for (size_t i = 0; i < bshape.size(); ++i) {
+            d.batch_shape[i] = bshape[i];
+            d.a_batch_stride[i] = abs[i];
+            d.b_batch_stride[i] = bbs[i];
+        }
+        ORMI_HIP_CHECK(ormi_hip_gemm(&d));
+    }
+
+    void realize(const NodePtr& root) {
+        if (!root || root->is_realized()) return;
+        if (root->device.type != DeviceEnum::HIP) throw std::runtime_error("HIP scheduler: node belongs to another device.");
+        if (is_view_op(root->op)) {
+            realize(root->parents[0]);
+            root->data = root->parents[0]->data;
+            return;
+        }
+        if (fusible_root(*root)) {
+            run_map(root);
+            return;
+        }
+        if (try_execute_graph_break(root)) return;
+        if (root->op == OpEnum::LEAF || root->op == OpEnum::CONST) throw std::runtime_error("HIP scheduler: leaf without a buffer.");
+        throw std::runtime_error(std::string("HIP scheduler: no lowering for op ") + ops::op_name(root->op));
+    }
+
+    static RegisterGraphBreaker reg_sum(DeviceEnum::HIP, OpEnum::SUM, [](std::shared_ptr<Node> n) { reduce_handler(n, ReduceOp::Sum); });
+    static RegisterGraphBreaker reg_max(DeviceEnum::HIP, OpEnum::MAX, [](std::shared_ptr<Node> n) { reduce_handler(n, ReduceOp::Max); });
+    static RegisterGraphBreaker reg_argmax(DeviceEnum::HIP, OpEnum::ARGMAX, [](std::shared_ptr<Node> n) { reduce_handler(n, ReduceOp::Argmax); });
+    static RegisterGraphBreaker reg_matmul(DeviceEnum::HIP, OpEnum::MATMUL, matmul_handler);
+    static RegisterScheduler reg_sched(DeviceEnum::HIP, [](std::shared_ptr<Node> n) { realize(n); });
+    // Element-wise JIT entry for a node whose parents are realized: the
+    // reference's execute_jit slot (csrc/backend/runtime.cpp:29-38).
+    static RegisterJit reg_jit(DeviceEnum::HIP, [](std::shared_ptr<Node> n) { run_map(n); });
+}

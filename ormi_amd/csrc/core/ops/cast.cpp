@@ -1,0 +1,30 @@
+// CAST (additive): element type conversion, materialized contiguously.
+// Float -> bf16/fp16 rounds to nearest even.
+#include <stdexcept>
+#include "core/ops/api.h"
+#include "core/shape.h"
+#include "core/adjoint.h"
+#include "core/registry.h"
+
+namespace ormi {
+    using ops::OpEnum;
+    using NodeVec = std::vector<std::shared_ptr<Node>>;
+
+    namespace ops {
+        NodePtr cast(NodePtr x, DType dtype) {
+            if (dtype == DType::Bool || dtype == DType::Int32) throw std::runtime_error("CAST supports float32, bfloat16, float16 and int64 targets.");
+            return std::make_shared<Node>(OpEnum::CAST, NodeVec{x}, x->device, CastAttrs{dtype});
+        }
+    }
+
+    static void adjoint_cast(std::shared_ptr<Node> n) {
+        auto x = n->parents[0];
+        if (!x->requires_grad) return;
+        std::shared_ptr<Node> g = n->grad;
+        if (x->dtype != g->dtype) g = std::make_shared<Node>(OpEnum::CAST, NodeVec{g}, n->device, CastAttrs{x->dtype});
+        accumulate_grad(x, g, n->device);
+    }
+
+    static RegisterShape rs_cast(OpEnum::CAST, infer_unary_shape);
+    static RegisterAdjoint ra_cast(OpEnum::CAST, adjoint_cast);
+}

@@ -1,0 +1,56 @@
+#include <stdexcept>
+#include <algorithm>
+#include "core/shape.h"
+#include "core/node.h"
+
+namespace ormi {
+    bool TensorView::is_contiguous() const {
+        long long expected = 1;
+        for (int i = (int)shape.size() - 1; i >= 0; --i) {
+            if (strides[i] != expected) return false;
+            expected *= shape[i];
+        }
+        return true;
+    }
+
+    std::vector<int> calc_contiguous_strides(const std::vector<int>& shape) {
+        std::vector<int> strides(shape.size(), 1);
+        for (int i = (int)shape.size() - 2; i >= 0; --i) strides[i] = strides[i + 1] * shape[i + 1];
+        return strides;
+    }
+
+    // Right-aligned numpy broadcasting (reference: csrc/core/shape.cpp:27-44).
+    std::vector<int> broadcast_shapes(const std::vector<int>& a, const std::vector<int>& b) {
+        const int na = (int)a.size(), nb = (int)b.size();
+        const int n = std::max(na, nb);
+        std::vector<int> out(n);
+        for (int i = 0; i < n; ++i) {
+            const int da = i < n - na ? 1 : a[i - (n - na)];
+            const int db = i < n - nb ? 1 : b[i - (n - nb)];
+            if (da != db && da != 1 && db != 1) throw std::runtime_error("Operands could not be broadcast together.");
+            out[i] = std::max(da, db);
+        }
+        return out;
+    }
+
+    std::vector<int> infer_shape(ops::OpEnum op, const std::vector<std::shared_ptr<Node>>& parents, const OpAttributes& attrs) {
+        if (op == ops::OpEnum::LEAF || op == ops::OpEnum::CONST || parents.empty()) return {};
+        auto func = Registry<ShapeInferFunc>::get(op);
+        if (!func) throw std::runtime_error("Shape inference rule not registered for this OpEnum.");
+        return func(parents, attrs);
+    }
+
+    std::vector<int> infer_unary_shape(const std::vector<std::shared_ptr<Node>>& parents, const OpAttributes&) {
+        return parents[0]->view.shape;
+    }
+
+    std::vector<int> infer_binary_shape(const std::vector<std::shared_ptr<Node>>& parents, const OpAttributes&) {
+        return broadcast_shapes(parents[0]->view.shape, parents[1]->view.shape);
+    }
+
+    long long shape_numel(const std::vector<int>& shape) {
+        long long n = 1;
+        for (int d : shape) n *= d;
+        return n;
+    }
+}

@@ -1,0 +1,378 @@
+// libormi_hip.so: device set-up, memory, hipRTC compile cache, kernel launch,
+// events, and the small fill/convert kernels. Implements include/ormi_hip.h.
+#include <hip/hip_runtime.h>
+#include <hip/hiprtc.h>
+
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "ormi_hip.h"
+#include "ormi_hip_internal.h"
+#include "device/ormi_device.h"
+
+namespace ormi_hip {
+
+static thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+struct DeviceState {
+    std::mutex mu;
+    bool inited = false;
+    int device = -1;
+    hipDeviceProp_t props{};
+    std::string arch;  // full target id, e.g. gfx950:sramecc+:xnack-
+};
+
+static DeviceState& state() {
+    static DeviceState* s = new DeviceState();  // never destroyed: buffers may be freed at exit
+    return *s;
+}
+
+int ensure_init() {
+    DeviceState& s = state();
+    if (s.inited) return ORMI_HIP_OK;
+    return ormi_hip_init(0);
+}
+
+int compute_units() {
+    return state().inited ? state().props.multiProcessorCount : 256;
+}
+
+// ---------------------------------------------------------------- kernels --
+template <typename T>
+__global__ void fill_kernel(T* __restrict__ dst, T value, size_t count) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) dst[i] = value;
+}
+
+__device__ __forceinline__ float load_as_f32(const void* p, int dt, size_t i) {
+    switch (dt) {
+        case ORMI_DTYPE_F32: return ((const float*)p)[i];
+        case ORMI_DTYPE_BF16: return ormi_bf16_to_f32(((const unsigned short*)p)[i]);
+        case ORMI_DTYPE_F16: return ormi_f16_to_f32(((const unsigned short*)p)[i]);
+        case ORMI_DTYPE_I32: return (float)((const int*)p)[i];
+        case ORMI_DTYPE_I64: return (float)((const long long*)p)[i];
+        default: return ((const unsigned char*)p)[i] ? 1.0f : 0.0f;
+    }
+}
+
+__global__ void convert_kernel(void* __restrict__ dst, int dst_dt, const void* __restrict__ src, int src_dt, size_t count) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
+        if (src_dt == ORMI_DTYPE_I64 && dst_dt == ORMI_DTYPE_I64) {
+            ((long long*)dst)[i] = ((const long long*)src)[i];
+            continue;
+        }
+        const float v = load_as_f32(src, src_dt, i);
+        switch (dst_dt) {
+            case ORMI_DTYPE_F32: ((float*)dst)[i] = v; break;
+            case ORMI_DTYPE_BF16: ((unsigned short*)dst)[i] = ormi_f32_to_bf16(v); break;
+            case ORMI_DTYPE_F16: ((unsigned short*)dst)[i] = ormi_f32_to_f16(v); break;
+            case ORMI_DTYPE_I32: ((int*)dst)[i] = (int)ormi_f32_to_i64(v); break;
+            case ORMI_DTYPE_I64: ((long long*)dst)[i] = ormi_f32_to_i64(v); break;
+            default: ((unsigned char*)dst)[i] = v != 0.0f; break;
+        }
+    }
+}
+
+static unsigned grid_for(size_t count, unsigned block) {
+    size_t g = (count + block - 1) / block;
+    const size_t cap = (size_t)compute_units() * 8;
+    if (g > cap) g = cap;
+    return g ? (unsigned)g : 1u;
+}
+
+// ------------------------------------------------------------ rtc cache --
+struct RtcEntry {
+    hipModule_t module;
+    hipFunction_t function;
+};
+
+struct RtcCache {
+    std::mutex mu;
+    std::unordered_map<std::string, uint64_t> by_key;
+    std::vector<RtcEntry> entries;
+};
+
+static RtcCache& rtc_cache() {
+    static RtcCache* c = new RtcCache();
+    return *c;
+}
+
+static int rtc_build(const char* source, const std::string& target, const char* const* options, int num_options,
+                     std::vector<char>& code) {
+    hiprtcProgram prog;
+    hiprtcResult r = hiprtcCreateProgram(&prog, source, "ormi_generated.hip", 0, nullptr, nullptr);
+    if (r != HIPRTC_SUCCESS) return fail(ORMI_HIP_ERR_COMPILE, std::string("hiprtcCreateProgram: ") + hiprtcGetErrorString(r));
+    std::vector<std::string> opts;
+    opts.push_back("--offload-arch=" + target);
+    for (int i = 0; i < num_options; ++i) opts.emplace_back(options[i]);
+    std::vector<const char*> copts;
+    for (auto& o : opts) copts.push_back(o.c_str());
+    r = hiprtcCompileProgram(prog, (int)copts.size(), copts.data());
+    if (r != HIPRTC_SUCCESS) {
+        size_t log_size = 0;
+        hiprtcGetProgramLogSize(prog, &log_size);
+        std::string log(log_size + 1, '\0');
+        if (log_size) hiprtcGetProgramLog(prog, &log[0]);
+        hiprtcDestroyProgram(&prog);
+        return fail(ORMI_HIP_ERR_COMPILE, std::string("hipRTC compile failed: ") + hiprtcGetErrorString(r) + "\n" + log);
+    }
+    size_t code_size = 0;
+    hiprtcGetCodeSize(prog, &code_size);
+    code.resize(code_size);
+    hiprtcGetCode(prog, code.data());
+    hiprtcDestroyProgram(&prog);
+    return ORMI_HIP_OK;
+}
+
+}  // namespace ormi_hip
+
+using namespace ormi_hip;
+
+#define ORMI_HIP_TRY(call)                                                                           \
+    do {                                                                                             \
+        hipError_t e_ = (call);                                                                      \
+        if (e_ != hipSuccess) return fail(ORMI_HIP_ERR_RUNTIME, std::string(#call) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+#define ORMI_ENSURE_INIT()                    \
+    do {                                      \
+        int rc_ = ensure_init();              \
+        if (rc_ != ORMI_HIP_OK) return rc_;   \
+    } while (0)
+
+extern "C" {
+
+const char* ormi_hip_last_error(void) { return g_last_error.c_str(); }
+
+int ormi_hip_device_count(int* count) {
+    if (!count) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_device_count: null output");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    *count = (e == hipSuccess) ? n : 0;
+    return ORMI_HIP_OK;
+}
+
+int ormi_hip_init(int device) {
+    DeviceState& s = state();
+    std::lock_guard<std::mutex> lock(s.mu);
+    if (s.inited) {
+        if (device != s.device) return fail(ORMI_HIP_ERR_UNSUPPORTED, "ormi_hip_init: library already bound to another device");
+        return ORMI_HIP_OK;
+    }
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return fail(ORMI_HIP_ERR_NO_DEVICE, "HIP Error: no GPU device is visible to this process");
+    if (device < 0 || device >= n) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_init: device index out of range");
+    ORMI_HIP_TRY(hipSetDevice(device));
+    ORMI_HIP_TRY(hipGetDeviceProperties(&s.props, device));
+    s.arch = s.props.gcnArchName;
+    s.device = device;
+    s.inited = true;
+    return ORMI_HIP_OK;
+}
+
+int ormi_hip_get_props(ormi_hip_props* out) {
+    if (!out) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_get_props: null output");
+    ORMI_ENSURE_INIT();
+    const DeviceState& s = state();
+    std::memset(out, 0, sizeof(*out));
+    std::strncpy(out->name, s.arch.c_str(), sizeof(out->name) - 1);
+    out->compute_units = s.props.multiProcessorCount;
+    out->clock_khz = s.props.clockRate;
+    out->lds_bytes_per_block = (int)s.props.sharedMemPerBlock;
+    out->total_mem_bytes = s.props.totalGlobalMem;
+    return ORMI_HIP_OK;
+}
+
+int ormi_hip_malloc(void** ptr, size_t bytes) {
+    if (!ptr) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_malloc: null output");
+    ORMI_ENSURE_INIT();
+    *ptr = nullptr;
+    if (bytes == 0) return ORMI_HIP_OK;
+    ORMI_HIP_TRY(hipMalloc(ptr, bytes));
+    return ORMI_HIP_OK;
+}
+
+int ormi_hip_free(void* ptr) {
+    if (!ptr) return ORMI_HIP_OK;
+    ORMI_HIP_TRY(hipFree(ptr));
+    return ORMI_HIP_OK;
+}
+
+int ormi_hip_fill(void* dst, const void* value, size_t elem_bytes, size_t count) {
+    if (count == 0) return ORMI_HIP_OK;
+    if (!dst || !value) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_fill: null pointer");
+    ORMI_ENSURE_INIT();
+    const unsigned block = 256, grid = grid_for(count, block);
+    switch (elem_bytes) {
+        case 1: { unsigned char v; std::memcpy(&v, value, 1); fill_kernel<unsigned char><<<grid, block>>>((unsigned char*)dst, v, count); break; }
+        case 2: { unsigned short v; std::memcpy(&v, value, 2); fill_kernel<unsigned short><<<grid, block>>>((unsigned short*)dst, v, count); break; }
+        case 4: { unsigned v; std::memcpy(&v, value, 4); fill_kernel<unsigned><<<grid, block>>>((unsigned*)dst, v, count); break; }
+        case 8: { unsigned long long v; std::memcpy(&v, value, 8); fill_kernel<unsigned long long><<<grid, block>>>((unsigned long long*)dst, v, count); break; }
+        default: return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_fill: element size must be 1, 2, 4 or 8");
+    }
+    ORMI_HIP_TRY(hipGetLastError());
+    return ORMI_HIP_OK;
+}
+
+int ormi_hip_memset_d8(void* dst, unsigned char value, size_t count) { return ormi_hip_fill(dst, &value, 1, count); }
+int ormi_hip_memset_d32(void* dst, uint32_t value, size_t count) { return ormi_hip_fill(dst, &value, 4, count); }
+
+int ormi_hip_memcpy_h2d(void* dst, const void* src, size_t bytes) {
+    if (bytes == 0) return ORMI_HIP_OK;
+    if (!dst || !src) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_memcpy_h2d: null pointer");
+    ORMI_ENSURE_INIT();
+    ORMI_HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    return ORMI_HIP_OK;
+}
+
+int ormi_hip_memcpy_d2h(void* dst, const void* src, size_t bytes) {
+    if (bytes == 0) return ORMI_HIP_OK;
+    if (!dst || !src) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_memcpy_d2h: null pointer");
+    ORMI_ENSURE_INIT();
+    ORMI_HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    return ORMI_HIP_OK;
+}
+
+int ormi_hip_memcpy_d2d(void* dst, const void* src, size_t bytes) {
+    if (bytes == 0) return ORMI_HIP_OK;
+    if (!dst || !src) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_memcpy_d2d: null pointer");
+    ORMI_ENSURE_INIT();
+    ORMI_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, 0));
+    return ORMI_HIP_OK;
+}
+
+int ormi_hip_synchronize(void) {
+    ORMI_ENSURE_INIT();
+    ORMI_HIP_TRY(hipDeviceSynchronize());
+    return ORMI_HIP_OK;
+}
+
+int ormi_hip_convert(void* dst, int dst_dtype, const void* src, int src_dtype, size_t count) {
+    if (count == 0) return ORMI_HIP_OK;
+    if (!dst || !src) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_convert: null pointer");
+    if (dst_dtype < 0 || dst_dtype > ORMI_DTYPE_I64 || src_dtype < 0 || src_dtype > ORMI_DTYPE_I64)
+        return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_convert: unknown dtype code");
+    ORMI_ENSURE_INIT();
+    const unsigned block = 256, grid = grid_for(count, block);
+    convert_kernel<<<grid, block>>>(dst, dst_dtype, src, src_dtype, count);
+    ORMI_HIP_TRY(hipGetLastError());
+    return ORMI_HIP_OK;
+}
+
+int ormi_hip_rtc_compile(const char* source, const char* kernel_name, const char* const* options, int num_options,
+                         uint64_t* handle) {
+    if (!source || !kernel_name || !handle || (num_options > 0 && !options))
+        return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_rtc_compile: null argument");
+    ORMI_ENSURE_INIT();
+    std::string key(kernel_name);
+    key.push_back('\0');
+    for (int i = 0; i < num_options; ++i) {
+        key += options[i];
+        key.push_back('\0');
+    }
+    key += source;
+    RtcCache& c = rtc_cache();
+    {
+        std::lock_guard<std::mutex> lock(c.mu);
+        auto it = c.by_key.find(key);
+        if (it != c.by_key.end()) {
+            *handle = it->second;
+            return ORMI_HIP_OK;
+        }
+    }
+    std::vector<char> code;
+    int rc = rtc_build(source, state().arch, options, num_options, code);
+    if (rc != ORMI_HIP_OK) return rc;
+    RtcEntry e{};
+    ORMI_HIP_TRY(hipModuleLoadData(&e.module, code.data()));
+    hipError_t ge = hipModuleGetFunction(&e.function, e.module, kernel_name);
+    if (ge != hipSuccess) {
+        (void)hipModuleUnload(e.module);
+        return fail(ORMI_HIP_ERR_COMPILE, std::string("hipModuleGetFunction(") + kernel_name + "): " + hipGetErrorString(ge));
+    }
+    std::lock_guard<std::mutex> lock(c.mu);
+    auto it = c.by_key.find(key);
+    if (it != c.by_key.end()) {  // another thread compiled the same source meanwhile
+        (void)hipModuleUnload(e.module);
+        *handle = it->second;
+        return ORMI_HIP_OK;
+    }
+    c.entries.push_back(e);
+    *handle = (uint64_t)c.entries.size();
+    c.by_key.emplace(std::move(key), *handle);
+    return ORMI_HIP_OK;
+}
+
+int ormi_hip_rtc_compile_only(const char* source, const char* target, const char* const* options, int num_options,
+                              size_t* code_bytes) {
+    if (!source || !target || !code_bytes || (num_options > 0 && !options))
+        return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_rtc_compile_only: null argument");
+    std::vector<char> code;
+    int rc = rtc_build(source, target, options, num_options, code);
+    if (rc != ORMI_HIP_OK) return rc;
+    *code_bytes = code.size();
+    return ORMI_HIP_OK;
+}
+
+int ormi_hip_rtc_cache_size(uint64_t* entries) {
+    if (!entries) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_rtc_cache_size: null output");
+    RtcCache& c = rtc_cache();
+    std::lock_guard<std::mutex> lock(c.mu);
+    *entries = c.entries.size();
+    return ORMI_HIP_OK;
+}
+
+int ormi_hip_launch(uint64_t handle, const uint32_t grid[3], const uint32_t block[3], uint32_t lds_bytes, void** args) {
+    if (!grid || !block) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_launch: null grid/block");
+    hipFunction_t fn;
+    {
+        RtcCache& c = rtc_cache();
+        std::lock_guard<std::mutex> lock(c.mu);
+        if (handle == 0 || handle > c.entries.size()) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_launch: unknown kernel handle");
+        fn = c.entries[handle - 1].function;
+    }
+    if (grid[0] == 0 || grid[1] == 0 || grid[2] == 0) return ORMI_HIP_OK;  // empty launch: nothing to do
+    if (block[0] * block[1] * block[2] == 0 || block[0] * block[1] * block[2] > 1024)
+        return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_launch: block size must be 1..1024 threads");
+    ORMI_HIP_TRY(hipModuleLaunchKernel(fn, grid[0], grid[1], grid[2], block[0], block[1], block[2], lds_bytes, 0, args, nullptr));
+    return ORMI_HIP_OK;
+}
+
+int ormi_hip_event_create(void** event) {
+    if (!event) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_event_create: null output");
+    ORMI_ENSURE_INIT();
+    hipEvent_t e;
+    ORMI_HIP_TRY(hipEventCreate(&e));
+    *event = (void*)e;
+    return ORMI_HIP_OK;
+}
+
+int ormi_hip_event_record(void* event) {
+    if (!event) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_event_record: null event");
+    ORMI_HIP_TRY(hipEventRecord((hipEvent_t)event, 0));
+    return ORMI_HIP_OK;
+}
+
+int ormi_hip_event_elapsed_ms(void* start, void* end, float* ms) {
+    if (!start || !end || !ms) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_event_elapsed_ms: null argument");
+    ORMI_HIP_TRY(hipEventSynchronize((hipEvent_t)end));
+    ORMI_HIP_TRY(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)end));
+    return ORMI_HIP_OK;
+}
+
+int ormi_hip_event_destroy(void* event) {
+    if (!event) return ORMI_HIP_OK;
+    ORMI_HIP_TRY(hipEventDestroy((hipEvent_t)event));
+    return ORMI_HIP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,30 @@
+#pragma once
+#include <functional>
+#include <memory>
+#include "core/node.h"
+
+namespace ormi {
+    // Realize root (reference: csrc/backend/runtime.cpp:13-39). A device that
+    // registered a scheduler decides itself which nodes get buffers (the HIP
+    // device fuses pointwise regions); every other device gets the reference
+    // order: all parents first, views alias, graph breakers, else the device JIT.
+    void execute_graph(std::shared_ptr<Node> root);
+
+    // The reference order, for any device (the HIP scheduler never calls it).
+    void execute_graph_eager(std::shared_ptr<Node> root);
+
+    bool is_view_op(ops::OpEnum op);
+
+    using JitFunc = std::function<void(std::shared_ptr<Node>)>;
+    using SchedulerFunc = std::function<void(std::shared_ptr<Node>)>;
+
+    // Per-device element-wise JIT, the reference's switch (runtime.cpp:29-38) as a table.
+    void register_jit(DeviceEnum dev, JitFunc fn);
+    void register_scheduler(DeviceEnum dev, SchedulerFunc fn);
+    bool has_jit(DeviceEnum dev);
+    // Call the registered element-wise JIT of root's device directly.
+    void run_jit(std::shared_ptr<Node> root);
+
+    struct RegisterJit { RegisterJit(DeviceEnum d, JitFunc f) { register_jit(d, std::move(f)); } };
+    struct RegisterScheduler { RegisterScheduler(DeviceEnum d, SchedulerFunc f) { register_scheduler(d, std::move(f)); } };
+}

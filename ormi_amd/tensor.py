@@ -1,0 +1,230 @@
+"""Tensor: the Python face of the lazy graph.
+
+Same constructor, operators, views, realize/numpy/backward/zero_grad as
+ormi_core.Tensor (reference ormi-core/src/ormi_core/tensor.py:10-190). Additive:
+the "hip" device, a dtype argument for leaves, and element-wise / reduction
+methods for the ops the reference lacks (relu, tanh, sigmoid, gelu, sum, mean,
+max, argmax, astype).
+"""
+from __future__ import annotations
+
+import numpy as np
+from numpy.lib.stride_tricks import as_strided
+
+from ._ext import ormi_backend
+from .exceptions import raise_device_mismatch
+
+OpEnum = ormi_backend.OpEnum
+DeviceEnum = ormi_backend.DeviceEnum
+Device = ormi_backend.Device
+Node = ormi_backend.Node
+
+_DEVICE_STRINGS = {"cpu": DeviceEnum.CPU, "cuda": DeviceEnum.CUDA, "hip": DeviceEnum.HIP}
+
+
+def _parse_device(device) -> Device:
+    if device is None:
+        return Device(DeviceEnum.CPU, 0)
+    if isinstance(device, str):
+        name, _, idx = device.lower().partition(":")
+        if name not in _DEVICE_STRINGS:
+            raise_device_mismatch(msg="Unsupported string backend", got=device)
+        return Device(_DEVICE_STRINGS[name], int(idx) if idx else 0)
+    if isinstance(device, DeviceEnum):
+        return Device(device, 0)
+    if isinstance(device, Device):
+        return device
+    raise_device_mismatch(msg="Device argument is of invalid type.", got=type(device))
+
+
+class Tensor:
+    def __init__(self, data=None, device=None, requires_grad: bool = False, _node: Node | None = None,
+                 dtype: str | None = None):
+        self.device = _parse_device(device)
+        if _node is not None:
+            self._node = _node
+        elif data is not None:
+            if not isinstance(data, np.ndarray):
+                data = np.array(data, dtype=np.int64 if dtype == "int64" else np.float32)
+            buffer = ormi_backend.numpy_to_buffer(data, self.device.type, dtype)
+            self._node = Node(buffer, requires_grad, self.device)
+        else:
+            self._node = None
+
+    # ------------------------------------------------------------ properties
+    @property
+    def op(self):
+        return self._node.op if self._node else OpEnum.LEAF
+
+    @property
+    def requires_grad(self) -> bool:
+        return self._node.requires_grad if self._node else False
+
+    @property
+    def shape(self):
+        return tuple(self._node.shape) if self._node else None
+
+    @property
+    def dtype(self) -> str | None:
+        return self._node.dtype if self._node else None
+
+    @property
+    def grad(self):
+        if self._node and self._node.grad:
+            return Tensor(_node=self._node.grad, device=self.device)
+        return None
+
+    # ------------------------------------------------------------- operators
+    def _ensure_tensor(self, other) -> "Tensor":
+        if isinstance(other, Tensor):
+            if self.device.type != other.device.type:
+                raise_device_mismatch(msg="Cannot mix devices in operation.", got=other.device.type)
+            return other
+        return Tensor(data=other, device=self.device)
+
+    def _binary(self, op, a: "Tensor", b: "Tensor") -> "Tensor":
+        return Tensor(_node=Node(op, [a._node, b._node], self.device), device=self.device)
+
+    def _unary(self, op) -> "Tensor":
+        return Tensor(_node=Node(op, [self._node], self.device), device=self.device)
+
+    def __add__(self, other):
+        return self._binary(OpEnum.ADD, self, self._ensure_tensor(other))
+
+    def __sub__(self, other):
+        return self._binary(OpEnum.SUB, self, self._ensure_tensor(other))
+
+    def __mul__(self, other):
+        return self._binary(OpEnum.MUL, self, self._ensure_tensor(other))
+
+    def __truediv__(self, other):
+        return self._binary(OpEnum.DIV, self, self._ensure_tensor(other))
+
+    def __pow__(self, power):
+        return self._binary(OpEnum.POW, self, self._ensure_tensor(power))
+
+    def __matmul__(self, other):
+        if not isinstance(other, Tensor):
+            raise TypeError("Matmul requires both operands to be Tensors.")
+        if self.device.type != other.device.type:
+            raise_device_mismatch(msg="Cannot perform MATMUL across different devices", got=other.device.type)
+        return self._binary(OpEnum.MATMUL, self, other)
+
+    def __neg__(self):
+        return self._unary(OpEnum.NEG)
+
+    def __radd__(self, other):
+        return self + other
+
+    def __rmul__(self, other):
+        return self * other
+
+    def __rsub__(self, other):
+        return self._binary(OpEnum.SUB, self._ensure_tensor(other), self)
+
+    def __rtruediv__(self, other):
+        return self._binary(OpEnum.DIV, self._ensure_tensor(other), self)
+
+    # ------------------------------------------------ element-wise (additive)
+    def exp(self):
+        return self._unary(OpEnum.EXP)
+
+    def log(self):
+        return self._unary(OpEnum.LOG)
+
+    def sin(self):
+        return self._unary(OpEnum.SIN)
+
+    def cos(self):
+        return self._unary(OpEnum.COS)
+
+    def relu(self):
+        return self._unary(OpEnum.RELU)
+
+    def tanh(self):
+        return self._unary(OpEnum.TANH)
+
+    def sigmoid(self):
+        return self._unary(OpEnum.SIGMOID)
+
+    def gelu(self):
+        return self._unary(OpEnum.GELU)
+
+    def astype(self, dtype: str) -> "Tensor":
+        return Tensor(_node=ormi_backend.cast(self._node, dtype), device=self.device)
+
+    # ---------------------------------------------------- reductions (additive)
+    @staticmethod
+    def _axes(axis) -> list[int]:
+        if axis is None:
+            return []
+        if isinstance(axis, int):
+            return [axis]
+        return list(axis)
+
+    def sum(self, axis=None, keepdims: bool = False) -> "Tensor":
+        return Tensor(_node=ormi_backend.sum(self._node, self._axes(axis), keepdims), device=self.device)
+
+    def max(self, axis=None, keepdims: bool = False) -> "Tensor":
+        return Tensor(_node=ormi_backend.max(self._node, self._axes(axis), keepdims), device=self.device)
+
+    def argmax(self, axis: int | None = None, keepdims: bool = False) -> "Tensor":
+        return Tensor(_node=ormi_backend.argmax(self._node, self._axes(axis), keepdims), device=self.device)
+
+    def mean(self, axis=None, keepdims: bool = False) -> "Tensor":
+        """sum * (1/N), N = number of reduced elements (exact scaling for powers of two)."""
+        axes = self._axes(axis)
+        shape = self.shape
+        reduced = range(len(shape)) if not axes else [a % len(shape) for a in axes]
+        n = 1
+        for a in set(reduced):
+            n *= shape[a]
+        return self.sum(axis, keepdims) * (1.0 / n)
+
+    # ------------------------------------------------------------------ views
+    def reshape(self, shape) -> "Tensor":
+        return Tensor(_node=ormi_backend.reshape(self._node, list(shape)), device=self.device)
+
+    def transpose(self, axes=None) -> "Tensor":
+        if axes is None:
+            axes = tuple(reversed(range(len(self.shape))))
+        return Tensor(_node=ormi_backend.transpose(self._node, list(axes)), device=self.device)
+
+    def expand(self, shape) -> "Tensor":
+        return Tensor(_node=ormi_backend.expand(self._node, list(shape)), device=self.device)
+
+    @property
+    def T(self) -> "Tensor":
+        return self.transpose()
+
+    # --------------------------------------------------------------- realize
+    def realize(self) -> "Tensor":
+        if self._node and self._node.is_realized:
+            return self
+        ormi_backend.execute_graph(self._node)
+        return self
+
+    def numpy(self) -> np.ndarray:
+        self.realize()
+        if not self._node or not self._node.is_realized:
+            raise RuntimeError("Cannot fetch an unrealized tensor.")
+        raw = ormi_backend.buffer_to_numpy(self._node.data)
+        byte_strides = tuple(s * raw.itemsize for s in self._node.view.strides)
+        return as_strided(raw, shape=self.shape, strides=byte_strides)
+
+    def backward(self):
+        if not self.requires_grad:
+            raise RuntimeError("Cannot call backward() on a tensor that does not require gradients.")
+        ormi_backend.compute_gradients(self._node)
+
+    def zero_grad(self):
+        if self._node:
+            self._node.grad = None
+
+    def zero_grad_graph(self):
+        if self._node:
+            ormi_backend.zero_grad_graph(self._node)
+
+    def __repr__(self):
+        state = "realized" if (self._node and self._node.is_realized) else "lazy"
+        return f"Tensor(op={self.op.name}, shape={self.shape}, state={state}, device={self.device.type.name})"

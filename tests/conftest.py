@@ -1,0 +1,69 @@
+"""Shared fixtures. `gpu` marks tests that need the MI355X (HIP device)."""
+import ctypes
+import re
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X GPU (the HIP device); run with -m gpu")
+
+
+@pytest.fixture(scope="session")
+def ob():
+    import ormi_amd
+
+    return ormi_amd.ormi_backend
+
+
+@pytest.fixture(scope="session")
+def cpu(ob):
+    """The CPU oracle device (test infrastructure)."""
+    import oracle
+
+    oracle.load()
+    return "cpu"
+
+
+@pytest.fixture(scope="session")
+def hip(ob):
+    """The HIP device. GPU tests fail (not skip) when it is missing, so a GPU run
+    that silently lost the device cannot pass."""
+    assert ob.hip_available(), "HIP device unavailable: these tests need the MI355X"
+    return "hip"
+
+
+@pytest.fixture(scope="session")
+def cabi():
+    """libormi_hip.so through ctypes, with argtypes from include/ormi_hip.h."""
+    lib = ctypes.CDLL(str(ROOT / "ormi_amd" / "lib" / "libormi_hip.so"))
+    lib.ormi_hip_last_error.restype = ctypes.c_char_p
+    for name in ["ormi_hip_malloc"]:
+        getattr(lib, name).argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
+    lib.ormi_hip_free.argtypes = [ctypes.c_void_p]
+    lib.ormi_hip_memcpy_h2d.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]
+    lib.ormi_hip_memcpy_d2h.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]
+    lib.ormi_hip_memcpy_d2d.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]
+    lib.ormi_hip_fill.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_size_t]
+    lib.ormi_hip_convert.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t]
+    lib.ormi_hip_rtc_compile_only.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p),
+                                              ctypes.c_int, ctypes.POINTER(ctypes.c_size_t)]
+    return lib
+
+
+def header_functions():
+    text = (ROOT / "include" / "ormi_hip.h").read_text()
+    return sorted(set(re.findall(r"\b(ormi_hip_\w+)\s*\(", text)))
+
+
+def fp32_sum_tolerance(x: np.ndarray, axis) -> np.ndarray:
+    """Bound for |fp32 sum (any order) - exact sum|: n * eps32 * sum|x| (Higham)."""
+    n = x.size if axis is None else np.prod([x.shape[a] for a in np.atleast_1d(axis)])
+    return n * np.finfo(np.float32).eps * np.abs(x.astype(np.float64)).sum(axis=axis)

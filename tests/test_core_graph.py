@@ -1,0 +1,188 @@
+"""Graph IR, shapes, strides, views and autograd structure (CPU only; no kernels run).
+
+Restates the reference's structural tests: csrc/tests/core/test_shape.cpp:25-99,
+test_node.cpp:59-91, ops/view/test_{transpose,reshape,expand}.cpp,
+ops/reduce/test_reduce.cpp:61-116, ops/blas/test_matmul.cpp:71-118,
+ops/pointwise/test_div.cpp:61-91, test_autograd.cpp:70-83.
+"""
+import numpy as np
+import pytest
+
+
+def leaf(ob, cpu, shape, fill=1.0, requires_grad=False):
+    buf = ob.numpy_to_buffer(np.full(shape, fill, np.float32), ob.DeviceEnum.CPU)
+    return ob.Node(buf, requires_grad, ob.Device(ob.DeviceEnum.CPU, 0))
+
+
+def test_contiguous_strides(ob):
+    assert ob.calc_contiguous_strides([2, 3, 4]) == [12, 4, 1]
+    assert ob.calc_contiguous_strides([5, 5]) == [5, 1]
+    assert ob.calc_contiguous_strides([10]) == [1]
+    assert ob.calc_contiguous_strides([]) == []
+
+
+def test_broadcast_shapes(ob):
+    assert ob.broadcast_shapes([2, 3], [2, 3]) == [2, 3]
+    assert ob.broadcast_shapes([2, 3], []) == [2, 3]
+    assert ob.broadcast_shapes([], [4, 5, 6]) == [4, 5, 6]
+    assert ob.broadcast_shapes([2, 3], [3]) == [2, 3]
+    assert ob.broadcast_shapes([2, 1, 4], [3, 4]) == [2, 3, 4]
+    assert ob.broadcast_shapes([1, 5, 1], [4, 1, 6]) == [4, 5, 6]
+    for a, b in ([2], [3]), ([2, 3], [2, 4]), ([3, 2], [2, 3]):
+        with pytest.raises(RuntimeError):
+            ob.broadcast_shapes(a, b)
+
+
+def test_binary_shape_and_requires_grad(ob, cpu):
+    a = leaf(ob, cpu, (2, 3), requires_grad=True)
+    b = leaf(ob, cpu, (3,))
+    c = ob.add(a, b)
+    assert c.shape == [2, 3] and c.strides == [3, 1]
+    assert c.requires_grad and not c.is_realized
+    with pytest.raises(RuntimeError):
+        ob.add(leaf(ob, cpu, (2,)), leaf(ob, cpu, (3,)))
+
+
+def test_transpose_view(ob, cpu):
+    a = leaf(ob, cpu, (2, 3, 4))
+    t = ob.transpose(a, [2, 0, 1])
+    assert t.shape == [4, 2, 3] and t.strides == [1, 12, 4]
+    with pytest.raises(RuntimeError):
+        ob.transpose(a, [0, 1])
+
+
+def test_reshape_view(ob, cpu):
+    a = leaf(ob, cpu, (2, 3, 4))
+    assert ob.reshape(a, [6, 4]).strides == [4, 1]
+    assert ob.reshape(a, [24]).strides == [1]
+    assert ob.reshape(a, [2, 12]).strides == [12, 1]
+    assert ob.reshape(ob.reshape(a, [24]), [1, 24]).strides == [24, 1]
+    with pytest.raises(RuntimeError):
+        ob.reshape(a, [5, 5])
+    # Non-contiguous merge cannot be a view.
+    with pytest.raises(RuntimeError):
+        ob.reshape(ob.transpose(a, [2, 1, 0]), [24])
+
+
+def test_expand_view(ob, cpu):
+    a = leaf(ob, cpu, (3, 1))
+    e = ob.expand(a, [2, 3, 4])
+    assert e.shape == [2, 3, 4] and e.strides == [0, 1, 0]
+    with pytest.raises(RuntimeError):
+        ob.expand(a, [2, 4, 4])
+
+
+def test_sum_shapes(ob, cpu):
+    a = leaf(ob, cpu, (2, 3, 4))
+    assert ob.sum(a, [], False).shape == []
+    assert ob.sum(a, [], True).shape == [1, 1, 1]
+    assert ob.sum(a, [1], False).shape == [2, 4]
+    assert ob.sum(a, [0, 2], True).shape == [1, 3, 1]
+    assert ob.sum(a, [-1], False).shape == [2, 3]
+    assert ob.argmax(a, [1], False).dtype == "int64"
+    with pytest.raises(RuntimeError):
+        ob.argmax(a, [0, 1], False)
+    with pytest.raises(RuntimeError):
+        ob.sum(a, [3], False)
+
+
+def test_matmul_shapes(ob, cpu):
+    assert ob.matmul(leaf(ob, cpu, (2, 3)), leaf(ob, cpu, (3, 4))).shape == [2, 4]
+    assert ob.matmul(leaf(ob, cpu, (5, 2, 3)), leaf(ob, cpu, (3, 4))).shape == [5, 2, 4]
+    assert ob.matmul(leaf(ob, cpu, (5, 1, 2, 3)), leaf(ob, cpu, (7, 3, 4))).shape == [5, 7, 2, 4]
+    with pytest.raises(RuntimeError):
+        ob.matmul(leaf(ob, cpu, (2, 3)), leaf(ob, cpu, (4, 4)))
+    with pytest.raises(RuntimeError):
+        ob.matmul(leaf(ob, cpu, (3,)), leaf(ob, cpu, (3, 4)))
+
+
+def test_sum_adjoint_structure(ob, cpu):
+    """SUM's gradient is RESHAPE -> EXPAND of the incoming gradient (reference sum.cpp:59-97)."""
+    x = leaf(ob, cpu, (2, 3), requires_grad=True)
+    s = ob.sum(x, [1], False)
+    total = ob.sum(s, [], False)
+    ob.compute_gradients(total)
+    g = x.grad
+    # The seed is a 0-d ones buffer, so both axes end up broadcast (stride 0).
+    assert g.op == ob.OpEnum.EXPAND and g.shape == [2, 3] and g.strides == [0, 0]
+    assert g.parents[0].op == ob.OpEnum.RESHAPE and g.parents[0].shape == [2, 1]
+
+
+def test_matmul_adjoint_structure(ob, cpu):
+    """dX = dZ.Y^T, dY = X^T.dZ through TRANSPOSE views (reference matmul.cpp:71-135)."""
+    x = leaf(ob, cpu, (2, 3), requires_grad=True)
+    y = leaf(ob, cpu, (3, 4), requires_grad=True)
+    z = ob.matmul(x, y)
+    ob.compute_gradients(ob.sum(z, [], False))
+    gx, gy = x.grad, y.grad
+    assert gx.op == ob.OpEnum.MATMUL and gx.shape == [2, 3]
+    assert gx.parents[1].op == ob.OpEnum.TRANSPOSE and gx.parents[1].strides == [1, 4]
+    assert gy.op == ob.OpEnum.MATMUL and gy.shape == [3, 4]
+    assert gy.parents[0].op == ob.OpEnum.TRANSPOSE and gy.parents[0].strides == [1, 3]
+
+
+def test_broadcast_adjoint_unbroadcasts(ob, cpu):
+    a = leaf(ob, cpu, (4, 3), requires_grad=True)
+    b = leaf(ob, cpu, (3,), requires_grad=True)
+    c = ob.add(a, b)
+    ob.compute_gradients(ob.sum(c, [], False))
+    assert b.grad.op == ob.OpEnum.SUM and b.grad.shape == [3]
+    assert a.grad.shape == [4, 3]
+
+
+def test_div_adjoint_structure(ob, cpu):
+    """dY = -(dZ * (X / (Y*Y))) (reference test_div.cpp:61-91)."""
+    x = leaf(ob, cpu, (2,), requires_grad=True)
+    y = leaf(ob, cpu, (2,), requires_grad=True)
+    ob.compute_gradients(ob.div(x, y))
+    assert x.grad.op == ob.OpEnum.DIV
+    gy = y.grad
+    assert gy.op == ob.OpEnum.NEG
+    assert gy.parents[0].op == ob.OpEnum.MUL
+    q = gy.parents[0].parents[1]
+    assert q.op == ob.OpEnum.DIV and q.parents[1].op == ob.OpEnum.MUL
+
+
+def test_activation_adjoints_use_derivative_ops(ob, cpu):
+    x = leaf(ob, cpu, (3,), requires_grad=True)
+    for op, fn, dop in [("relu", ob.relu, ob.OpEnum.STEP), ("tanh", ob.tanh, ob.OpEnum.TANH_GRAD),
+                        ("sigmoid", ob.sigmoid, ob.OpEnum.SIGMOID_GRAD), ("gelu", ob.gelu, ob.OpEnum.GELU_GRAD)]:
+        x.grad = None
+        ob.compute_gradients(fn(x))
+        assert x.grad.op == ob.OpEnum.MUL, op
+        assert x.grad.parents[1].op == dop, op
+
+
+def test_missing_adjoint_raises(ob, cpu):
+    x = leaf(ob, cpu, (3,), requires_grad=True)
+    y = ob.step(ob.relu(x))  # STEP carries no gradient: requires_grad is False
+    assert not y.requires_grad
+    z = ob.mul(ob.relu(x), ob.Node(ob.OpEnum.TANH_GRAD, [x], x.device))
+    with pytest.raises(RuntimeError, match="No Adjoint rule"):
+        ob.compute_gradients(z)
+
+
+def test_zero_grad_graph(ob, cpu):
+    a = leaf(ob, cpu, (2,), requires_grad=True)
+    b = ob.mul(a, a)
+    ob.compute_gradients(b)
+    assert a.grad is not None
+    ob.zero_grad_graph(b)
+    assert a.grad is None and b.grad is None
+
+
+def test_deep_graph_no_recursion_limit(ob, cpu):
+    """Topological walks are iterative: a 20000-deep chain builds gradients and realizes."""
+    x = leaf(ob, cpu, (2,), 0.5, requires_grad=True)
+    y = x
+    for _ in range(20000):
+        y = ob.neg(y)
+    ob.compute_gradients(y)
+    assert x.grad is not None
+    ob.execute_graph(y)
+    assert np.allclose(ob.buffer_to_numpy(y.data), 0.5)
+
+
+def test_unknown_device_errors(ob):
+    with pytest.raises(RuntimeError, match="no CUDA backend"):
+        ob.numpy_to_buffer(np.zeros(2, np.float32), ob.DeviceEnum.CUDA)

@@ -1,0 +1,390 @@
+"""HIP device parity against the CPU oracle (and float64 closed forms at full size).
+
+Tolerances (from the north star): bit-exact for argmax and max, rtol 1e-6 for
+fp32 pointwise (atol 1e-6 floor for values near 0, where a 1-ulp transcendental
+difference dominates), rtol 1e-5 for fp32 reductions (atol from the summation
+error bound), rtol 2e-2 for bf16 GEMM (reference computed from the bf16-rounded
+inputs; atol 1e-3 of the output scale).
+"""
+import math
+
+import numpy as np
+import pytest
+
+from conftest import fp32_sum_tolerance
+
+pytestmark = pytest.mark.gpu
+
+
+def T(data, dev, **kw):
+    from ormi_amd import Tensor
+
+    return Tensor(data, device=dev, **kw)
+
+
+def both(x, **kw):
+    return T(x, "cpu", **kw), T(x, "hip", **kw)
+
+
+def assert_bits_equal(a, b):
+    assert a.dtype == b.dtype and a.shape == b.shape
+    assert np.array_equal(np.ascontiguousarray(a).view(np.uint8), np.ascontiguousarray(b).view(np.uint8))
+
+
+# ----------------------------------------------------------------- KATs on HIP
+def test_reference_kats_on_hip(cpu, hip):
+    a, b = T([4.0, 6.0], hip), T([2.0, 3.0], hip)
+    assert (a + b).numpy().tolist() == [6, 9]
+    assert (a - b).numpy().tolist() == [2, 3]
+    assert (a * b).numpy().tolist() == [8, 18]
+    assert (a / b).numpy().tolist() == [2, 2]
+    assert (-a).numpy().tolist() == [-4, -6]
+    assert (a ** 2.0).numpy().tolist() == [16, 36]
+    a = T([2.0, 4.0], hip)
+    assert (10.0 - a).numpy().tolist() == [8, 6]
+    assert (10.0 / a).numpy().tolist() == [5, 2.5]
+    m = T([[1.0, 2.0], [3.0, 4.0]], hip) @ T([[2.0, 0.0], [0.0, 2.0]], hip)
+    assert m.numpy().tolist() == [[2, 4], [6, 8]]
+    x = T([[1.0, 2.0, 3.0], [4.0, 5.0, 6.0]], hip)
+    assert x.reshape((3, 2)).numpy().tolist() == [[1, 2], [3, 4], [5, 6]]
+    assert x.transpose().numpy().tolist() == [[1, 4], [2, 5], [3, 6]]
+    assert x.sum().numpy() == 21.0 and x.sum(1).numpy().tolist() == [6, 15]
+    assert x.sum(0, keepdims=True).numpy().tolist() == [[5, 7, 9]]
+    cube = T(np.arange(1, 9, dtype=np.float32).reshape(2, 2, 2), hip)
+    assert cube.sum((0, 2)).numpy().tolist() == [14, 22]
+    a, b = T([2.0, 3.0], hip, requires_grad=True), T([4.0, 5.0], hip, requires_grad=True)
+    ((a * b) + a).backward()
+    assert a.grad.numpy().tolist() == [5, 6] and b.grad.numpy().tolist() == [2, 3]
+    s = T(np.full(2, 1.570796327, np.float32), hip).sin().numpy()
+    assert np.allclose(s, 1.0, atol=1e-5)
+
+
+def test_matmul_kats_on_hip(ob, hip):
+    def view(vals, shape, strides):
+        buf = ob.numpy_to_buffer(np.array(vals, np.float32), ob.DeviceEnum.HIP)
+        n = ob.Node(buf, False, ob.Device(ob.DeviceEnum.HIP, 0))
+        n.view = ob.TensorView(list(shape), list(strides))
+        return n
+
+    def run(a, b):
+        c = ob.matmul(a, b)
+        ob.execute_graph(c)
+        return ob.buffer_to_numpy(c.data).reshape(-1).tolist()
+
+    assert run(view([1, 2, 3, 4, 5, 6], [2, 3], [3, 1]), view([7, 8, 9, 10, 11, 12], [3, 2], [2, 1])) == [58, 64, 139, 154]
+    assert run(view([1, 2, 3, 4, 5, 6], [3, 2], [1, 3]), view([1, 2, 3, 4], [2, 2], [2, 1])) == [13, 18, 17, 24, 21, 30]
+    assert run(view(list(range(1, 13)), [2, 2, 3], [6, 3, 1]), view([1, 2, 3, 4, 5, 6], [2, 3, 2], [0, 2, 1])) == \
+        [22, 28, 49, 64, 76, 100, 103, 136]
+
+
+def test_fusion_contract(ob, hip):
+    """HIP realizes a pointwise chain as one kernel: interior nodes stay unrealized
+    (the reference's CPU order realizes them, csrc/tests/backend/test_runtime.cpp:42)."""
+    a, b, c = (T(np.full((2, 2), v, np.float32), hip) for v in (2.0, 3.0, 4.0))
+    ab = a + b
+    d = ab * c
+    d.realize()
+    assert d._node.is_realized and not ab._node.is_realized
+    assert d.numpy().tolist() == [[20, 20], [20, 20]]
+    v = T(np.ones((2, 3, 4), np.float32), hip)
+    r = v.reshape((6, 4)).realize()
+    assert r._node.data.ptr == v._node.data.ptr  # zero-copy view
+
+
+# ------------------------------------------------------- config 2: broadcast chain
+def c2_inputs(rows, cols, seed=1):
+    rng = np.random.default_rng(seed)
+    x = rng.normal(0, 1, (rows, cols)).astype(np.float32)
+    bias = rng.normal(0, 0.1, (cols,)).astype(np.float32)
+    scale = rng.uniform(0.5, 1.5, (rows, 1)).astype(np.float32)
+    return x, bias, scale
+
+
+def c2(dev, x, bias, scale):
+    X, B, S = T(x, dev), T(bias, dev), T(scale, dev)
+    return ((X + B) * S).tanh() * X.sigmoid() - 0.1 * X * X
+
+
+@pytest.mark.parametrize("shape", [(64, 128), (37, 129), (1, 4), (3, 1), (256, 4100)])
+def test_c2_parity_small(cpu, hip, shape):
+    x, bias, scale = c2_inputs(*shape)
+    got = c2(hip, x, bias, scale).numpy()
+    want = c2(cpu, x, bias, scale).numpy()
+    np.testing.assert_allclose(got, want, rtol=1e-6, atol=1e-6)
+
+
+def test_c2_full_size(cpu, hip):
+    """(8192, 4096): GPU vs the oracle's fused tape on the same inputs."""
+    x, bias, scale = c2_inputs(8192, 4096)
+    got = c2(hip, x, bias, scale).numpy()
+    want_t = c2(cpu, x, bias, scale)
+    from ormi_amd import ormi_backend as ob
+
+    ob.execute_jit(want_t._node)  # one tape over the whole chain (faster than per-node)
+    want = want_t.numpy()
+    np.testing.assert_allclose(got, want, rtol=1e-6, atol=1e-6)
+
+
+def test_pointwise_ops_match_oracle(cpu, hip):
+    rng = np.random.default_rng(21)
+    a = rng.uniform(-3, 3, (33, 65)).astype(np.float32)
+    b = rng.uniform(0.5, 2, (65,)).astype(np.float32)
+    for name in ("exp", "sin", "cos", "tanh", "sigmoid", "gelu", "relu"):
+        got = getattr(T(a, hip), name)().numpy()
+        want = getattr(T(a, cpu), name)().numpy()
+        np.testing.assert_allclose(got, want, rtol=1e-6, atol=1e-6, err_msg=name)
+    for dev_pair in [(hip, cpu)]:
+        outs = [((T(a, d) * T(a, d) + T(b, d)) / T(b, d) - T(a, d)).numpy() for d in dev_pair]
+        assert_bits_equal(outs[0], outs[1])  # + - * / without contraction: bit-exact
+        outs = [(T(np.abs(a) + 0.1, d).log() + T(b, d) ** T(a, d)).numpy() for d in dev_pair]
+        np.testing.assert_allclose(outs[0], outs[1], rtol=2e-6, atol=1e-6)
+
+
+def test_views_and_strides_as_leaves(cpu, hip):
+    rng = np.random.default_rng(22)
+    x = rng.standard_normal((16, 24)).astype(np.float32)
+    y = rng.standard_normal((24, 16)).astype(np.float32)
+    got = (T(x, hip).transpose() * T(y, hip) + T(x, hip).reshape((24, 16))).numpy()
+    want = (T(x, cpu).transpose() * T(y, cpu) + T(x, cpu).reshape((24, 16))).numpy()
+    assert_bits_equal(got, want)
+    e_h = T(x[:1], hip).expand((16, 24)) * T(x, hip)
+    e_c = T(x[:1], cpu).expand((16, 24)) * T(x, cpu)
+    assert_bits_equal(e_h.numpy(), e_c.numpy())
+
+
+def test_bf16_leaves_and_casts(cpu, hip):
+    rng = np.random.default_rng(23)
+    x = rng.standard_normal((40, 64)).astype(np.float32)
+    got = (T(x, hip, dtype="bfloat16") * 2.0 + 1.0).numpy()
+    want = (T(x, cpu, dtype="bfloat16") * 2.0 + 1.0).numpy()
+    assert_bits_equal(got, want)
+    got = T(x, hip).astype("bfloat16").numpy()
+    want = T(x, cpu).astype("bfloat16").numpy()
+    assert_bits_equal(got, want)
+
+
+# ---------------------------------------------------------- config 3: reductions
+@pytest.fixture(scope="module")
+def c3():
+    return np.random.default_rng(2).normal(0, 2, (16384, 8192)).astype(np.float32)
+
+
+def test_c3_row_max_and_argmax_bit_exact(cpu, hip, c3):
+    xh, xc = T(c3, hip), T(c3, cpu)
+    assert_bits_equal(xh.max(1).numpy(), xc.max(1).numpy())
+    am = xh.argmax(1).numpy()
+    assert am.dtype == np.int64
+    assert_bits_equal(am, xc.argmax(1).numpy())
+    assert np.array_equal(am, np.argmax(c3, axis=1))
+
+
+def test_c3_row_sum_mean(cpu, hip, c3):
+    xh, xc = T(c3, hip), T(c3, cpu)
+    exact = c3.astype(np.float64).sum(axis=1)
+    got = xh.sum(1).numpy()
+    want = xc.sum(1).numpy()
+    bound = fp32_sum_tolerance(c3, 1)
+    assert np.all(np.abs(got - exact) <= bound)
+    atol = 4 * np.finfo(np.float32).eps * np.sqrt(8192) * np.sqrt((c3.astype(np.float64) ** 2).sum(1))
+    assert np.all(np.abs(got - want) <= 1e-5 * np.abs(want) + atol)
+    mean_h = xh.mean(1).numpy()
+    assert np.all(np.abs(mean_h - got / 8192) <= 1e-7 * np.abs(got / 8192))  # 1/8192 scaling is exact
+
+
+def test_c3_softmax_denominator(cpu, hip, c3):
+    def sumexp(dev):
+        x = T(c3, dev)
+        return (x - x.max(1, keepdims=True)).exp().sum(1).numpy()
+
+    got, want = sumexp(hip), sumexp(cpu)
+    np.testing.assert_allclose(got, want, rtol=1e-5)
+
+
+def test_c3_column_sum(cpu, hip, c3):
+    got = T(c3, hip).sum(0).numpy()
+    want = T(c3, cpu).sum(0).numpy()
+    exact = c3.astype(np.float64).sum(axis=0)
+    assert np.all(np.abs(got - exact) <= fp32_sum_tolerance(c3, 0))
+    atol = 4 * np.finfo(np.float32).eps * np.sqrt(16384) * np.sqrt((c3.astype(np.float64) ** 2).sum(0))
+    assert np.all(np.abs(got - want) <= 1e-5 * np.abs(want) + atol)
+
+
+@pytest.mark.parametrize("shape,axes", [
+    ((7, 5), (0,)), ((7, 5), (1,)), ((7, 5), None), ((3, 4, 5), (0, 2)), ((3, 4, 5), (1,)),
+    ((2, 3, 4, 5), (1, 2)), ((1, 1000003), (1,)), ((1000003,), None), ((513, 3), (0,)), ((5, 1, 7), (1,)),
+])
+def test_reduction_shapes(cpu, hip, shape, axes):
+    rng = np.random.default_rng(24)
+    x = rng.integers(-8, 8, shape).astype(np.float32)  # small ints: sums are exact in fp32
+    for name in ("sum", "max"):
+        got = getattr(T(x, hip), name)(axes).numpy()
+        want = getattr(T(x, cpu), name)(axes).numpy()
+        assert_bits_equal(got, want)
+    if axes is None or len(axes) == 1:
+        ax = None if axes is None else axes[0]
+        assert np.array_equal(T(x, hip).argmax(ax).numpy(), np.argmax(x, axis=ax))
+
+
+def test_argmax_ties_and_nan(cpu, hip):
+    x = np.zeros((4, 300), np.float32)
+    x[0, 7] = x[0, 250] = 5.0
+    x[1, :] = -np.inf
+    x[2, 100] = np.nan
+    x[2, 200] = np.nan
+    x[3, 0] = -0.0
+    for axis in (0, 1):
+        got = T(x, hip).argmax(axis).numpy()
+        want = T(x, cpu).argmax(axis).numpy()
+        assert np.array_equal(got, want)
+    assert np.array_equal(T(x, hip).argmax(1).numpy(), np.argmax(x, axis=1))
+    assert_bits_equal(T(x, hip).max(1).numpy(), T(x, cpu).max(1).numpy())
+
+
+# ------------------------------------------ config 1: fused pointwise + row sum
+def c1_graph(dev, a, b, c):
+    A, B, C = T(a, dev, requires_grad=True), T(b, dev, requires_grad=True), T(c, dev, requires_grad=True)
+    y = ((A * B + C).relu() * 0.5).sum(1)
+    return A, B, C, y
+
+
+def test_c1_forward_backward(cpu, hip):
+    rng = np.random.default_rng(0)
+    a, b, c = (rng.uniform(-1, 1, (1024, 1024)).astype(np.float32) for _ in range(3))
+    Ah, Bh, Ch, yh = c1_graph(hip, a, b, c)
+    Ac, Bc, Cc, yc = c1_graph(cpu, a, b, c)
+    got, want = yh.numpy(), yc.numpy()
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5)
+    yh.sum().backward()
+    yc.sum().backward()
+    for gh, gc in ((Ah.grad, Ac.grad), (Bh.grad, Bc.grad), (Ch.grad, Cc.grad)):
+        assert_bits_equal(gh.numpy(), gc.numpy())  # products of exact values and a mask
+
+
+# ---------------------------------------------------------------- config 4: GEMM
+def gemm_ref64(a, b):
+    return a.astype(np.float64) @ b.astype(np.float64)
+
+
+def bf16_round(x):
+    u = x.astype(np.float32).view(np.uint32).astype(np.uint64)
+    return (((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16).astype(np.uint32).view(np.float32)
+
+
+@pytest.mark.parametrize("m,k,n", [(64, 64, 64), (256, 256, 256), (300, 200, 100), (33, 17, 9), (512, 1024, 768)])
+def test_fp32_gemm_vs_oracle(cpu, hip, m, k, n):
+    rng = np.random.default_rng(31)
+    a = rng.normal(0, 1 / 8, (m, k)).astype(np.float32)
+    b = rng.normal(0, 1 / 8, (k, n)).astype(np.float32)
+    got = (T(a, hip) @ T(b, hip)).numpy()
+    want = (T(a, cpu) @ T(b, cpu)).numpy()
+    bound = 2 * k * np.finfo(np.float32).eps * (np.abs(a).astype(np.float64) @ np.abs(b))
+    assert np.all(np.abs(got - want) <= bound)
+    assert np.all(np.abs(got - gemm_ref64(a, b)) <= bound)
+
+
+@pytest.mark.parametrize("m,k,n", [(256, 256, 256), (512, 512, 512), (300, 200, 104), (1024, 64, 2048)])
+def test_bf16_gemm_vs_oracle(cpu, hip, m, k, n):
+    rng = np.random.default_rng(32)
+    a = rng.normal(0, 1 / 64, (m, k)).astype(np.float32)
+    b = rng.normal(0, 1 / 64, (k, n)).astype(np.float32)
+    got = (T(a, hip, dtype="bfloat16") @ T(b, hip, dtype="bfloat16")).numpy()
+    want = (T(a, cpu, dtype="bfloat16") @ T(b, cpu, dtype="bfloat16")).numpy()
+    scale = np.abs(want).max()
+    np.testing.assert_allclose(got, want, rtol=2e-2, atol=1e-3 * scale)
+    exact = gemm_ref64(bf16_round(a), bf16_round(b))
+    bound = 2 * k * np.finfo(np.float32).eps * (np.abs(bf16_round(a)).astype(np.float64) @ np.abs(bf16_round(b)))
+    assert np.all(np.abs(got - exact) <= bound)
+
+
+def test_gemm_transposed_layouts(cpu, hip):
+    """NN, NT, TN, TT through transpose views: the layouts of the forward and the two
+    backward GEMMs (reference csrc/core/ops/blas/matmul.cpp:86-124)."""
+    rng = np.random.default_rng(33)
+    a = rng.standard_normal((320, 192)).astype(np.float32)
+    b = rng.standard_normal((192, 448)).astype(np.float32)
+    exact = gemm_ref64(a, b)
+    bound = 2 * 192 * np.finfo(np.float32).eps * (np.abs(a).astype(np.float64) @ np.abs(b))
+    for dt in ("float32", "bfloat16"):
+        if dt == "bfloat16":
+            ar, br = bf16_round(a), bf16_round(b)
+            ex = gemm_ref64(ar, br)
+            bd = 2 * 192 * np.finfo(np.float32).eps * (np.abs(ar).astype(np.float64) @ np.abs(br))
+        else:
+            ex, bd = exact, bound
+        A_n, B_n = T(a, hip, dtype=dt), T(b, hip, dtype=dt)
+        A_t, B_t = T(a.T.copy(), hip, dtype=dt).transpose(), T(b.T.copy(), hip, dtype=dt).transpose()
+        for A, B in ((A_n, B_n), (A_n, B_t), (A_t, B_n), (A_t, B_t)):
+            got = (A @ B).numpy()
+            assert np.all(np.abs(got - ex) <= bd), dt
+
+
+def test_gemm_batched_broadcast(cpu, hip):
+    rng = np.random.default_rng(34)
+    a = rng.standard_normal((3, 2, 64, 96)).astype(np.float32)
+    b = rng.standard_normal((2, 96, 32)).astype(np.float32)
+    got = (T(a, hip) @ T(b, hip)).numpy()
+    want = (T(a, cpu) @ T(b, cpu)).numpy()
+    np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-4)
+
+
+def test_c4_bf16_4096_sampled(hip):
+    """Full config: A, B ~ N(0, 1/64) in bf16, fp32 out; 2048 sampled entries vs float64."""
+    rng = np.random.default_rng(3)
+    a = rng.normal(0, 1 / 64, (4096, 4096)).astype(np.float32)
+    b = rng.normal(0, 1 / 64, (4096, 4096)).astype(np.float32)
+    got = (T(a, hip, dtype="bfloat16") @ T(b, hip, dtype="bfloat16")).numpy()
+    ar, br = bf16_round(a).astype(np.float64), bf16_round(b).astype(np.float64)
+    idx = rng.integers(0, 4096, (2048, 2))
+    exact = np.einsum("ij,ji->i", ar[idx[:, 0]], br[:, idx[:, 1]])
+    scale = np.abs(exact).max()
+    np.testing.assert_allclose(got[idx[:, 0], idx[:, 1]], exact, rtol=2e-2, atol=1e-3 * scale)
+    bound = 2 * 4096 * np.finfo(np.float32).eps * np.einsum("ij,ji->i", np.abs(ar[idx[:, 0]]), np.abs(br[:, idx[:, 1]]))
+    assert np.all(np.abs(got[idx[:, 0], idx[:, 1]] - exact) <= bound)
+
+
+def test_c4_fp32_forward_and_backward(cpu, hip):
+    """(2048,1024)x(1024,4096) and dA = dC.B^T, dB = A^T.dC via autograd, vs float64."""
+    rng = np.random.default_rng(3)
+    a = rng.normal(0, 1 / 64, (2048, 1024)).astype(np.float32)
+    b = rng.normal(0, 1 / 64, (1024, 4096)).astype(np.float32)
+    dc = rng.normal(0, 1, (2048, 4096)).astype(np.float32)
+    A, B = T(a, hip, requires_grad=True), T(b, hip, requires_grad=True)
+    C = A @ B
+    np.testing.assert_allclose(C.numpy(), gemm_ref64(a, b), rtol=1e-4, atol=1e-6)
+    (C * T(dc, hip)).sum().backward()
+    ga = A.grad.numpy()
+    gb = B.grad.numpy()
+    ea = dc.astype(np.float64) @ b.T.astype(np.float64)
+    eb = a.T.astype(np.float64) @ dc.astype(np.float64)
+    bound_a = 2 * 4096 * np.finfo(np.float32).eps * (np.abs(dc).astype(np.float64) @ np.abs(b.T))
+    bound_b = 2 * 2048 * np.finfo(np.float32).eps * (np.abs(a.T).astype(np.float64) @ np.abs(dc))
+    assert np.all(np.abs(ga - ea) <= bound_a)
+    assert np.all(np.abs(gb - eb) <= bound_b)
+
+
+# ------------------------------------------------------------- config 5: MLP step
+def mlp_step(dev, X, Yt, Ws, lr=1e-3):
+    ws = [T(w, dev, requires_grad=True) for w in Ws]
+    h = T(X, dev)
+    for i, w in enumerate(ws):
+        h = h @ w
+        if i < len(ws) - 1:
+            h = h.gelu()
+    d = h - T(Yt, dev)
+    loss = (d * d).sum() * (1.0 / (X.shape[0] * Yt.shape[1]))
+    loss.backward()
+    new = [(w - w.grad * lr).numpy() for w in ws]
+    return loss.numpy(), new
+
+
+def test_mlp_step_small_vs_oracle(cpu, hip):
+    rng = np.random.default_rng(4)
+    dims = [64, 256, 256, 64]
+    X = rng.normal(0, 1, (128, dims[0])).astype(np.float32)
+    Yt = rng.normal(0, 1, (128, dims[-1])).astype(np.float32)
+    Ws = [rng.uniform(-math.sqrt(6 / i), math.sqrt(6 / i), (i, o)).astype(np.float32) for i, o in zip(dims, dims[1:])]
+    lh, wh = mlp_step(hip, X, Yt, Ws)
+    lc, wc = mlp_step(cpu, X, Yt, Ws)
+    np.testing.assert_allclose(lh, lc, rtol=1e-5)
+    for a, b in zip(wh, wc):
+        np.testing.assert_allclose(a, b, rtol=1e-5, atol=1e-6)
