@@ -6,7 +6,8 @@
 // those, sizes and strides are kernel arguments (never literals), so a kernel is
 // reused for every tensor with the same structure; the source only encodes the
 // tape, operand dtypes, which strides are 0 or 1, the vector width and the
-// index width.
+// index width. A structural signature of exactly those choices keys a cache of
+// generated kernels, so a repeat launch builds its argument list and nothing else.
 //
 // Index space. The kernel's logical shape is canonicalized first: size-1 dims are
 // dropped and neighbouring dims merged wherever every operand (and the output)
@@ -18,13 +19,16 @@
 //              sized for the chip's compute units.
 //   * row:     I empty. One wave64 per (row, part): lanes stride the row with
 //              128-bit loads, then a DPP/cross-lane wave reduction.
-//   * column:  I non-empty. 64 lanes along I (128-bit loads), 4 waves split R;
-//              the 4 partials are combined through LDS.
+//   * column:  I non-empty. 64 lanes along I (128-bit loads), W waves split R;
+//              the W partials are combined through LDS in wave order.
 // When O (or O x I) is too small to fill 256 CUs, R is split into parts whose
 // partial results go to a workspace, and a second kernel combines them in part
 // order (two-pass; deterministic, no atomics).
 #include <algorithm>
+#include <cstdlib>
+#include <mutex>
 #include <sstream>
+#include <unordered_map>
 
 #include "backend/hip/hip_backend.h"
 
@@ -36,9 +40,32 @@ namespace ormi::hip {
         ;
 
     const std::vector<std::string>& rtc_options() {
+        // Packed-FP32 instructions stay disabled in generated code as in every
+        // hipcc-built translation unit.
         static const std::vector<std::string> opts = {"-O3", "-std=c++17", "-ffp-contract=off",
-                                                      "-fhip-fp32-correctly-rounded-divide-sqrt"};
+                                                      "-fhip-fp32-correctly-rounded-divide-sqrt",
+                                                      "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
         return opts;
+    }
+
+    static int env_int(const char* name, int dflt) {
+        const char* v = std::getenv(name);
+        return v && *v ? std::atoi(v) : dflt;
+    }
+
+    const Tuning& tuning() {
+        static const Tuning t = [] {
+            Tuning x;
+            x.map_unroll = std::clamp(env_int("ORMI_MAP_UNROLL", x.map_unroll), 1, 8);
+            x.map_blocks_per_cu = std::clamp(env_int("ORMI_MAP_BLOCKS_PER_CU", x.map_blocks_per_cu), 1, 1024);
+            x.row_unroll = std::clamp(env_int("ORMI_ROW_UNROLL", x.row_unroll), 1, 8);
+            x.col_waves = std::clamp(env_int("ORMI_COL_WAVES", x.col_waves), 1, 16);
+            x.map_nt_loads = env_int("ORMI_MAP_NT_LOADS", x.map_nt_loads) != 0;
+            x.reduce_nt_loads = env_int("ORMI_REDUCE_NT_LOADS", x.reduce_nt_loads) != 0;
+            x.map_nt_stores = env_int("ORMI_MAP_NT_STORES", x.map_nt_stores) != 0;
+            return x;
+        }();
+        return t;
     }
 
     FastDiv make_fastdiv(uint32_t d) {
@@ -51,9 +78,6 @@ namespace ormi::hip {
     }
 
     namespace {
-        constexpr int kBlock = 256;
-        constexpr int kUnroll = 4;
-
         const char* storage_type(DType t) {
             switch (t) {
                 case DType::Float32: return "float";
@@ -64,8 +88,6 @@ namespace ormi::hip {
             }
             return "float";
         }
-
-        size_t esize(DType t) { return dtype_size(t); }
 
         bool vector_dtype(DType t) { return t == DType::Float32 || t == DType::BFloat16 || t == DType::Float16; }
 
@@ -167,6 +189,7 @@ namespace ormi::hip {
             bool idx32 = true;
             int vec = 1;
             int vec_dim = -1;  // dim whose coordinate advances by VEC
+            bool nt_loads = false;
             ArgList args;
             std::ostringstream body;
 
@@ -184,7 +207,7 @@ namespace ormi::hip {
                 if (s != 1 || !vector_dtype(e.leaves[L].dtype)) return false;
                 for (size_t k = 0; k < c.dims.size(); ++k)
                     if ((int)k != d && c.st[L][k] % 4 != 0) return false;
-                return ((uintptr_t)e.leaves[L].ptr % (4 * esize(e.leaves[L].dtype))) == 0;
+                return ((uintptr_t)e.leaves[L].ptr % (4 * dtype_size(e.leaves[L].dtype))) == 0;
             }
 
             void choose_vec(int d) {
@@ -196,6 +219,8 @@ namespace ormi::hip {
                 vec = 4;
             }
 
+            // 32-bit index arithmetic when every index the kernel forms (element
+            // counts, operand offsets, the cursor bound extra_extent) fits.
             void choose_idx(long long extra_extent) {
                 const long long lim = (1ll << 31) - 1;
                 long long numel = 1;
@@ -269,7 +294,7 @@ namespace ormi::hip {
                 for (int d : dims) o << ind << idx() << " c" << d << " = 0;\n";
             }
 
-            // "off" expression of leaf L over `dims`, empty when all terms vanish.
+            // Offset expression of leaf L over `dims`, empty when all terms vanish.
             std::string offset(size_t L, const std::vector<int>& dims) const {
                 std::string s;
                 for (int d : dims) {
@@ -280,22 +305,22 @@ namespace ormi::hip {
                 return s;
             }
 
-            // Load leaf L at element offset `off` into x<L><sfx>[0..vec).
+            // Load leaf L at element offset `off` into dst[0..vec).
             void load_leaf(std::ostringstream& o, const std::string& ind, size_t L, const std::string& off, const std::string& dst) {
                 const DType dt = e.leaves[L].dtype;
                 const std::string p = "L" + std::to_string(L);
                 if (scalar[L]) return;  // hoisted
                 const bool unit = vec > 1 && c.st[L][vec_dim] == 1;
+                const bool nt = nt_loads;
                 if (unit) {
-                    if (dt == DType::Float32) {
-                        o << ind << "{ const ormi_f4 v_ = *(const ormi_f4*)(" << p << " + (" << off << "));";
-                        for (int k = 0; k < vec; ++k) o << " " << dst << "[" << k << "] = v_[" << k << "];";
-                        o << " }\n";
-                    } else {
-                        o << ind << "{ const ormi_u16x4 v_ = *(const ormi_u16x4*)(" << p << " + (" << off << "));";
-                        for (int k = 0; k < vec; ++k) o << " " << dst << "[" << k << "] = " << to_f32(dt, "v_[" + std::to_string(k) + "]") << ";";
-                        o << " }\n";
+                    const char* vt = dt == DType::Float32 ? "ormi_f4" : "ormi_u16x4";
+                    const std::string addr = std::string("(const ") + vt + "*)(" + p + " + (" + off + "))";
+                    o << ind << "{ const " << vt << " v_ = " << (nt ? "__builtin_nontemporal_load(" + addr + ")" : "*" + addr) << ";";
+                    for (int k = 0; k < vec; ++k) {
+                        const std::string ek = "v_[" + std::to_string(k) + "]";
+                        o << " " << dst << "[" << k << "] = " << (dt == DType::Float32 ? ek : to_f32(dt, ek)) << ";";
                     }
+                    o << " }\n";
                 } else {
                     o << ind << "{ const float v_ = " << to_f32(dt, p + "[" + off + "]") << ";";
                     for (int k = 0; k < vec; ++k) o << " " << dst << "[" << k << "] = v_;";
@@ -339,15 +364,14 @@ namespace ormi::hip {
                     if (!scalar[L]) o << ind << "float x" << L << "[" << unroll << "][" << vec << "];\n";
             }
 
-            std::string finish(const std::string& kind, const std::string& kernel_body, KernelLaunch& k) {
+            std::string finish(const std::string& kind, int block, KernelLaunch& k) {
                 std::ostringstream sig;
                 for (size_t i = 0; i < args.decls.size(); ++i) sig << (i ? ",\n    " : "    ") << args.decls[i];
-                const std::string tag = hex_hash(kernel_body + sig.str());
-                k.name = "ormi_" + kind + "_" + tag;
+                const std::string kernel_body = body.str();
+                k.name = "ormi_" + kind + "_" + hex_hash(kernel_body + sig.str());
                 std::ostringstream src;
-                src << kDeviceHeader << "\n\nextern \"C\" __global__ __launch_bounds__(" << kBlock << ") void " << k.name << "(\n"
+                src << kDeviceHeader << "\n\nextern \"C\" __global__ __launch_bounds__(" << block << ") void " << k.name << "(\n"
                     << sig.str() << ") {\n" << kernel_body << "}\n";
-                k.args = args.vals;
                 return src.str();
             }
         };
@@ -366,14 +390,94 @@ namespace ormi::hip {
             return n;
         }
 
+        const Expr& no_expr() {
+            static const Expr e;
+            return e;
+        }
+
         std::string reduce_name(ReduceOp op) {
             return op == ReduceOp::Sum ? "sum" : op == ReduceOp::Max ? "max" : "argmax";
+        }
+
+        // Everything a generated source depends on, without sizes, strides or
+        // pointers: kernel kind, parameter list, which strides are 0 / 1 /
+        // general, group layout, vector width, index width, tuning and the tape.
+        std::string signature(const Gen& g, const std::string& kind) {
+            std::ostringstream s;
+            const Tuning& t = tuning();
+            s << kind << '|' << t.map_unroll << t.row_unroll << t.col_waves << t.map_nt_loads << t.map_nt_stores << t.reduce_nt_loads << '|';
+            for (const auto& d : g.args.decls) s << d << ';';
+            s << '|';
+            for (const auto& d : g.c.dims) s << (int)d.group;
+            s << '|' << g.vec << ',' << g.vec_dim << ',' << g.idx32 << '|';
+            for (size_t L = 0; L < g.e.leaves.size(); ++L) {
+                if (g.scalar[L]) {
+                    s << 'S';
+                    continue;
+                }
+                for (long long v : g.c.st[L]) s << (v == 0 ? '0' : v == 1 ? '1' : 'x');
+                s << ',';
+            }
+            s << '|';
+            for (const auto& in : g.e.insts) s << (int)in.op << ',' << in.a << ',' << in.b << ',' << (int)in.cast << ';';
+            s << g.e.root;
+            return s.str();
+        }
+
+        // Generated kernels by signature: name and source once emitted, and
+        // the hipRTC handle once compiled.
+        struct CachedKernel {
+            std::string name;
+            std::string source;
+            uint64_t handle = 0;
+        };
+        std::mutex& cache_mu() {
+            static std::mutex m;
+            return m;
+        }
+        std::unordered_map<std::string, CachedKernel>& kernel_cache() {
+            static auto* c = new std::unordered_map<std::string, CachedKernel>();
+            return *c;
+        }
+
+        // On a hit, fills k's name and handle (or source) and returns true.
+        bool cache_lookup(const std::string& sig, KernelLaunch& k) {
+            k.key = sig;
+            std::lock_guard<std::mutex> lock(cache_mu());
+            auto it = kernel_cache().find(sig);
+            if (it == kernel_cache().end()) return false;
+            k.name = it->second.name;
+            k.handle = it->second.handle;
+            if (!k.handle) k.source = it->second.source;
+            return true;
+        }
+
+        void cache_store(const KernelLaunch& k) {
+            std::lock_guard<std::mutex> lock(cache_mu());
+            auto& e = kernel_cache()[k.key];
+            e.name = k.name;
+            if (!k.source.empty()) e.source = k.source;
+            if (k.handle) e.handle = k.handle;
+        }
+
+        // Emit the source of a kernel unless the cache already has it.
+        template <typename EmitBody>
+        void resolve(Gen& g, const std::string& kind, int block, KernelLaunch& k, EmitBody emit) {
+            k.args = g.args.vals;
+            k.block[0] = (uint32_t)block;
+            if (cache_lookup(signature(g, kind), k)) return;
+            emit();
+            k.source = g.finish(kind, block, k);
+            cache_store(k);
         }
     }  // namespace
 
     // ------------------------------------------------------------------ map --
     KernelLaunch plan_map(const Expr& expr, const std::vector<int>& shape, void* out, DType out_dtype, int cu) {
+        const Tuning& tn = tuning();
+        const int block = 256, unroll = tn.map_unroll;
         Gen g(expr);
+        g.nt_loads = tn.map_nt_loads;
         for (int s : shape) g.c.dims.push_back({(long long)s, G_M});
         for (const auto& L : expr.leaves) g.c.st.push_back(L.st);
         canonicalize(g.c, g.scalar);
@@ -387,11 +491,11 @@ namespace ormi::hip {
         long long numel = 1;
         for (auto& d : g.c.dims) numel *= d.size;
         const long long G = numel / g.vec;
-        const long long tiles = (G + kBlock * kUnroll - 1) / (kBlock * kUnroll);
-        const long long cap = (long long)std::max(cu, 1) * 16;
-        const long long grid = std::max(1LL, std::min(tiles, cap));
+        const long long tile = (long long)block * unroll;
+        const long long tiles = (G + tile - 1) / tile;
+        const long long grid = std::max(1LL, std::min(tiles, (long long)std::max(cu, 1) * tn.map_blocks_per_cu));
         // The grid-stride cursor reaches G + grid * tile before the loop exits.
-        g.choose_idx(G + grid * kBlock * kUnroll);
+        g.choose_idx(G + grid * tile);
 
         KernelLaunch k;
         g.args.ptr(std::string(storage_type(out_dtype)) + "* __restrict__ out", out);
@@ -399,57 +503,63 @@ namespace ormi::hip {
         g.args.i64("G", G);
         g.declare_dims();
         g.declare_strides();
-
-        std::vector<int> all;
-        for (int d = 0; d < n; ++d) all.push_back(d);
-        const std::string t = g.idx();
-        const int V = g.vec;
-        std::ostringstream& b = g.body;
-        g.hoist_scalars(b, "  ");
-        b << "  const " << t << " tile = " << kBlock * kUnroll << ";\n";
-        b << "  for (" << t << " base = (" << t << ")blockIdx.x * tile; base < (" << t << ")G; base += (" << t << ")gridDim.x * tile) {\n";
-        g.declare_leaf_regs(b, "    ", kUnroll);
-        b << "    " << t << " gi[" << kUnroll << "];\n";
-        b << "#pragma unroll\n    for (int u = 0; u < " << kUnroll << "; ++u) {\n";
-        b << "      const " << t << " gg = base + u * " << kBlock << " + (" << t << ")threadIdx.x;\n";
-        b << "      gi[u] = gg;\n";
-        b << "      const " << t << " gc = gg < (" << t << ")G ? gg : (" << t << ")G - 1;\n";
-        g.declare_coords(b, "      ", all);
-        g.decompose(b, "      ", "gc", all);
-        for (size_t L = 0; L < expr.leaves.size(); ++L) {
-            if (g.scalar[L]) continue;
-            std::string off = g.offset(L, all);
-            if (off.empty()) off = "0";
-            g.load_leaf(b, "      ", L, off, "x" + std::to_string(L) + "[u]");
-        }
-        b << "    }\n";
-        b << "#pragma unroll\n    for (int u = 0; u < " << kUnroll << "; ++u) {\n";
-        b << "      float res[" << V << "];\n";
-        b << "#pragma unroll\n      for (int k = 0; k < " << V << "; ++k) {\n";
-        const std::string root = g.eval(b, "        ", "u", "k");
-        b << "        res[k] = " << root << ";\n      }\n";
-        b << "      if (gi[u] < (" << t << ")G) {\n";
-        if (V == 4 && out_dtype == DType::Float32) {
-            b << "        *(ormi_f4*)(out + gi[u] * 4) = ormi_f4{res[0], res[1], res[2], res[3]};\n";
-        } else if (V == 4) {
-            b << "        *(ormi_u16x4*)(out + gi[u] * 4) = ormi_u16x4{" << from_f32(out_dtype, "res[0]") << ", "
-              << from_f32(out_dtype, "res[1]") << ", " << from_f32(out_dtype, "res[2]") << ", " << from_f32(out_dtype, "res[3]") << "};\n";
-        } else {
-            b << "        out[gi[u]] = " << from_f32(out_dtype, "res[0]") << ";\n";
-        }
-        b << "      }\n    }\n  }\n";
-
-        k.source = g.finish("map", b.str(), k);
         k.grid[0] = (uint32_t)grid;
-        std::ostringstream plan;
-        plan << "map ndim=" << n << " vec=" << V << " idx=" << (g.idx32 ? 32 : 64) << " groups=" << G;
-        k.plan = plan.str();
+        {
+            std::ostringstream plan;
+            plan << "map ndim=" << n << " vec=" << g.vec << " idx=" << (g.idx32 ? 32 : 64) << " groups=" << G << " unroll=" << unroll;
+            k.plan = plan.str();
+        }
+        resolve(g, "map", block, k, [&] {
+            std::vector<int> all;
+            for (int d = 0; d < n; ++d) all.push_back(d);
+            const std::string t = g.idx();
+            const int V = g.vec;
+            std::ostringstream& b = g.body;
+            g.hoist_scalars(b, "  ");
+            b << "  const " << t << " tile = " << tile << ";\n";
+            b << "  for (" << t << " base = (" << t << ")blockIdx.x * tile; base < (" << t << ")G; base += (" << t << ")gridDim.x * tile) {\n";
+            g.declare_leaf_regs(b, "    ", unroll);
+            b << "    " << t << " gi[" << unroll << "];\n";
+            b << "#pragma unroll\n    for (int u = 0; u < " << unroll << "; ++u) {\n";
+            b << "      const " << t << " gg = base + u * " << block << " + (" << t << ")threadIdx.x;\n";
+            b << "      gi[u] = gg;\n";
+            b << "      const " << t << " gc = gg < (" << t << ")G ? gg : (" << t << ")G - 1;\n";
+            g.declare_coords(b, "      ", all);
+            g.decompose(b, "      ", "gc", all);
+            for (size_t L = 0; L < expr.leaves.size(); ++L) {
+                if (g.scalar[L]) continue;
+                std::string off = g.offset(L, all);
+                g.load_leaf(b, "      ", L, off.empty() ? "0" : off, "x" + std::to_string(L) + "[u]");
+            }
+            b << "    }\n";
+            b << "#pragma unroll\n    for (int u = 0; u < " << unroll << "; ++u) {\n";
+            b << "      float res[" << V << "];\n";
+            b << "#pragma unroll\n      for (int k = 0; k < " << V << "; ++k) {\n";
+            const std::string root = g.eval(b, "        ", "u", "k");
+            b << "        res[k] = " << root << ";\n      }\n";
+            b << "      if (gi[u] < (" << t << ")G) {\n";
+            const bool nt = tn.map_nt_stores;
+            if (V == 4) {
+                const bool f32 = out_dtype == DType::Float32;
+                const char* vt = f32 ? "ormi_f4" : "ormi_u16x4";
+                std::string val = std::string(vt) + "{";
+                for (int q = 0; q < 4; ++q) val += (q ? ", " : "") + from_f32(out_dtype, "res[" + std::to_string(q) + "]");
+                val += "}";
+                const std::string addr = std::string("(") + vt + "*)(out + gi[u] * 4)";
+                if (nt) b << "        __builtin_nontemporal_store(" << val << ", " << addr << ");\n";
+                else b << "        *" << addr << " = " << val << ";\n";
+            } else {
+                b << "        out[gi[u]] = " << from_f32(out_dtype, "res[0]") << ";\n";
+            }
+            b << "      }\n    }\n  }\n";
+        });
         return k;
     }
 
     // ------------------------------------------------------------- reduce --
     ReducePlan plan_reduce(const Expr& expr, const std::vector<int>& in_shape, const std::vector<int>& axes_in, ReduceOp op,
                            void* out, int cu) {
+        const Tuning& tn = tuning();
         const int n = (int)in_shape.size();
         std::vector<bool> red(n, axes_in.empty());
         for (int a : axes_in) red[a] = true;
@@ -458,6 +568,7 @@ namespace ormi::hip {
             if (red[d]) last_red = d;
 
         Gen g(expr);
+        g.nt_loads = tn.reduce_nt_loads;
         // Kernel dim order: O dims, R dims, I dims (each in logical order).
         std::vector<int> perm;
         for (int d = 0; d < n; ++d) if (!red[d] && d < last_red) perm.push_back(d);
@@ -481,25 +592,22 @@ namespace ormi::hip {
         KernelLaunch& k = plan.first;
         const std::string name = reduce_name(op);
         const bool is_sum = op == ReduceOp::Sum;
+        const bool is_arg = op == ReduceOp::Argmax;
         const int V = g.vec;
-        std::ostringstream& b = g.body;
         std::ostringstream summary;
 
         if (!column) {
             // ---------------------------------------------------------- row --
+            const int RU = tn.row_unroll;
             const long long RG = R / V;
             long long P = 1;
             const long long target_waves = (long long)std::max(cu, 1) * 32;
             if (O < target_waves / 2) P = std::max(1LL, std::min((target_waves + O - 1) / O, (RG + 255) / 256));
             const long long CH = (RG + P - 1) / P;
-            P = (RG + CH - 1) / CH;  // drop empty parts
-            if (RG == 0) P = 1;
-            g.choose_idx(O * P * 64);
+            P = RG == 0 ? 1 : (RG + CH - 1) / CH;  // drop empty parts
+            g.choose_idx(O * P * 64 + RG * V + 64 * V * RU);
             plan.two_pass = P > 1;
-            const std::string t = g.idx();
-
-            void* dst_v = plan.two_pass ? nullptr : out;  // bound later for two-pass
-            g.args.ptr("void* __restrict__ outp", dst_v);
+            g.args.ptr("void* __restrict__ outp", plan.two_pass ? nullptr : out);  // workspace bound later
             g.args.ptr("int* __restrict__ outi", nullptr);
             g.declare_leaves();
             g.args.i64("NO", O);
@@ -508,112 +616,118 @@ namespace ormi::hip {
             g.args.i64("CH", CH);
             g.declare_dims();
             g.declare_strides();
-
-            g.hoist_scalars(b, "  ");
-            b << "  const int lane = threadIdx.x & 63;\n";
-            b << "  const " << t << " wid = (" << t << ")blockIdx.x * 4 + (" << t << ")(threadIdx.x >> 6);\n";
-            b << "  if (wid >= (" << t << ")NO * (" << t << ")NP) return;\n";
-            b << "  const " << t << " o = wid / (" << t << ")NP, p = wid - o * (" << t << ")NP;\n";
-            g.declare_coords(b, "  ", od);
-            g.decompose(b, "  ", "o", od);
-            for (size_t L = 0; L < expr.leaves.size(); ++L) {
-                if (g.scalar[L]) continue;
-                std::string off = g.offset(L, od);
-                b << "  const " << t << " base" << L << " = " << (off.empty() ? "0" : off) << ";\n";
-            }
-            b << "  const " << t << " rg0 = p * (" << t << ")CH;\n";
-            b << "  const " << t << " rg1 = rg0 + (" << t << ")CH < (" << t << ")RG ? rg0 + (" << t << ")CH : (" << t << ")RG;\n";
-            if (is_sum) b << "  float acc[" << V << "] = {" << std::string(V > 1 ? "0.0f, 0.0f, 0.0f, 0.0f" : "0.0f") << "};\n";
-            else b << "  float bv = -__builtin_inff(); int bi = 0x7fffffff;\n";
-            // Body for UNR groups starting at rg, stepping 64.
-            auto emit_step = [&](int UNR, const std::string& ind) {
-                g.declare_leaf_regs(b, ind, UNR);
-                b << ind << "#pragma unroll\n" << ind << "for (int u = 0; u < " << UNR << "; ++u) {\n";
-                b << ind << "  const " << t << " rgu = rg + u * 64;\n";
-                g.declare_coords(b, ind + "  ", rd);
-                g.decompose(b, ind + "  ", "rgu", rd);
-                for (size_t L = 0; L < expr.leaves.size(); ++L) {
-                    if (g.scalar[L]) continue;
-                    std::string off = g.offset(L, rd);
-                    g.load_leaf(b, ind + "  ", L, "base" + std::to_string(L) + (off.empty() ? "" : " + " + off),
-                                "x" + std::to_string(L) + "[u]");
-                }
-                b << ind << "}\n";
-                b << ind << "#pragma unroll\n" << ind << "for (int u = 0; u < " << UNR << "; ++u) {\n";
-                b << ind << "#pragma unroll\n" << ind << "  for (int k = 0; k < " << V << "; ++k) {\n";
-                const std::string v = g.eval(b, ind + "    ", "u", "k");
-                if (is_sum) b << ind << "    acc[k] += " << v << ";\n";
-                else b << ind << "    ormi_am_take(bv, bi, " << v << ", (int)((rg + u * 64) * " << V << " + k));\n";
-                b << ind << "  }\n" << ind << "}\n";
-            };
-            b << "  " << t << " rg = rg0 + lane;\n";
-            b << "  for (; rg + " << 64 * (kUnroll - 1) << " < rg1; rg += " << 64 * kUnroll << ") {\n";
-            emit_step(kUnroll, "    ");
-            b << "  }\n";
-            b << "  for (; rg < rg1; rg += 64) {\n";
-            emit_step(1, "    ");
-            b << "  }\n";
-            if (is_sum) {
-                b << "  float s = " << (V > 1 ? "(acc[0] + acc[1]) + (acc[2] + acc[3])" : "acc[0]") << ";\n";
-                b << "  s = ormi_wave_sum(s);\n";
-                b << "  if (lane == 0) ((float*)outp)[wid] = s;\n";
-            } else {
-                b << "  ormi_wave_argmax(bv, bi);\n";
-                b << "  if (lane == 0) {\n";
-                if (op == ReduceOp::Argmax) b << "    if (NP == 1) ((long long*)outp)[wid] = (long long)bi; else { ((float*)outp)[wid] = bv; outi[wid] = bi; }\n";
-                else b << "    ((float*)outp)[wid] = bv; if (NP > 1) outi[wid] = bi;\n";
-                b << "  }\n";
-            }
-            k.source = g.finish("row" + name, b.str(), k);
-            const long long waves = O * P;
-            k.grid[0] = (uint32_t)std::max(1LL, (waves + 3) / 4);
+            k.grid[0] = (uint32_t)std::max(1LL, (O * P + 3) / 4);
             summary << "row " << name << " O=" << O << " R=" << R << " vec=" << V << " parts=" << P << " idx=" << (g.idx32 ? 32 : 64);
             k.plan = summary.str();
+            resolve(g, "row" + name, 256, k, [&] {
+                const std::string t = g.idx();
+                std::ostringstream& b = g.body;
+                g.hoist_scalars(b, "  ");
+                b << "  const int lane = threadIdx.x & 63;\n";
+                b << "  const " << t << " wid = (" << t << ")blockIdx.x * 4 + (" << t << ")(threadIdx.x >> 6);\n";
+                b << "  if (wid >= (" << t << ")NO * (" << t << ")NP) return;\n";
+                b << "  const " << t << " o = wid / (" << t << ")NP, p = wid - o * (" << t << ")NP;\n";
+                g.declare_coords(b, "  ", od);
+                g.decompose(b, "  ", "o", od);
+                for (size_t L = 0; L < expr.leaves.size(); ++L) {
+                    if (g.scalar[L]) continue;
+                    std::string off = g.offset(L, od);
+                    b << "  const " << t << " base" << L << " = " << (off.empty() ? "0" : off) << ";\n";
+                }
+                b << "  const " << t << " rg0 = p * (" << t << ")CH;\n";
+                b << "  const " << t << " rg1 = rg0 + (" << t << ")CH < (" << t << ")RG ? rg0 + (" << t << ")CH : (" << t << ")RG;\n";
+                if (is_sum) b << "  float acc[" << V << "];\n#pragma unroll\n  for (int k = 0; k < " << V << "; ++k) acc[k] = 0.0f;\n";
+                else b << "  float bv = -__builtin_inff(); int bi = 0x7fffffff;\n";
+                // UNR groups per lane starting at rg, 64 groups apart.
+                auto emit_step = [&](int UNR, const std::string& ind) {
+                    g.declare_leaf_regs(b, ind, UNR);
+                    b << ind << "#pragma unroll\n" << ind << "for (int u = 0; u < " << UNR << "; ++u) {\n";
+                    b << ind << "  const " << t << " rgu = rg + u * 64;\n";
+                    g.declare_coords(b, ind + "  ", rd);
+                    g.decompose(b, ind + "  ", "rgu", rd);
+                    for (size_t L = 0; L < expr.leaves.size(); ++L) {
+                        if (g.scalar[L]) continue;
+                        std::string off = g.offset(L, rd);
+                        g.load_leaf(b, ind + "  ", L, "base" + std::to_string(L) + (off.empty() ? "" : " + " + off),
+                                    "x" + std::to_string(L) + "[u]");
+                    }
+                    b << ind << "}\n";
+                    b << ind << "#pragma unroll\n" << ind << "for (int u = 0; u < " << UNR << "; ++u) {\n";
+                    b << ind << "#pragma unroll\n" << ind << "  for (int k = 0; k < " << V << "; ++k) {\n";
+                    const std::string v = g.eval(b, ind + "    ", "u", "k");
+                    if (is_sum) b << ind << "    acc[k] += " << v << ";\n";
+                    else b << ind << "    ormi_am_take(bv, bi, " << v << ", (int)((rg + u * 64) * " << V << " + k));\n";
+                    b << ind << "  }\n" << ind << "}\n";
+                };
+                b << "  " << t << " rg = rg0 + lane;\n";
+                b << "  for (; rg + " << 64 * (RU - 1) << " < rg1; rg += " << 64 * RU << ") {\n";
+                emit_step(RU, "    ");
+                b << "  }\n";
+                if (RU > 1) {
+                    b << "  for (; rg < rg1; rg += 64) {\n";
+                    emit_step(1, "    ");
+                    b << "  }\n";
+                }
+                if (is_sum) {
+                    b << "  float s = " << (V > 1 ? "(acc[0] + acc[1]) + (acc[2] + acc[3])" : "acc[0]") << ";\n";
+                    b << "  s = ormi_wave_sum(s);\n";
+                    b << "  if (lane == 0) ((float*)outp)[wid] = s;\n";
+                } else {
+                    b << "  ormi_wave_argmax(bv, bi);\n";
+                    b << "  if (lane == 0) {\n";
+                    if (is_arg) b << "    if (NP == 1) ((long long*)outp)[wid] = (long long)bi; else { ((float*)outp)[wid] = bv; outi[wid] = bi; }\n";
+                    else b << "    ((float*)outp)[wid] = bv; if (NP > 1) outi[wid] = bi;\n";
+                    b << "  }\n";
+                }
+            });
             if (plan.two_pass) {
                 plan.workspace_bytes = (size_t)(O * P) * (sizeof(float) + sizeof(int));
                 // Second pass: one wave per output row over its P partials, in part order.
                 KernelLaunch& s2 = plan.second;
-                std::ostringstream sb;
-                sb << "  const int lane = threadIdx.x & 63;\n";
-                sb << "  const long long o = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);\n";
-                sb << "  if (o >= NO) return;\n";
-                sb << "  const float* pv = pvals + o * NP; const int* pi = pidx + o * NP;\n";
-                if (is_sum) {
-                    sb << "  float s = 0.0f;\n  for (long long q = lane; q < NP; q += 64) s += pv[q];\n";
-                    sb << "  s = ormi_wave_sum(s);\n  if (lane == 0) ((float*)outp)[o] = s;\n";
-                } else {
-                    sb << "  float bv = -__builtin_inff(); int bi = 0x7fffffff;\n";
-                    sb << "  for (long long q = lane; q < NP; q += 64) ormi_am_take(bv, bi, pv[q], pi[q]);\n";
-                    sb << "  ormi_wave_argmax(bv, bi);\n";
-                    if (op == ReduceOp::Argmax) sb << "  if (lane == 0) ((long long*)outp)[o] = (long long)bi;\n";
-                    else sb << "  if (lane == 0) ((float*)outp)[o] = bv;\n";
-                }
-                Gen g2(expr);
+                Gen g2(no_expr());  // reads only the workspace
                 g2.args.ptr("void* __restrict__ outp", out);
                 g2.args.ptr("const float* __restrict__ pvals", nullptr);
                 g2.args.ptr("const int* __restrict__ pidx", nullptr);
                 g2.args.i64("NO", O);
                 g2.args.i64("NP", P);
-                s2.source = g2.finish("rowfin" + name, sb.str(), s2);
                 s2.grid[0] = (uint32_t)std::max(1LL, (O + 3) / 4);
                 s2.plan = "row-finish " + name;
+                resolve(g2, "rowfin" + name, 256, s2, [&] {
+                    std::ostringstream& sb = g2.body;
+                    sb << "  const int lane = threadIdx.x & 63;\n";
+                    sb << "  const long long o = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);\n";
+                    sb << "  if (o >= NO) return;\n";
+                    sb << "  const float* pv = pvals + o * NP; const int* pi = pidx + o * NP;\n";
+                    if (is_sum) {
+                        sb << "  float s = 0.0f;\n  for (long long q = lane; q < NP; q += 64) s += pv[q];\n";
+                        sb << "  s = ormi_wave_sum(s);\n  if (lane == 0) ((float*)outp)[o] = s;\n";
+                    } else {
+                        sb << "  float bv = -__builtin_inff(); int bi = 0x7fffffff;\n";
+                        sb << "  for (long long q = lane; q < NP; q += 64) ormi_am_take(bv, bi, pv[q], pi[q]);\n";
+                        sb << "  ormi_wave_argmax(bv, bi);\n";
+                        if (is_arg) sb << "  if (lane == 0) ((long long*)outp)[o] = (long long)bi;\n";
+                        else sb << "  if (lane == 0) ((float*)outp)[o] = bv;\n";
+                    }
+                });
             }
             return plan;
         }
 
         // ------------------------------------------------------------ column --
+        const int W = tn.col_waves;
+        const int block = 64 * W;
         const long long IG = I / V;
         const long long BI = (IG + 63) / 64;
         long long P = 1;
-        const long long target_blocks = (long long)std::max(cu, 1) * 8;
-        if (BI * O < target_blocks) P = std::max(1LL, std::min((target_blocks + BI * O - 1) / (BI * O), (R + 63) / 64));
+        // Enough waves to keep HBM busy (about 16 per CU), each covering at
+        // least 32 rows of its part.
+        const long long target_waves = (long long)std::max(cu, 1) * 16;
+        const long long waves1 = BI * O * W;
+        if (waves1 < target_waves) P = std::max(1LL, std::min((target_waves + waves1 - 1) / waves1, R / (32LL * W)));
         const long long CH = (R + P - 1) / P;
-        P = (R + CH - 1) / CH;
-        if (R == 0) P = 1;
-        g.choose_idx(O * I * P);
+        P = R == 0 ? 1 : (R + CH - 1) / CH;
+        g.choose_idx(O * I * P + R + 4LL * W * 4);
         plan.two_pass = P > 1;
-        const std::string t = g.idx();
-
         g.args.ptr("void* __restrict__ outp", plan.two_pass ? nullptr : out);
         g.args.ptr("int* __restrict__ outi", nullptr);
         g.declare_leaves();
@@ -625,107 +739,111 @@ namespace ormi::hip {
         g.args.i64("CH", CH);
         g.declare_dims();
         g.declare_strides();
-
-        g.hoist_scalars(b, "  ");
-        b << "  __shared__ float sv[4][64][" << V << "];\n";
-        if (!is_sum) b << "  __shared__ int si[4][64][" << V << "];\n";
-        b << "  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;\n";
-        b << "  const " << t << " bid = (" << t << ")blockIdx.x;\n";
-        b << "  const " << t << " bi_ = bid % (" << t << ")NBI; const " << t << " rest = bid / (" << t << ")NBI;\n";
-        b << "  const " << t << " o = rest % (" << t << ")NO, p = rest / (" << t << ")NO;\n";
-        b << "  const " << t << " ig = bi_ * 64 + lane;\n";
-        b << "  const bool active = ig < (" << t << ")NIG;\n";
-        b << "  const " << t << " igc = active ? ig : (" << t << ")NIG - 1;\n";
-        std::vector<int> oi = od;
-        oi.insert(oi.end(), id.begin(), id.end());
-        g.declare_coords(b, "  ", oi);
-        g.decompose(b, "  ", "o", od);
-        g.decompose(b, "  ", "igc", id);
-        for (size_t L = 0; L < expr.leaves.size(); ++L) {
-            if (g.scalar[L]) continue;
-            std::string off = g.offset(L, oi);
-            b << "  const " << t << " base" << L << " = " << (off.empty() ? "0" : off) << ";\n";
-        }
-        b << "  const " << t << " r0 = p * (" << t << ")CH;\n";
-        b << "  const " << t << " r1 = r0 + (" << t << ")CH < (" << t << ")NR ? r0 + (" << t << ")CH : (" << t << ")NR;\n";
-        if (is_sum) b << "  float acc[" << V << "];\n#pragma unroll\n  for (int k = 0; k < " << V << "; ++k) acc[k] = 0.0f;\n";
-        else b << "  float bv[" << V << "]; int bx[" << V << "];\n#pragma unroll\n  for (int k = 0; k < " << V
-               << "; ++k) { bv[k] = -__builtin_inff(); bx[k] = 0x7fffffff; }\n";
-        auto emit_cstep = [&](int UNR, const std::string& ind) {
-            g.declare_leaf_regs(b, ind, UNR);
-            b << ind << "#pragma unroll\n" << ind << "for (int u = 0; u < " << UNR << "; ++u) {\n";
-            b << ind << "  const " << t << " ru = r + u * 4;\n";
-            g.declare_coords(b, ind + "  ", rd);
-            g.decompose(b, ind + "  ", "ru", rd);
+        k.grid[0] = (uint32_t)std::max(1LL, BI * O * P);
+        summary << "column " << name << " O=" << O << " R=" << R << " I=" << I << " vec=" << V << " waves=" << W << " parts=" << P
+                << " idx=" << (g.idx32 ? 32 : 64);
+        k.plan = summary.str();
+        resolve(g, "col" + name, block, k, [&] {
+            const std::string t = g.idx();
+            std::ostringstream& b = g.body;
+            const int CU = 4;  // rows in flight per wave
+            g.hoist_scalars(b, "  ");
+            b << "  __shared__ float sv[" << W << "][64][" << V << "];\n";
+            if (!is_sum) b << "  __shared__ int si[" << W << "][64][" << V << "];\n";
+            b << "  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;\n";
+            b << "  const " << t << " bid = (" << t << ")blockIdx.x;\n";
+            b << "  const " << t << " bi_ = bid % (" << t << ")NBI; const " << t << " rest = bid / (" << t << ")NBI;\n";
+            b << "  const " << t << " o = rest % (" << t << ")NO, p = rest / (" << t << ")NO;\n";
+            b << "  const " << t << " ig = bi_ * 64 + lane;\n";
+            b << "  const bool active = ig < (" << t << ")NIG;\n";
+            b << "  const " << t << " igc = active ? ig : (" << t << ")NIG - 1;\n";
+            std::vector<int> oi = od;
+            oi.insert(oi.end(), id.begin(), id.end());
+            g.declare_coords(b, "  ", oi);
+            g.decompose(b, "  ", "o", od);
+            g.decompose(b, "  ", "igc", id);
             for (size_t L = 0; L < expr.leaves.size(); ++L) {
                 if (g.scalar[L]) continue;
-                std::string off = g.offset(L, rd);
-                g.load_leaf(b, ind + "  ", L, "base" + std::to_string(L) + (off.empty() ? "" : " + " + off), "x" + std::to_string(L) + "[u]");
+                std::string off = g.offset(L, oi);
+                b << "  const " << t << " base" << L << " = " << (off.empty() ? "0" : off) << ";\n";
             }
-            b << ind << "}\n";
-            b << ind << "#pragma unroll\n" << ind << "for (int u = 0; u < " << UNR << "; ++u) {\n";
-            b << ind << "#pragma unroll\n" << ind << "  for (int k = 0; k < " << V << "; ++k) {\n";
-            const std::string v = g.eval(b, ind + "    ", "u", "k");
-            if (is_sum) b << ind << "    acc[k] += " << v << ";\n";
-            else b << ind << "    ormi_am_take(bv[k], bx[k], " << v << ", (int)(r + u * 4));\n";
-            b << ind << "  }\n" << ind << "}\n";
-        };
-        b << "  " << t << " r = r0 + w;\n";
-        b << "  if (active) {\n";
-        b << "    for (; r + " << 4 * (kUnroll - 1) << " < r1; r += " << 4 * kUnroll << ") {\n";
-        emit_cstep(kUnroll, "      ");
-        b << "    }\n";
-        b << "    for (; r < r1; r += 4) {\n";
-        emit_cstep(1, "      ");
-        b << "    }\n  }\n";
-        b << "#pragma unroll\n  for (int k = 0; k < " << V << "; ++k) {";
-        if (is_sum) b << " sv[w][lane][k] = acc[k]; }\n";
-        else b << " sv[w][lane][k] = bv[k]; si[w][lane][k] = bx[k]; }\n";
-        b << "  __syncthreads();\n";
-        b << "  if (w == 0 && active) {\n";
-        b << "    const " << t << " e0 = (p * (" << t << ")NO + o) * (" << t << ")NI + ig * " << V << ";\n";
-        b << "#pragma unroll\n    for (int k = 0; k < " << V << "; ++k) {\n";
-        if (is_sum) {
-            b << "      const float s = ((sv[0][lane][k] + sv[1][lane][k]) + sv[2][lane][k]) + sv[3][lane][k];\n";
-            b << "      ((float*)outp)[e0 + k] = s;\n";
-        } else {
-            b << "      float v = sv[0][lane][k]; int x = si[0][lane][k];\n";
-            b << "      ormi_am_take(v, x, sv[1][lane][k], si[1][lane][k]);\n";
-            b << "      ormi_am_take(v, x, sv[2][lane][k], si[2][lane][k]);\n";
-            b << "      ormi_am_take(v, x, sv[3][lane][k], si[3][lane][k]);\n";
-            if (op == ReduceOp::Argmax) b << "      if (outi == nullptr) ((long long*)outp)[e0 + k] = (long long)x; else { ((float*)outp)[e0 + k] = v; outi[e0 + k] = x; }\n";
-            else b << "      ((float*)outp)[e0 + k] = v; if (outi != nullptr) outi[e0 + k] = x;\n";
-        }
-        b << "    }\n  }\n";
-        k.source = g.finish("col" + name, b.str(), k);
-        k.grid[0] = (uint32_t)std::max(1LL, BI * O * P);
-        summary << "column " << name << " O=" << O << " R=" << R << " I=" << I << " vec=" << V << " parts=" << P << " idx=" << (g.idx32 ? 32 : 64);
-        k.plan = summary.str();
+            b << "  const " << t << " r0 = p * (" << t << ")CH;\n";
+            b << "  const " << t << " r1 = r0 + (" << t << ")CH < (" << t << ")NR ? r0 + (" << t << ")CH : (" << t << ")NR;\n";
+            if (is_sum) b << "  float acc[" << V << "];\n#pragma unroll\n  for (int k = 0; k < " << V << "; ++k) acc[k] = 0.0f;\n";
+            else b << "  float bv[" << V << "]; int bx[" << V << "];\n#pragma unroll\n  for (int k = 0; k < " << V
+                   << "; ++k) { bv[k] = -__builtin_inff(); bx[k] = 0x7fffffff; }\n";
+            auto emit_cstep = [&](int UNR, const std::string& ind) {
+                g.declare_leaf_regs(b, ind, UNR);
+                b << ind << "#pragma unroll\n" << ind << "for (int u = 0; u < " << UNR << "; ++u) {\n";
+                b << ind << "  const " << t << " ru = r + u * " << W << ";\n";
+                g.declare_coords(b, ind + "  ", rd);
+                g.decompose(b, ind + "  ", "ru", rd);
+                for (size_t L = 0; L < expr.leaves.size(); ++L) {
+                    if (g.scalar[L]) continue;
+                    std::string off = g.offset(L, rd);
+                    g.load_leaf(b, ind + "  ", L, "base" + std::to_string(L) + (off.empty() ? "" : " + " + off), "x" + std::to_string(L) + "[u]");
+                }
+                b << ind << "}\n";
+                b << ind << "#pragma unroll\n" << ind << "for (int u = 0; u < " << UNR << "; ++u) {\n";
+                b << ind << "#pragma unroll\n" << ind << "  for (int k = 0; k < " << V << "; ++k) {\n";
+                const std::string v = g.eval(b, ind + "    ", "u", "k");
+                if (is_sum) b << ind << "    acc[k] += " << v << ";\n";
+                else b << ind << "    ormi_am_take(bv[k], bx[k], " << v << ", (int)(r + u * " << W << "));\n";
+                b << ind << "  }\n" << ind << "}\n";
+            };
+            b << "  " << t << " r = r0 + w;\n";
+            b << "  if (active) {\n";
+            b << "    for (; r + " << W * (CU - 1) << " < r1; r += " << W * CU << ") {\n";
+            emit_cstep(CU, "      ");
+            b << "    }\n";
+            b << "    for (; r < r1; r += " << W << ") {\n";
+            emit_cstep(1, "      ");
+            b << "    }\n  }\n";
+            b << "#pragma unroll\n  for (int k = 0; k < " << V << "; ++k) {";
+            if (is_sum) b << " sv[w][lane][k] = acc[k]; }\n";
+            else b << " sv[w][lane][k] = bv[k]; si[w][lane][k] = bx[k]; }\n";
+            b << "  __syncthreads();\n";
+            b << "  if (w == 0 && active) {\n";
+            b << "    const " << t << " e0 = (p * (" << t << ")NO + o) * (" << t << ")NI + ig * " << V << ";\n";
+            b << "#pragma unroll\n    for (int k = 0; k < " << V << "; ++k) {\n";
+            if (is_sum) {
+                b << "      float s = sv[0][lane][k];\n";
+                b << "#pragma unroll\n      for (int q = 1; q < " << W << "; ++q) s += sv[q][lane][k];\n";
+                b << "      ((float*)outp)[e0 + k] = s;\n";
+            } else {
+                b << "      float v = sv[0][lane][k]; int x = si[0][lane][k];\n";
+                b << "#pragma unroll\n      for (int q = 1; q < " << W << "; ++q) ormi_am_take(v, x, sv[q][lane][k], si[q][lane][k]);\n";
+                if (is_arg) b << "      if (outi == nullptr) ((long long*)outp)[e0 + k] = (long long)x; else { ((float*)outp)[e0 + k] = v; outi[e0 + k] = x; }\n";
+                else b << "      ((float*)outp)[e0 + k] = v; if (outi != nullptr) outi[e0 + k] = x;\n";
+            }
+            b << "    }\n  }\n";
+        });
         if (plan.two_pass) {
             // Partials are laid out [P][O*I]; the second pass walks them in part order.
             plan.workspace_bytes = (size_t)(P * O * I) * (sizeof(float) + sizeof(int));
             KernelLaunch& s2 = plan.second;
-            std::ostringstream sb;
-            sb << "  const long long e = (long long)blockIdx.x * 256 + threadIdx.x;\n";
-            sb << "  if (e >= NE) return;\n";
-            if (is_sum) {
-                sb << "  float s = 0.0f;\n  for (long long q = 0; q < NP; ++q) s += pvals[q * NE + e];\n";
-                sb << "  ((float*)outp)[e] = s;\n";
-            } else {
-                sb << "  float bv = -__builtin_inff(); int bi = 0x7fffffff;\n";
-                sb << "  for (long long q = 0; q < NP; ++q) ormi_am_take(bv, bi, pvals[q * NE + e], pidx[q * NE + e]);\n";
-                if (op == ReduceOp::Argmax) sb << "  ((long long*)outp)[e] = (long long)bi;\n";
-                else sb << "  ((float*)outp)[e] = bv;\n";
-            }
-            Gen g2(expr);
+            Gen g2(no_expr());  // reads only the workspace
             g2.args.ptr("void* __restrict__ outp", out);
             g2.args.ptr("const float* __restrict__ pvals", nullptr);
             g2.args.ptr("const int* __restrict__ pidx", nullptr);
             g2.args.i64("NE", O * I);
             g2.args.i64("NP", P);
-            s2.source = g2.finish("colfin" + name, sb.str(), s2);
             s2.grid[0] = (uint32_t)std::max(1LL, (O * I + 255) / 256);
             s2.plan = "column-finish " + name;
+            resolve(g2, "colfin" + name, 256, s2, [&] {
+                std::ostringstream& sb = g2.body;
+                sb << "  const long long e = (long long)blockIdx.x * 256 + threadIdx.x;\n";
+                sb << "  if (e >= NE) return;\n";
+                if (is_sum) {
+                    sb << "  float s = 0.0f;\n  for (long long q = 0; q < NP; ++q) s += pvals[q * NE + e];\n";
+                    sb << "  ((float*)outp)[e] = s;\n";
+                } else {
+                    sb << "  float bv = -__builtin_inff(); int bi = 0x7fffffff;\n";
+                    sb << "  for (long long q = 0; q < NP; ++q) ormi_am_take(bv, bi, pvals[q * NE + e], pidx[q * NE + e]);\n";
+                    if (is_arg) sb << "  ((long long*)outp)[e] = (long long)bi;\n";
+                    else sb << "  ((float*)outp)[e] = bv;\n";
+                }
+            });
         }
         return plan;
     }
@@ -746,10 +864,18 @@ namespace ormi::hip {
     }
 
     void launch(const KernelLaunch& k) {
-        std::vector<const char*> opts;
-        for (const auto& o : rtc_options()) opts.push_back(o.c_str());
-        uint64_t handle = 0;
-        ORMI_HIP_CHECK(ormi_hip_rtc_compile(k.source.c_str(), k.name.c_str(), opts.data(), (int)opts.size(), &handle));
+        uint64_t handle = k.handle;
+        if (!handle) {
+            if (k.source.empty()) throw std::runtime_error("HIP codegen: kernel " + k.name + " has no source");
+            std::vector<const char*> opts;
+            for (const auto& o : rtc_options()) opts.push_back(o.c_str());
+            ORMI_HIP_CHECK(ormi_hip_rtc_compile(k.source.c_str(), k.name.c_str(), opts.data(), (int)opts.size(), &handle));
+            if (!k.key.empty()) {
+                KernelLaunch done = k;
+                done.handle = handle;
+                cache_store(done);
+            }
+        }
         std::vector<uint64_t> vals = k.args;
         std::vector<void*> ptrs(vals.size());
         for (size_t i = 0; i < vals.size(); ++i) ptrs[i] = &vals[i];

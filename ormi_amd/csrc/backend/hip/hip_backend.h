@@ -72,13 +72,28 @@ namespace ormi::hip {
 
     // A generated kernel: source, entry name, launch shape, packed arguments.
     struct KernelLaunch {
-        std::string source;
+        std::string source;          // empty when the kernel came from the cache
         std::string name;
+        std::string key;             // structural signature (cache key)
+        uint64_t handle = 0;         // compiled kernel, once known
         uint32_t grid[3] = {1, 1, 1};
         uint32_t block[3] = {256, 1, 1};
         std::vector<uint64_t> args;  // every parameter is 8 bytes
         std::string plan;            // human-readable summary (tests, debugging)
     };
+
+    // Launch-shape knobs of the generated kernels. Defaults are the values
+    // measured best on MI355X; ORMI_* environment variables override them.
+    struct Tuning {
+        int map_unroll = 4;        // VEC groups per thread per iteration (map)
+        int map_blocks_per_cu = 64;
+        int row_unroll = 4;        // VEC groups per lane per iteration (row reduce)
+        int col_waves = 8;         // waves per block along R (column reduce)
+        bool map_nt_loads = false;    // non-temporal hint on a map's operand loads
+        bool map_nt_stores = false;   // non-temporal hint on a map's output stores
+        bool reduce_nt_loads = true;  // non-temporal hint on a reduction's loads
+    };
+    const Tuning& tuning();
 
     // Element-wise map of expr over `shape` into out (contiguous, out_dtype).
     KernelLaunch plan_map(const Expr& expr, const std::vector<int>& shape, void* out, DType out_dtype, int compute_units);

@@ -3,24 +3,31 @@
 // cublasSgemmBatched call (csrc/backend/cuda/kernels/blas/matmul.cu:98-105).
 //
 // Design
-//   * Block tile BM x BN x BK, 256 threads = 4 wave64s in a 2x2 grid; each wave
-//     owns a (BM/2) x (BN/2) sub-tile made of 32x32 MFMA tiles
+//   * Block tile BM x BN x BK, WGM x WGN wave64s; each wave owns a
+//     (BM/WGM) x (BN/WGN) sub-tile of 32x32 MFMA tiles
 //     (v_mfma_f32_32x32x16_{bf16,f16}, or v_mfma_f32_32x32x2_f32).
 //   * Both operands sit in LDS as [mn][k] rows of BK elements plus 16 bytes of
 //     padding (144-byte rows), so every MFMA operand fragment is one
-//     conflict-free 16-byte ds_read per lane. Double-buffered: the next k-tile
-//     is fetched from HBM into registers while the current one feeds the MFMAs.
+//     conflict-free 16-byte ds_read per lane. LDS is double-buffered: the next
+//     k-tile is fetched from HBM into registers while the current one feeds the
+//     MFMAs, and fragments for the next k-step are read from LDS while the
+//     current k-step's MFMAs issue.
 //   * An operand whose k index is contiguous in memory ("N" for A, "T" for B)
 //     is copied 16 bytes at a time. One whose m/n index is contiguous is
-//     fetched as VE x VE blocks (VE = elements per 16 bytes) and transposed in
+//     fetched as VE x MC blocks (VE = elements per 16 bytes) and transposed in
 //     registers before the LDS store, so NN, NT and TN (the forward and the
 //     two backward GEMMs autograd issues) all run the same MFMA loop.
 //   * The tile index is remapped so the 8 XCDs (round-robin block dispatch)
 //     each own a compact group of tiles, sharing operand panels in their L2.
+//   * When the output has too few tiles to occupy the 256 CUs, K is split
+//     across blocks; partial products go to a workspace and a second kernel
+//     adds them in split order (deterministic).
 //   * Shapes or strides the fast path cannot take (alignment, ragged 16-byte
 //     chunks) run a plain tiled kernel instead.
 #include <hip/hip_runtime.h>
 #include <cstdint>
+#include <cstdlib>
+#include <mutex>
 #include <string>
 
 #include "ormi_hip.h"
@@ -36,7 +43,7 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 struct GemmParams {
     const char* a;
     const char* b;
-    float* c;
+    float* c;          // final output, or the split-K workspace
     int M, N, K;
     long long a_sm, a_sk, b_sk, b_sn;  // element strides
     int batch_ndim;
@@ -44,6 +51,9 @@ struct GemmParams {
     long long a_bs[ORMI_GEMM_MAX_BATCH_DIMS];
     long long b_bs[ORMI_GEMM_MAX_BATCH_DIMS];
     int tiles_m, tiles_n;
+    int batch;         // number of batches
+    int splits;        // K splits (1 = write C directly)
+    int k_per_split;   // multiple of BK
 };
 
 // Element-type traits: storage size, elements per 16 bytes, MFMA step.
@@ -71,98 +81,104 @@ struct TrF32 {
     }
 };
 
-// 16-bit VE x VE transpose within one thread: out[i] holds element i of in[0..7].
-__device__ __forceinline__ void transpose_8x8_b16(const u32x4_t (&in)[8], u32x4_t (&out)[8]) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const unsigned x = in[2 * e][i >> 1], y = in[2 * e + 1][i >> 1];
-            out[i][e] = (i & 1) ? ((x >> 16) | (y & 0xffff0000u)) : ((x & 0xffffu) | (y << 16));
-        }
-    }
-}
-__device__ __forceinline__ void transpose_4x4_b32(const u32x4_t (&in)[4], u32x4_t (&out)[4]) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) out[i][e] = in[e][i];
-}
-
-// Registers holding one operand tile between the HBM fetch and the LDS store.
-template <int NCHUNK>
-struct Staged {
-    u32x4_t v[NCHUNK];
-};
-
-// Fetch one BMN x BK operand tile (rows = m or n, columns = k) into registers.
-// KC: k is the unit-stride index. s_mn / s_k are element strides.
-template <typename Tr, int BMN, int BK, bool KC, bool EVEN>
+// Fetch one BMN x BK operand tile (rows = m or n, columns = k) into registers
+// and store it to LDS as [BMN][KCH + 1] 16-byte chunks.
+// KC: k is the unit-stride index. NT: threads per block.
+template <typename Tr, int BMN, int BK, bool KC, bool EVEN, int NT>
 struct TileLoader {
-    static constexpr int VE = Tr::VE;
-    static constexpr int KCH = BK / VE;                         // 16-byte chunks per row
-    static constexpr int NCHUNK = KC ? (BMN * KCH) / 256 : VE;  // per thread
-    static_assert(KC || (BMN / VE) * KCH == 256, "transposed loader needs one VE x VE block per thread");
+    static constexpr int VE = Tr::VE, ES = Tr::ESIZE;
+    static constexpr int KCH = BK / VE;  // 16-byte chunks per row
+    // Direct copy: 16-byte chunks per thread.
+    static constexpr int NCHUNK = (BMN * KCH) / NT;
+    // Transposed copy: each thread owns VE k-rows x MC mn-elements.
+    static constexpr int MC = (BMN * BK) / (VE * NT);
+    static constexpr int MCW = MC * ES / 4;  // dwords per k-row
+    static constexpr int NREG = KC ? NCHUNK * 4 : VE * MCW;
+    static_assert(KC ? (NCHUNK >= 1 && NCHUNK * NT == BMN * KCH) : (KCH == 8 && MC >= 1 && MC * VE * NT == BMN * BK && MCW >= 1),
+                  "tile / thread-count combination not supported");
 
-    __device__ static void load(Staged<NCHUNK>& st, const char* base, long long s_mn, long long s_k, int mn0, int k0,
-                                int MN, int K) {
+    unsigned r[NREG];
+
+    __device__ void load(const char* base, long long s_mn, long long s_k, int mn0, int k0, int MN, int K) {
         const int tid = threadIdx.x;
         if constexpr (KC) {
 #pragma unroll
             for (int i = 0; i < NCHUNK; ++i) {
-                const int idx = i * 256 + tid;
+                const int idx = i * NT + tid;
                 const int row = idx / KCH, kc = idx % KCH;
                 const int mn = mn0 + row, k = k0 + kc * VE;
-                if (EVEN || (mn < MN && k < K)) {
-                    st.v[i] = *(const u32x4_t*)(base + ((long long)mn * s_mn + k) * Tr::ESIZE);
-                } else {
-                    st.v[i] = u32x4_t{0u, 0u, 0u, 0u};
-                }
+                u32x4_t v = {0u, 0u, 0u, 0u};
+                if (EVEN || (mn < MN && k < K)) v = *(const u32x4_t*)(base + ((long long)mn * s_mn + k) * ES);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) r[i * 4 + e] = v[e];
             }
         } else {
             const int lane = tid & 63, wave = tid >> 6;
-            const int mc = wave * 8 + (lane & 7);  // mn chunk of VE elements
+            const int mc = wave * 8 + (lane & 7);  // mn unit of MC elements
             const int kb = lane >> 3;              // k block of VE rows
-            const int mn = mn0 + mc * VE;
+            const int mn = mn0 + mc * MC;
 #pragma unroll
             for (int j = 0; j < VE; ++j) {
                 const int k = k0 + kb * VE + j;
-                if (EVEN || (mn < MN && k < K)) {
-                    st.v[j] = *(const u32x4_t*)(base + ((long long)k * s_k + mn) * Tr::ESIZE);
+                const bool ok = EVEN || (mn < MN && k < K);
+                const char* p = base + ((long long)k * s_k + mn) * ES;
+                if constexpr (MCW == 4) {
+                    u32x4_t v = {0u, 0u, 0u, 0u};
+                    if (ok) v = *(const u32x4_t*)p;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) r[j * 4 + e] = v[e];
+                } else if constexpr (MCW == 2) {
+                    typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+                    u32x2_t v = {0u, 0u};
+                    if (ok) v = *(const u32x2_t*)p;
+                    r[j * 2] = v[0];
+                    r[j * 2 + 1] = v[1];
                 } else {
-                    st.v[j] = u32x4_t{0u, 0u, 0u, 0u};
+                    r[j] = ok ? *(const unsigned*)p : 0u;
                 }
             }
         }
     }
 
-    // LDS tile: [BMN][KCH + 1] chunks of 16 bytes (one chunk of padding per row).
-    __device__ static void store(const Staged<NCHUNK>& st, u32x4_t (*lds)[KCH + 1]) {
+    __device__ void store(u32x4_t (*lds)[KCH + 1]) const {
         const int tid = threadIdx.x;
         if constexpr (KC) {
 #pragma unroll
             for (int i = 0; i < NCHUNK; ++i) {
-                const int idx = i * 256 + tid;
-                lds[idx / KCH][idx % KCH] = st.v[i];
+                const int idx = i * NT + tid;
+                lds[idx / KCH][idx % KCH] = u32x4_t{r[i * 4], r[i * 4 + 1], r[i * 4 + 2], r[i * 4 + 3]};
             }
         } else {
             const int lane = tid & 63, wave = tid >> 6;
             const int mc = wave * 8 + (lane & 7), kb = lane >> 3;
-            u32x4_t t[VE];
-            if constexpr (VE == 8) transpose_8x8_b16(st.v, t);
-            else transpose_4x4_b32(st.v, t);
 #pragma unroll
-            for (int i = 0; i < VE; ++i) lds[mc * VE + i][kb] = t[i];
+            for (int i = 0; i < MC; ++i) {
+                u32x4_t t;
+                if constexpr (ES == 2) {
+                    // Element i of k-row j is half (i & 1) of dword i / 2 of that row.
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const unsigned x = r[(2 * e) * MCW + (i >> 1)], y = r[(2 * e + 1) * MCW + (i >> 1)];
+                        t[e] = (i & 1) ? ((x >> 16) | (y & 0xffff0000u)) : ((x & 0xffffu) | (y << 16));
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) t[e] = r[e * MCW + i];
+                }
+                lds[mc * MC + i][kb] = t;
+            }
         }
     }
 };
 
-template <typename Tr, int BM, int BN, int BK, bool A_KC, bool B_KC, bool EVEN>
-__global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
+template <typename Tr, int BM, int BN, int BK, int WGM, int WGN, bool A_KC, bool B_KC, bool EVEN>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_kernel(GemmParams p) {
+    constexpr int NT = 64 * WGM * WGN;
     constexpr int VE = Tr::VE, KCH = BK / VE;
-    constexpr int WTM = BM / 2, WTN = BN / 2, TM = WTM / 32, TN = WTN / 32;
-    using LA = TileLoader<Tr, BM, BK, A_KC, EVEN>;
-    using LB = TileLoader<Tr, BN, BK, B_KC, EVEN>;
+    constexpr int WTM = BM / WGM, WTN = BN / WGN, TM = WTM / 32, TN = WTN / 32;
+    static_assert(TM >= 1 && TN >= 1 && KCH % 2 == 0, "bad tile shape");
+    using LA = TileLoader<Tr, BM, BK, A_KC, EVEN, NT>;
+    using LB = TileLoader<Tr, BN, BK, B_KC, EVEN, NT>;
 
     __shared__ u32x4_t As[2][BM][KCH + 1];
     __shared__ u32x4_t Bs[2][BN][KCH + 1];
@@ -179,25 +195,26 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
     const int tn_idx = (t % group_size) / gm;
     const int m0 = tm_idx * BM, n0 = tn_idx * BN;
 
-    // ---- batch offsets
-    long long a_off = 0, b_off = 0, c_off = 0;
-    {
-        int bidx = blockIdx.z;
-        c_off = (long long)bidx * p.M * p.N;
-        for (int d = p.batch_ndim - 1; d >= 0; --d) {
-            const int coord = bidx % p.batch_shape[d];
-            bidx /= p.batch_shape[d];
-            a_off += coord * p.a_bs[d];
-            b_off += coord * p.b_bs[d];
-        }
+    // ---- batch and K split
+    const int split = blockIdx.z % p.splits;
+    int bidx = blockIdx.z / p.splits;
+    long long a_off = 0, b_off = 0;
+    const long long c_off = ((long long)split * p.batch + bidx) * p.M * p.N;
+    for (int d = p.batch_ndim - 1; d >= 0; --d) {
+        const int coord = bidx % p.batch_shape[d];
+        bidx /= p.batch_shape[d];
+        a_off += coord * p.a_bs[d];
+        b_off += coord * p.b_bs[d];
     }
     const char* a = p.a + a_off * Tr::ESIZE;
     const char* b = p.b + b_off * Tr::ESIZE;
     float* c = p.c + c_off;
+    const int kbeg = split * p.k_per_split;
+    const int kend = min(p.K, kbeg + p.k_per_split);
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int KT = (p.K + BK - 1) / BK;
+    const int wm = wave / WGN, wn = wave % WGN;
+    const int KT = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
 
     f32x16_t acc[TM][TN];
 #pragma unroll
@@ -207,37 +224,47 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    Staged<LA::NCHUNK> sa;
-    Staged<LB::NCHUNK> sb;
-    LA::load(sa, a, p.a_sm, p.a_sk, m0, 0, p.M, p.K);
-    LB::load(sb, b, p.b_sn, p.b_sk, n0, 0, p.N, p.K);
-    LA::store(sa, As[0]);
-    LB::store(sb, Bs[0]);
+    LA la;
+    LB lb;
+    if (KT > 0) {
+        la.load(a, p.a_sm, p.a_sk, m0, kbeg, p.M, kend);
+        lb.load(b, p.b_sn, p.b_sk, n0, kbeg, p.N, kend);
+        la.store(As[0]);
+        lb.store(Bs[0]);
+    }
     __syncthreads();
 
     for (int kt = 0; kt < KT; ++kt) {
         const int cur = kt & 1;
         const bool more = kt + 1 < KT;
         if (more) {
-            LA::load(sa, a, p.a_sm, p.a_sk, m0, (kt + 1) * BK, p.M, p.K);
-            LB::load(sb, b, p.b_sn, p.b_sk, n0, (kt + 1) * BK, p.N, p.K);
+            la.load(a, p.a_sm, p.a_sk, m0, kbeg + (kt + 1) * BK, p.M, kend);
+            lb.load(b, p.b_sn, p.b_sk, n0, kbeg + (kt + 1) * BK, p.N, kend);
         }
+        u32x4_t af[2][TM], bfr[2][TN];
+        const int half = lane >> 5, row = lane & 31;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) af[0][i] = As[cur][wm * WTM + i * 32 + row][half];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) bfr[0][j] = Bs[cur][wn * WTN + j * 32 + row][half];
 #pragma unroll
         for (int ks = 0; ks < KCH / 2; ++ks) {
-            const int chunk = ks * 2 + (lane >> 5);
-            u32x4_t af[TM], bfr[TN];
+            const int q = ks & 1;
+            if (ks + 1 < KCH / 2) {
+                const int chunk = (ks + 1) * 2 + half;
 #pragma unroll
-            for (int i = 0; i < TM; ++i) af[i] = As[cur][wm * WTM + i * 32 + (lane & 31)][chunk];
+                for (int i = 0; i < TM; ++i) af[q ^ 1][i] = As[cur][wm * WTM + i * 32 + row][chunk];
 #pragma unroll
-            for (int j = 0; j < TN; ++j) bfr[j] = Bs[cur][wn * WTN + j * 32 + (lane & 31)][chunk];
+                for (int j = 0; j < TN; ++j) bfr[q ^ 1][j] = Bs[cur][wn * WTN + j * 32 + row][chunk];
+            }
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
-                for (int j = 0; j < TN; ++j) Tr::mma(af[i], bfr[j], acc[i][j]);
+                for (int j = 0; j < TN; ++j) Tr::mma(af[q][i], bfr[q][j], acc[i][j]);
         }
         if (more) {
-            LA::store(sa, As[cur ^ 1]);
-            LB::store(sb, Bs[cur ^ 1]);
+            la.store(As[cur ^ 1]);
+            lb.store(Bs[cur ^ 1]);
         }
         __syncthreads();
     }
@@ -258,13 +285,259 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
     }
 }
 
-// Any strides, any shape: 16x16 output tile per block, fp32 accumulation.
-template <typename T>
-__device__ __forceinline__ float to_f32(T v);
-template <> __device__ __forceinline__ float to_f32<float>(float v) { return v; }
-template <> __device__ __forceinline__ float to_f32<unsigned short>(unsigned short v) { return __uint_as_float((unsigned)v << 16); }
+// ------------------------------------------------------------------------
+// 16-bit GEMM with direct HBM->LDS loads (gfx950 global_load_lds_dwordx4).
+//
+// Each load instruction moves 64 lanes x 16 bytes into 1 KB of LDS in lane
+// order, so tiles are stored unpadded and bank conflicts are avoided with XOR
+// swizzles of the 16-byte chunk index instead:
+//   k-contiguous operand  [BMN][64]  128-byte rows, physical chunk = c ^ swz_k(row),
+//       swz_k(r) = (r & 7) ^ ((r >> 3) & 1): 16 consecutive rows read by one
+//       ds_read_b128 land on distinct banks for 32- and 64-bank LDS;
+//   mn-contiguous operand [64][BMN]  BMN*2-byte rows, physical chunk = c ^ swz_mn(k),
+//       swz_mn(k) = 4 * (k & 3): the 4 rows x 4 chunks one transpose read
+//       touches cover 64 distinct banks.
+// The mn-contiguous operand is read with ds_read_b64_tr_b16: in each 16-lane
+// group, output lane j slot s is input lane (4s + j/4) element (j % 4); with
+// input lane i pointing at [kbase + i/4][nbase + 4 (i % 4)], lane j receives
+// [kbase + 0..3][nbase + j], i.e. four consecutive k of one column — two such
+// reads form an MFMA operand fragment, so NN and TN need no register
+// transposes. K must be a multiple of 64; rows and columns past M / N are
+// clamped on load (they only feed outputs that are not stored).
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) char lds_char;
 
-template <typename T, bool IS_F16>
+#ifndef ORMI_GEMM_SCHED
+#define ORMI_GEMM_SCHED 1
+#endif
+#ifndef ORMI_GEMM_DMA_ASM
+#define ORMI_GEMM_DMA_ASM 1
+#endif
+
+__device__ __forceinline__ int swz_k(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+__device__ __forceinline__ int swz_mn(int k) { return (k & 3) << 2; }
+
+// Issue the direct loads of one 64-deep k-tile of an operand into LDS.
+// KC: k-contiguous; BMN: tile extent along m (or n); NW: waves sharing the work.
+template <int BMN, bool KC, int NW>
+__device__ __forceinline__ void dma_tile(lds_char* lds, const char* base, long long s_mn, long long s_k, int mn0, int k0,
+                                         int MN) {
+    constexpr int SEGS = BMN * 64 * 2 / 1024;  // 1 KB segments per tile
+    static_assert(SEGS % NW == 0, "segments must split evenly over waves");
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int s = 0; s < SEGS / NW; ++s) {
+        const int q = wave * (SEGS / NW) + s;
+        long long off;
+        if constexpr (KC) {
+            const int row = q * 8 + (lane >> 3);
+            const int c = (lane & 7) ^ swz_k(row);
+            const int mn = min(mn0 + row, MN - 1);
+            off = (long long)mn * s_mn + (k0 + c * 8);
+        } else {
+            constexpr int CPR = BMN / 8;       // 16-byte chunks per k-row
+            constexpr int RPS = 64 / CPR;      // k-rows per segment
+            const int row = q * RPS + lane / CPR;
+            const int c = (lane % CPR) ^ swz_mn(row);
+            const int mn = min(mn0 + c * 8, MN - 8);
+            off = (long long)(k0 + row) * s_k + mn;
+        }
+        const char* src = base + off * 2;
+#if ORMI_GEMM_DMA_ASM
+        // Issued as inline assembly: the compiler's wait-count pass assumes any
+        // LDS read may alias a pending LDS DMA and would make every fragment
+        // read of the current stage wait for these loads of the next stage.
+        // The kernel waits for them itself (vmcnt(0) before each barrier).
+        const unsigned dst = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(lds + q * 1024));
+        asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(dst), "v"(src) : "memory", "m0");
+#else
+        __builtin_amdgcn_global_load_lds((const void*)src, (__attribute__((address_space(3))) void*)(lds + q * 1024), 16, 0, 0);
+#endif
+    }
+}
+
+// MFMA operand fragment for tile rows [row0, row0 + 32) and k-step ks (16 k):
+// lane l holds 8 consecutive k of row row0 + l % 32, starting at 16 ks + 8 (l / 32).
+template <int BMN, bool KC>
+__device__ __forceinline__ u32x4_t frag(const lds_char* lds, int row0, int ks) {
+    const int lane = threadIdx.x & 63;
+    if constexpr (KC) {
+        const int row = row0 + (lane & 31);
+        const int c = ks * 2 + (lane >> 5);
+        return *(const __attribute__((address_space(3))) u32x4_t*)(lds + row * 128 + ((c ^ swz_k(row)) << 4));
+    } else {
+        const int g = lane >> 4, i = lane & 15;
+        const int nb = row0 + (g & 1) * 16 + 4 * (i & 3);
+        u32x4_t out;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int k = ks * 16 + (g >> 1) * 8 + h * 4 + (i >> 2);
+            const int c = nb >> 3;
+            const lds_char* p = lds + k * (BMN * 2) + ((c ^ swz_mn(k)) << 4) + ((nb & 4) << 1);
+            const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4_t*)p);
+            out[2 * h] = (unsigned)(unsigned short)v[0] | ((unsigned)(unsigned short)v[1] << 16);
+            out[2 * h + 1] = (unsigned)(unsigned short)v[2] | ((unsigned)(unsigned short)v[3] << 16);
+        }
+        return out;
+    }
+}
+
+// One k-tile: start loading the next tile into the other stage (An, Bn), run
+// the MFMAs on this stage (As, Bs), then wait for the loads and synchronize.
+// The stage pointers are __restrict__ parameters of an inlined function: the
+// alias scopes that inlining attaches let the compiler see that the reads of
+// this stage do not depend on the in-flight loads of the other, so LDS reads
+// are not made to wait for those loads.
+template <typename Tr, int BM, int BN, int WGM, int WGN, bool A_KC, bool B_KC>
+struct DmaStep {
+    static constexpr int NW = WGM * WGN, BK = 64;
+    static constexpr int WTM = BM / WGM, WTN = BN / WGN, TM = WTM / 32, TN = WTN / 32;
+
+    __device__ __forceinline__ static void run(const lds_char* __restrict__ As, const lds_char* __restrict__ Bs,
+                                               lds_char* __restrict__ An, lds_char* __restrict__ Bn, bool load_next,
+                                               const char* a, const char* b, const GemmParams& p, int m0, int n0, int knext,
+                                               int wm, int wn, f32x16_t (&acc)[TM][TN]) {
+        if (load_next) {
+            dma_tile<BM, A_KC, NW>(An, a, p.a_sm, p.a_sk, m0, knext, p.M);
+            dma_tile<BN, B_KC, NW>(Bn, b, p.b_sn, p.b_sk, n0, knext, p.N);
+        }
+        u32x4_t af[2][TM], bfr[2][TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) af[0][i] = frag<BM, A_KC>(As, wm * WTM + i * 32, 0);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) bfr[0][j] = frag<BN, B_KC>(Bs, wn * WTN + j * 32, 0);
+#pragma unroll
+        for (int ks = 0; ks < BK / 16; ++ks) {
+            const int q = ks & 1;
+            // Fragments of step ks+1 are requested before step ks's MFMAs
+            // issue, so their LDS latency hides behind the matrix work; the
+            // scheduling barriers keep the compiler from sinking the reads.
+            if (ks + 1 < BK / 16) {
+#pragma unroll
+                for (int i = 0; i < TM; ++i) af[q ^ 1][i] = frag<BM, A_KC>(As, wm * WTM + i * 32, ks + 1);
+#pragma unroll
+                for (int j = 0; j < TN; ++j) bfr[q ^ 1][j] = frag<BN, B_KC>(Bs, wn * WTN + j * 32, ks + 1);
+            }
+            if (ORMI_GEMM_SCHED) __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) Tr::mma(af[q][i], bfr[q][j], acc[i][j]);
+            if (ORMI_GEMM_SCHED) __builtin_amdgcn_sched_barrier(0);
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+    }
+};
+
+template <typename Tr, int BM, int BN, int WGM, int WGN, bool A_KC, bool B_KC>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_dma_kernel(GemmParams p) {
+    constexpr int NW = WGM * WGN, BK = 64;
+    constexpr int WTM = BM / WGM, WTN = BN / WGN, TM = WTM / 32, TN = WTN / 32;
+    constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2;
+    // Two stages in four distinct arrays: the loads into one stage and the
+    // reads of the other are then provably disjoint, so the compiler does not
+    // make each LDS read wait for the in-flight loads (vmcnt) of the next tile.
+    __shared__ __attribute__((aligned(1024))) char sa0[A_BYTES];
+    __shared__ __attribute__((aligned(1024))) char sb0[B_BYTES];
+    __shared__ __attribute__((aligned(1024))) char sa1[A_BYTES];
+    __shared__ __attribute__((aligned(1024))) char sb1[B_BYTES];
+
+    const int T = p.tiles_m * p.tiles_n;
+    int t = blockIdx.x;
+    if ((T & 7) == 0) t = (t & 7) * (T >> 3) + (t >> 3);
+    constexpr int GROUP = 4;
+    const int group_size = GROUP * p.tiles_n;
+    const int g = t / group_size, first_m = g * GROUP;
+    const int gm = min(p.tiles_m - first_m, GROUP);
+    const int m0 = (first_m + (t % group_size) % gm) * BM;
+    const int n0 = ((t % group_size) / gm) * BN;
+
+    const int split = blockIdx.z % p.splits;
+    int bidx = blockIdx.z / p.splits;
+    long long a_off = 0, b_off = 0;
+    const long long c_off = ((long long)split * p.batch + bidx) * p.M * p.N;
+    for (int d = p.batch_ndim - 1; d >= 0; --d) {
+        const int coord = bidx % p.batch_shape[d];
+        bidx /= p.batch_shape[d];
+        a_off += coord * p.a_bs[d];
+        b_off += coord * p.b_bs[d];
+    }
+    const char* a = p.a + a_off * 2;
+    const char* b = p.b + b_off * 2;
+    float* c = p.c + c_off;
+    const int kbeg = split * p.k_per_split;
+    const int kend = min(p.K, kbeg + p.k_per_split);
+    const int KT = kend > kbeg ? (kend - kbeg) / BK : 0;
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave / WGN, wn = wave % WGN;
+
+    f32x16_t acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    if (KT > 0) {
+        dma_tile<BM, A_KC, NW>((lds_char*)sa0, a, p.a_sm, p.a_sk, m0, kbeg, p.M);
+        dma_tile<BN, B_KC, NW>((lds_char*)sb0, b, p.b_sn, p.b_sk, n0, kbeg, p.N);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+
+    using Step = DmaStep<Tr, BM, BN, WGM, WGN, A_KC, B_KC>;
+    for (int kt = 0; kt < KT; ++kt) {
+        const bool odd = kt & 1;
+        lds_char* A0 = (lds_char*)sa0;
+        lds_char* A1 = (lds_char*)sa1;
+        lds_char* B0 = (lds_char*)sb0;
+        lds_char* B1 = (lds_char*)sb1;
+        Step::run(odd ? A1 : A0, odd ? B1 : B0, odd ? A0 : A1, odd ? B0 : B1, kt + 1 < KT, a, b, p, m0, n0,
+                  kbeg + (kt + 1) * BK, wm, wn, acc);
+    }
+
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int col = n0 + wn * WTN + j * 32 + (lane & 31);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (row < p.M && col < p.N) c[(long long)row * p.N + col] = acc[i][j][r];
+            }
+        }
+    }
+}
+
+// C[e] = sum over splits s (in order) of ws[s][e].
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(float* __restrict__ c, const float* __restrict__ ws, long long n,
+                                                            int splits) {
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    for (long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += stride) {
+        float s = ws[e];
+        for (int q = 1; q < splits; ++q) s += ws[(long long)q * n + e];
+        c[e] = s;
+    }
+}
+
+// Any strides, any shape: 16x16 output tile per block, fp32 accumulation.
+template <int DT>
+__device__ __forceinline__ float gemm_elem(const void* p, long long i) {
+    if constexpr (DT == ORMI_DTYPE_F32) return ((const float*)p)[i];
+    else if constexpr (DT == ORMI_DTYPE_BF16) return __uint_as_float((unsigned)((const unsigned short*)p)[i] << 16);
+    else {
+        const unsigned short h = ((const unsigned short*)p)[i];
+        _Float16 x;
+        __builtin_memcpy(&x, &h, 2);
+        return (float)x;
+    }
+}
+
+template <int DT>
 __global__ __launch_bounds__(256) void gemm_generic_kernel(GemmParams p) {
     __shared__ float As[16][17];
     __shared__ float Bs[16][17];
@@ -279,23 +552,12 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(GemmParams p) {
         a_off += coord * p.a_bs[d];
         b_off += coord * p.b_bs[d];
     }
-    const T* a = (const T*)p.a + a_off;
-    const T* b = (const T*)p.b + b_off;
     float acc = 0.0f;
     for (int k0 = 0; k0 < p.K; k0 += 16) {
         const int ar = blockIdx.y * 16 + ty, ak = k0 + tx;
-        float av = 0.0f, bv = 0.0f;
-        if (ar < p.M && ak < p.K) {
-            const T v = a[(long long)ar * p.a_sm + (long long)ak * p.a_sk];
-            if constexpr (IS_F16) { _Float16 h; __builtin_memcpy(&h, &v, 2); av = (float)h; } else av = to_f32<T>(v);
-        }
         const int bk = k0 + ty, bc = blockIdx.x * 16 + tx;
-        if (bk < p.K && bc < p.N) {
-            const T v = b[(long long)bk * p.b_sk + (long long)bc * p.b_sn];
-            if constexpr (IS_F16) { _Float16 h; __builtin_memcpy(&h, &v, 2); bv = (float)h; } else bv = to_f32<T>(v);
-        }
-        As[ty][tx] = av;
-        Bs[ty][tx] = bv;
+        As[ty][tx] = (ar < p.M && ak < p.K) ? gemm_elem<DT>(p.a, a_off + (long long)ar * p.a_sm + (long long)ak * p.a_sk) : 0.0f;
+        Bs[ty][tx] = (bk < p.K && bc < p.N) ? gemm_elem<DT>(p.b, b_off + (long long)bk * p.b_sk + (long long)bc * p.b_sn) : 0.0f;
         __syncthreads();
 #pragma unroll
         for (int kk = 0; kk < 16; ++kk) acc = __builtin_fmaf(As[ty][kk], Bs[kk][tx], acc);
@@ -304,19 +566,132 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(GemmParams p) {
     if (row < p.M && col < p.N) p.c[c_off + (long long)row * p.N + col] = acc;
 }
 
-template <typename Tr, int BM, int BN, int BK, bool A_KC, bool B_KC>
-static void launch_mfma(const GemmParams& p, int batch, bool even) {
-    dim3 grid(p.tiles_m * p.tiles_n, 1, batch);
-    if (even) gemm_mfma_kernel<Tr, BM, BN, BK, A_KC, B_KC, true><<<grid, 256>>>(p);
-    else gemm_mfma_kernel<Tr, BM, BN, BK, A_KC, B_KC, false><<<grid, 256>>>(p);
+// ------------------------------------------------------------------ dispatch --
+struct Cfg {
+    int BM, BN, BK;
+};
+
+template <typename Tr, int BM, int BN, int BK, int WGM, int WGN>
+struct Launcher {
+    static constexpr Cfg cfg{BM, BN, BK};
+    template <bool A_KC, bool B_KC>
+    static void go(const GemmParams& p, dim3 grid, bool even) {
+        if (even) gemm_mfma_kernel<Tr, BM, BN, BK, WGM, WGN, A_KC, B_KC, true><<<grid, 64 * WGM * WGN>>>(p);
+        else gemm_mfma_kernel<Tr, BM, BN, BK, WGM, WGN, A_KC, B_KC, false><<<grid, 64 * WGM * WGN>>>(p);
+    }
+    static void run(const GemmParams& p, dim3 grid, bool even, bool a_kc, bool b_kc) {
+        if (a_kc && b_kc) go<true, true>(p, grid, even);
+        else if (a_kc) go<true, false>(p, grid, even);
+        else if (b_kc) go<false, true>(p, grid, even);
+        else go<false, false>(p, grid, even);
+    }
+};
+
+// 16-bit configurations, selectable with ORMI_GEMM_CFG16 for tuning:
+//   0: 256x256x64, 2x2 waves (128x128 per wave, 1 wave/SIMD)
+//   1: 256x256x64, 2x4 waves (128x64 per wave, 2 waves/SIMD)
+//   2: 256x256x64, 4x2 waves (64x128 per wave, 2 waves/SIMD)
+//   3: 128x128x64, 2x2 waves (64x64 per wave, 2 blocks/CU)
+// fp32 configurations (ORMI_GEMM_CFG32):
+//   0: 128x128x32, 2x2 waves (64x64 per wave)
+//   1: 256x128x32, 4x2 waves (64x64 per wave)
+//   2: 128x256x32, 2x4 waves (64x64 per wave)
+static int env_cfg(const char* name, int dflt) {
+    const char* v = std::getenv(name);
+    return v && *v ? std::atoi(v) : dflt;
 }
 
-template <typename Tr, int BM, int BN, int BK>
-static void dispatch_layout(const GemmParams& p, int batch, bool even, bool a_kc, bool b_kc) {
-    if (a_kc && b_kc) launch_mfma<Tr, BM, BN, BK, true, true>(p, batch, even);
-    else if (a_kc) launch_mfma<Tr, BM, BN, BK, true, false>(p, batch, even);
-    else if (b_kc) launch_mfma<Tr, BM, BN, BK, false, true>(p, batch, even);
-    else launch_mfma<Tr, BM, BN, BK, false, false>(p, batch, even);
+template <typename Tr>
+static Cfg cfg16(int id) {
+    switch (id) {
+        case 0: return Launcher<Tr, 256, 256, 64, 2, 2>::cfg;
+        case 1: return Launcher<Tr, 256, 256, 64, 2, 4>::cfg;
+        case 2: return Launcher<Tr, 256, 256, 64, 4, 2>::cfg;
+        default: return Launcher<Tr, 128, 128, 64, 2, 2>::cfg;
+    }
+}
+template <typename Tr>
+static void run16(int id, const GemmParams& p, dim3 grid, bool even, bool a_kc, bool b_kc) {
+    switch (id) {
+        case 0: Launcher<Tr, 256, 256, 64, 2, 2>::run(p, grid, even, a_kc, b_kc); break;
+        case 1: Launcher<Tr, 256, 256, 64, 2, 4>::run(p, grid, even, a_kc, b_kc); break;
+        case 2: Launcher<Tr, 256, 256, 64, 4, 2>::run(p, grid, even, a_kc, b_kc); break;
+        default: Launcher<Tr, 128, 128, 64, 2, 2>::run(p, grid, even, a_kc, b_kc); break;
+    }
+}
+static Cfg cfg32(int id) {
+    switch (id) {
+        case 1: return Launcher<TrF32, 256, 128, 32, 4, 2>::cfg;
+        case 2: return Launcher<TrF32, 128, 256, 32, 2, 4>::cfg;
+        default: return Launcher<TrF32, 128, 128, 32, 2, 2>::cfg;
+    }
+}
+static void run32(int id, const GemmParams& p, dim3 grid, bool even, bool a_kc, bool b_kc) {
+    switch (id) {
+        case 1: Launcher<TrF32, 256, 128, 32, 4, 2>::run(p, grid, even, a_kc, b_kc); break;
+        case 2: Launcher<TrF32, 128, 256, 32, 2, 4>::run(p, grid, even, a_kc, b_kc); break;
+        default: Launcher<TrF32, 128, 128, 32, 2, 2>::run(p, grid, even, a_kc, b_kc); break;
+    }
+}
+
+// Direct-load 16-bit configurations (ORMI_GEMM_DMA_CFG):
+//   0: 256x256, 2x2 waves (128x128 per wave)   1: 256x256, 2x4 waves (128x64)
+//   2: 256x256, 4x2 waves (64x128)              3: 128x128, 2x2 waves (64x64)
+template <typename Tr, int BM, int BN, int WGM, int WGN>
+struct DmaLauncher {
+    static constexpr Cfg cfg{BM, BN, 64};
+    template <bool A_KC, bool B_KC>
+    static void go(const GemmParams& p, dim3 grid) {
+        gemm_dma_kernel<Tr, BM, BN, WGM, WGN, A_KC, B_KC><<<grid, 64 * WGM * WGN>>>(p);
+    }
+    static void run(const GemmParams& p, dim3 grid, bool a_kc, bool b_kc) {
+        if (a_kc && b_kc) go<true, true>(p, grid);
+        else if (a_kc) go<true, false>(p, grid);
+        else if (b_kc) go<false, true>(p, grid);
+        else go<false, false>(p, grid);
+    }
+};
+template <typename Tr>
+static Cfg cfg_dma(int id) {
+    switch (id) {
+        case 0: return DmaLauncher<Tr, 256, 256, 2, 2>::cfg;
+        case 1: return DmaLauncher<Tr, 256, 256, 2, 4>::cfg;
+        case 2: return DmaLauncher<Tr, 256, 256, 4, 2>::cfg;
+        default: return DmaLauncher<Tr, 128, 128, 2, 2>::cfg;
+    }
+}
+template <typename Tr>
+static void run_dma(int id, const GemmParams& p, dim3 grid, bool a_kc, bool b_kc) {
+    switch (id) {
+        case 0: DmaLauncher<Tr, 256, 256, 2, 2>::run(p, grid, a_kc, b_kc); break;
+        case 1: DmaLauncher<Tr, 256, 256, 2, 4>::run(p, grid, a_kc, b_kc); break;
+        case 2: DmaLauncher<Tr, 256, 256, 4, 2>::run(p, grid, a_kc, b_kc); break;
+        default: DmaLauncher<Tr, 128, 128, 2, 2>::run(p, grid, a_kc, b_kc); break;
+    }
+}
+
+// Split-K workspace, grown on demand and kept; every use is ordered on the
+// null stream, so reuse by the next call is safe.
+static std::mutex g_ws_mu;
+static void* g_ws = nullptr;
+static size_t g_ws_bytes = 0;
+
+static int workspace(size_t bytes, void** out) {
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    if (bytes > g_ws_bytes) {
+        if (g_ws) {
+            hipError_t e = hipDeviceSynchronize();
+            if (e == hipSuccess) e = hipFree(g_ws);
+            if (e != hipSuccess) return fail(ORMI_HIP_ERR_RUNTIME, std::string("gemm workspace free: ") + hipGetErrorString(e));
+            g_ws = nullptr;
+            g_ws_bytes = 0;
+        }
+        hipError_t e = hipMalloc(&g_ws, bytes);
+        if (e != hipSuccess) return fail(ORMI_HIP_ERR_RUNTIME, std::string("gemm workspace: ") + hipGetErrorString(e));
+        g_ws_bytes = bytes;
+    }
+    *out = g_ws;
+    return ORMI_HIP_OK;
 }
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -356,6 +731,9 @@ extern "C" int ormi_hip_gemm(const ormi_gemm_desc* d) {
         p.a_bs[i] = d->a_batch_stride[i];
         p.b_bs[i] = d->b_batch_stride[i];
     }
+    p.batch = (int)batch;
+    p.splits = 1;
+    p.k_per_split = d->K;
 
     if (d->K == 0) {
         const float zero = 0.0f;
@@ -365,8 +743,8 @@ extern "C" int ormi_hip_gemm(const ormi_gemm_desc* d) {
     const bool f32 = d->dtype == ORMI_DTYPE_F32;
     const int VE = f32 ? 4 : 8;
     // Which index is unit-stride for each operand (k preferred when both are).
-    const bool a_kc = d->a_stride_k == 1, a_mc = d->a_stride_m == 1 || d->M == 1;
-    const bool b_kc = d->b_stride_k == 1, b_nc = d->b_stride_n == 1 || d->N == 1;
+    const bool a_kc = d->a_stride_k == 1, a_mc = d->a_stride_m == 1;
+    const bool b_kc = d->b_stride_k == 1, b_nc = d->b_stride_n == 1;
     bool fast = (a_kc || a_mc) && (b_kc || b_nc) && aligned16(d->a) && aligned16(d->b);
     if (fast) {
         // 16-byte chunks must be whole: the unit-stride extent and every other
@@ -380,26 +758,61 @@ extern "C" int ormi_hip_gemm(const ormi_gemm_desc* d) {
             fast = (d->a_batch_stride[i] % VE == 0) && (d->b_batch_stride[i] % VE == 0);
     }
 
+    hipError_t e;
     if (!fast) {
         dim3 grid((d->N + 15) / 16, (d->M + 15) / 16, (unsigned)batch);
-        if (f32) gemm_generic_kernel<float, false><<<grid, 256>>>(p);
-        else if (d->dtype == ORMI_DTYPE_BF16) gemm_generic_kernel<unsigned short, false><<<grid, 256>>>(p);
-        else gemm_generic_kernel<unsigned short, true><<<grid, 256>>>(p);
-    } else if (f32) {
-        constexpr int BM = 128, BN = 128, BK = 32;
-        p.tiles_m = (d->M + BM - 1) / BM;
-        p.tiles_n = (d->N + BN - 1) / BN;
-        const bool even = d->M % BM == 0 && d->N % BN == 0 && d->K % BK == 0;
-        dispatch_layout<TrF32, BM, BN, BK>(p, (int)batch, even, a_kc, b_kc);
-    } else {
-        constexpr int BM = 256, BN = 256, BK = 64;
-        p.tiles_m = (d->M + BM - 1) / BM;
-        p.tiles_n = (d->N + BN - 1) / BN;
-        const bool even = d->M % BM == 0 && d->N % BN == 0 && d->K % BK == 0;
-        if (d->dtype == ORMI_DTYPE_BF16) dispatch_layout<TrBF16, BM, BN, BK>(p, (int)batch, even, a_kc, b_kc);
-        else dispatch_layout<TrF16, BM, BN, BK>(p, (int)batch, even, a_kc, b_kc);
+        if (f32) gemm_generic_kernel<ORMI_DTYPE_F32><<<grid, 256>>>(p);
+        else if (d->dtype == ORMI_DTYPE_BF16) gemm_generic_kernel<ORMI_DTYPE_BF16><<<grid, 256>>>(p);
+        else gemm_generic_kernel<ORMI_DTYPE_F16><<<grid, 256>>>(p);
+        e = hipGetLastError();
+        if (e != hipSuccess) return fail(ORMI_HIP_ERR_RUNTIME, std::string("ormi_hip_gemm launch: ") + hipGetErrorString(e));
+        return ORMI_HIP_OK;
     }
-    hipError_t e = hipGetLastError();
+
+    // Direct-load path: 16-bit, K in whole 64-deep tiles, the mn-contiguous
+    // operand's extent in whole 16-byte chunks.
+    const bool dma = !f32 && env_cfg("ORMI_GEMM_DMA", 1) != 0 && d->K % 64 == 0 && (a_kc || d->M % 8 == 0) &&
+                     (b_kc || d->N % 8 == 0);
+    const int id = dma ? env_cfg("ORMI_GEMM_DMA_CFG", 0) : f32 ? env_cfg("ORMI_GEMM_CFG32", 0) : env_cfg("ORMI_GEMM_CFG16", 0);
+    const Cfg cf = dma ? (d->dtype == ORMI_DTYPE_BF16 ? cfg_dma<TrBF16>(id) : cfg_dma<TrF16>(id))
+                       : f32 ? cfg32(id) : (d->dtype == ORMI_DTYPE_BF16 ? cfg16<TrBF16>(id) : cfg16<TrF16>(id));
+    p.tiles_m = (d->M + cf.BM - 1) / cf.BM;
+    p.tiles_n = (d->N + cf.BN - 1) / cf.BN;
+    // Split K when the tiles cannot occupy the compute units, keeping at least
+    // four k-tiles per split.
+    const long long tiles = (long long)p.tiles_m * p.tiles_n * batch;
+    const int cus = compute_units();
+    int splits = 1;
+    if (tiles < cus) {
+        const long long want = (cus + tiles - 1) / tiles;
+        const long long most = d->K / (4LL * cf.BK);
+        splits = (int)std::max(1LL, std::min(want, most));
+    }
+    splits = std::max(1, std::min(splits, env_cfg("ORMI_GEMM_MAX_SPLITS", 16)));
+    if (batch * splits > 65535) splits = 1;
+    const int kps = ((d->K + splits - 1) / splits + cf.BK - 1) / cf.BK * cf.BK;
+    splits = (d->K + kps - 1) / kps;
+    p.splits = splits;
+    p.k_per_split = kps;
+    const size_t out_elems = (size_t)batch * d->M * d->N;
+    if (splits > 1) {
+        void* ws = nullptr;
+        rc = workspace(out_elems * splits * sizeof(float), &ws);
+        if (rc != ORMI_HIP_OK) return rc;
+        p.c = (float*)ws;
+    }
+    const bool even = d->M % cf.BM == 0 && d->N % cf.BN == 0 && d->K % cf.BK == 0;
+    dim3 grid(p.tiles_m * p.tiles_n, 1, (unsigned)(batch * splits));
+    if (dma && d->dtype == ORMI_DTYPE_BF16) run_dma<TrBF16>(id, p, grid, a_kc, b_kc);
+    else if (dma) run_dma<TrF16>(id, p, grid, a_kc, b_kc);
+    else if (f32) run32(id, p, grid, even, a_kc, b_kc);
+    else if (d->dtype == ORMI_DTYPE_BF16) run16<TrBF16>(id, p, grid, even, a_kc, b_kc);
+    else run16<TrF16>(id, p, grid, even, a_kc, b_kc);
+    if (splits > 1) {
+        const unsigned blocks = (unsigned)std::min<size_t>((out_elems + 255) / 256, (size_t)cus * 16);
+        splitk_reduce_kernel<<<blocks, 256>>>(d->c, p.c, (long long)out_elems, splits);
+    }
+    e = hipGetLastError();
     if (e != hipSuccess) return fail(ORMI_HIP_ERR_RUNTIME, std::string("ormi_hip_gemm launch: ") + hipGetErrorString(e));
     return ORMI_HIP_OK;
 }

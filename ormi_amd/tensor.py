@@ -37,6 +37,25 @@ def _parse_device(device) -> Device:
     raise_device_mismatch(msg="Device argument is of invalid type.", got=type(device))
 
 
+_SCALAR_LEAVES: dict = {}
+
+
+def _scalar_leaf(value: float, device: Device) -> Node:
+    """0-d constant leaf for a Python scalar operand, as Ormi makes one per use
+    (reference tensor.py:80-85), but created once per (device, value): leaves are
+    never written after creation, so sharing them is invisible to results and
+    saves a host-to-device copy on every operation with a literal."""
+    key = (int(device.type), device.id, np.float32(value).tobytes())
+    node = _SCALAR_LEAVES.get(key)
+    if node is None:
+        if len(_SCALAR_LEAVES) >= 4096:
+            _SCALAR_LEAVES.clear()
+        buf = ormi_backend.numpy_to_buffer(np.array(value, dtype=np.float32), device.type)
+        node = Node(buf, False, device)
+        _SCALAR_LEAVES[key] = node
+    return node
+
+
 class Tensor:
     def __init__(self, data=None, device=None, requires_grad: bool = False, _node: Node | None = None,
                  dtype: str | None = None):
@@ -80,6 +99,8 @@ class Tensor:
             if self.device.type != other.device.type:
                 raise_device_mismatch(msg="Cannot mix devices in operation.", got=other.device.type)
             return other
+        if isinstance(other, (int, float)) and not isinstance(other, bool):
+            return Tensor(_node=_scalar_leaf(float(other), self.device), device=self.device)
         return Tensor(data=other, device=self.device)
 
     def _binary(self, op, a: "Tensor", b: "Tensor") -> "Tensor":
