@@ -290,11 +290,13 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_kernel(GemmParams p)
 //
 // Each load instruction moves 64 lanes x 16 bytes into 1 KB of LDS in lane
 // order, so tiles are stored unpadded and bank conflicts are avoided with XOR
-// swizzles of the 16-byte chunk index instead:
-//   k-contiguous operand  [BMN][64]  128-byte rows, physical chunk = c ^ swz_k(row),
-//       swz_k(r) = (r & 7) ^ ((r >> 3) & 1): 16 consecutive rows read by one
-//       ds_read_b128 land on distinct banks for 32- and 64-bank LDS;
-//   mn-contiguous operand [64][BMN]  BMN*2-byte rows, physical chunk = c ^ swz_mn(k),
+// swizzles of the 16-byte chunk index instead (BK = tile depth, 32 or 64):
+//   k-contiguous operand  [BMN][BK]  2*BK-byte rows, physical chunk = c ^ swz_k(row),
+//       BK 64: swz_k(r) = (r & 7) ^ ((r >> 3) & 1);
+//       BK 32: swz_k(r) = ((r >> 1) & 3) ^ ((r >> 3) & 1);
+//       16 consecutive rows read by one ds_read_b128 land on distinct banks
+//       for 32- and 64-bank LDS;
+//   mn-contiguous operand [BK][BMN]  BMN*2-byte rows, physical chunk = c ^ swz_mn(k),
 //       swz_mn(k) = 4 * (k & 3): the 4 rows x 4 chunks one transpose read
 //       touches cover 64 distinct banks.
 // The mn-contiguous operand is read with ds_read_b64_tr_b16: in each 16-lane
@@ -302,69 +304,116 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_kernel(GemmParams p)
 // input lane i pointing at [kbase + i/4][nbase + 4 (i % 4)], lane j receives
 // [kbase + 0..3][nbase + j], i.e. four consecutive k of one column — two such
 // reads form an MFMA operand fragment, so NN and TN need no register
-// transposes. K must be a multiple of 64; rows and columns past M / N are
+// transposes. K must be a multiple of BK; rows and columns past M / N are
 // clamped on load (they only feed outputs that are not stored).
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) char lds_char;
 
+// The direct loads set M0 (the LDS destination) in inline assembly and list
+// it as clobbered; clang warns that M0 is a reserved register. No code the
+// compiler generates in these kernels keeps a value in M0 (the gfx950 LDS
+// instructions they use do not read it), which the generated assembly shows.
+#pragma clang diagnostic ignored "-Winline-asm"
+
 #ifndef ORMI_GEMM_SCHED
 #define ORMI_GEMM_SCHED 1
 #endif
-#ifndef ORMI_GEMM_DMA_ASM
-#define ORMI_GEMM_DMA_ASM 1
-#endif
 
-__device__ __forceinline__ int swz_k(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+template <int BK>
+__device__ __forceinline__ int swz_k(int r) {
+    static_assert(BK == 32 || BK == 64, "tile depth 32 or 64");
+    return BK == 64 ? (r & 7) ^ ((r >> 3) & 1) : ((r >> 1) & 3) ^ ((r >> 3) & 1);
+}
 __device__ __forceinline__ int swz_mn(int k) { return (k & 3) << 2; }
 
-// Issue the direct loads of one 64-deep k-tile of an operand into LDS.
+// Direct loads of one operand's BK-deep k-tiles into LDS. The per-lane byte
+// offsets within a tile do not change along k, so they are computed once;
+// each k-tile then costs one scalar base update and one load instruction
+// per 1 KB segment (global_load_lds_dwordx4 with a scalar base and a 32-bit
+// per-lane offset; the host keeps tile spans under 4 GB).
 // KC: k-contiguous; BMN: tile extent along m (or n); NW: waves sharing the work.
-template <int BMN, bool KC, int NW>
-__device__ __forceinline__ void dma_tile(lds_char* lds, const char* base, long long s_mn, long long s_k, int mn0, int k0,
-                                         int MN) {
-    constexpr int SEGS = BMN * 64 * 2 / 1024;  // 1 KB segments per tile
+template <int BMN, bool KC, int NW, int BK = 64>
+struct DmaPlan {
+    static constexpr int SEGS = BMN * BK * 2 / 1024;  // 1 KB segments per tile
+    static constexpr int PER = SEGS / NW;
     static_assert(SEGS % NW == 0, "segments must split evenly over waves");
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    unsigned voff[PER];
+
+    // Rows and columns past MN are clamped (they only feed outputs that are
+    // not stored); mn0 < MN, and for the mn-contiguous layout MN % 8 == 0.
+    __device__ __forceinline__ void init(long long s_mn, long long s_k, int mn0, int MN) {
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
-    for (int s = 0; s < SEGS / NW; ++s) {
-        const int q = wave * (SEGS / NW) + s;
-        long long off;
-        if constexpr (KC) {
-            const int row = q * 8 + (lane >> 3);
-            const int c = (lane & 7) ^ swz_k(row);
-            const int mn = min(mn0 + row, MN - 1);
-            off = (long long)mn * s_mn + (k0 + c * 8);
-        } else {
-            constexpr int CPR = BMN / 8;       // 16-byte chunks per k-row
-            constexpr int RPS = 64 / CPR;      // k-rows per segment
-            const int row = q * RPS + lane / CPR;
-            const int c = (lane % CPR) ^ swz_mn(row);
-            const int mn = min(mn0 + c * 8, MN - 8);
-            off = (long long)(k0 + row) * s_k + mn;
+        for (int s = 0; s < PER; ++s) {
+            const int q = wave * PER + s;
+            if constexpr (KC) {
+                constexpr int CPR = BK / 8;     // 16-byte chunks per row
+                const int row = q * (64 / CPR) + lane / CPR;
+                const int c = (lane % CPR) ^ swz_k<BK>(row);
+                const int mn = min(mn0 + row, MN - 1) - mn0;
+                voff[s] = (unsigned)(((long long)mn * s_mn + c * 8) * 2);
+            } else {
+                constexpr int CPR = BMN / 8;   // 16-byte chunks per k-row
+                constexpr int RPS = 64 / CPR;  // k-rows per segment
+                const int row = q * RPS + lane / CPR;
+                const int c = (lane % CPR) ^ swz_mn(row);
+                const int mn = min(mn0 + c * 8, MN - 8) - mn0;
+                voff[s] = (unsigned)(((long long)row * s_k + mn) * 2);
+            }
         }
-        const char* src = base + off * 2;
-#if ORMI_GEMM_DMA_ASM
-        // Issued as inline assembly: the compiler's wait-count pass assumes any
-        // LDS read may alias a pending LDS DMA and would make every fragment
-        // read of the current stage wait for these loads of the next stage.
-        // The kernel waits for them itself (vmcnt(0) before each barrier).
-        const unsigned dst = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(lds + q * 1024));
-        asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(dst), "v"(src) : "memory", "m0");
-#else
-        __builtin_amdgcn_global_load_lds((const void*)src, (__attribute__((address_space(3))) void*)(lds + q * 1024), 16, 0, 0);
-#endif
     }
-}
+    // Byte offset of element (mn0, k0) from the operand base, and the step
+    // between consecutive k-tiles.
+    __device__ __forceinline__ static long long origin(long long s_mn, long long s_k, int mn0, int k0) {
+        return KC ? ((long long)mn0 * s_mn + k0) * 2 : ((long long)k0 * s_k + mn0) * 2;
+    }
+    __device__ __forceinline__ static long long kstep(long long s_k) { return KC ? 2 * BK : 2 * BK * s_k; }
+
+    // Issued as inline assembly: the compiler's wait-count pass assumes any
+    // LDS read may alias a pending LDS DMA and would make every fragment read
+    // of the current stage wait for these loads of the next stage. The kernel
+    // waits for them itself (an explicit vmcnt before the barrier that
+    // publishes a stage).
+    // One load instruction (segment s of this wave's share) from a tile base
+    // that is already uniform (in scalar registers).
+    __device__ __forceinline__ void issue_one(lds_char* lds, const char* base, int s) const {
+        const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        const unsigned dst = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(lds + (wave * PER + s) * 1024));
+        asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(dst), "v"(voff[s]), "s"(base)
+                     : "memory", "m0");
+    }
+    __device__ __forceinline__ static const char* uniform(const char* tile) {
+        const unsigned long long t = (unsigned long long)(uintptr_t)tile;
+        const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)t);
+        const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(t >> 32));
+        return (const char*)(((unsigned long long)hi << 32) | lo);
+    }
+
+    __device__ __forceinline__ void issue(lds_char* lds, const char* tile) const {
+        const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        const unsigned long long t = (unsigned long long)(uintptr_t)tile;
+        const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)t);
+        const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(t >> 32));
+        const char* base = (const char*)(((unsigned long long)hi << 32) | lo);
+#pragma unroll
+        for (int s = 0; s < PER; ++s) {
+            const unsigned dst =
+                __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)(lds + (wave * PER + s) * 1024));
+            asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(dst), "v"(voff[s]), "s"(base)
+                         : "memory", "m0");
+        }
+    }
+};
 
 // MFMA operand fragment for tile rows [row0, row0 + 32) and k-step ks (16 k):
 // lane l holds 8 consecutive k of row row0 + l % 32, starting at 16 ks + 8 (l / 32).
-template <int BMN, bool KC>
+template <int BMN, bool KC, int BK = 64>
 __device__ __forceinline__ u32x4_t frag(const lds_char* lds, int row0, int ks) {
     const int lane = threadIdx.x & 63;
     if constexpr (KC) {
         const int row = row0 + (lane & 31);
         const int c = ks * 2 + (lane >> 5);
-        return *(const __attribute__((address_space(3))) u32x4_t*)(lds + row * 128 + ((c ^ swz_k(row)) << 4));
+        return *(const __attribute__((address_space(3))) u32x4_t*)(lds + row * (2 * BK) + ((c ^ swz_k<BK>(row)) << 4));
     } else {
         const int g = lane >> 4, i = lane & 15;
         const int nb = row0 + (g & 1) * 16 + 4 * (i & 3);
@@ -382,30 +431,29 @@ __device__ __forceinline__ u32x4_t frag(const lds_char* lds, int row0, int ks) {
     }
 }
 
-// One k-tile: start loading the next tile into the other stage (An, Bn), run
-// the MFMAs on this stage (As, Bs), then wait for the loads and synchronize.
-// The stage pointers are __restrict__ parameters of an inlined function: the
-// alias scopes that inlining attaches let the compiler see that the reads of
-// this stage do not depend on the in-flight loads of the other, so LDS reads
-// are not made to wait for those loads.
+// One k-tile: run the MFMAs on this stage (As, Bs) while the next tile loads
+// into the other stage (An, Bn), then wait for the loads and synchronize.
+// The first fragments of this stage are requested before the loads are
+// issued, so the LDS read latency of the tile's first step overlaps them.
 template <typename Tr, int BM, int BN, int WGM, int WGN, bool A_KC, bool B_KC>
 struct DmaStep {
     static constexpr int NW = WGM * WGN, BK = 64;
     static constexpr int WTM = BM / WGM, WTN = BN / WGN, TM = WTM / 32, TN = WTN / 32;
+    using PlanA = DmaPlan<BM, A_KC, NW>;
+    using PlanB = DmaPlan<BN, B_KC, NW>;
 
-    __device__ __forceinline__ static void run(const lds_char* __restrict__ As, const lds_char* __restrict__ Bs,
-                                               lds_char* __restrict__ An, lds_char* __restrict__ Bn, bool load_next,
-                                               const char* a, const char* b, const GemmParams& p, int m0, int n0, int knext,
-                                               int wm, int wn, f32x16_t (&acc)[TM][TN]) {
-        if (load_next) {
-            dma_tile<BM, A_KC, NW>(An, a, p.a_sm, p.a_sk, m0, knext, p.M);
-            dma_tile<BN, B_KC, NW>(Bn, b, p.b_sn, p.b_sk, n0, knext, p.N);
-        }
+    __device__ __forceinline__ static void run(const lds_char* As, const lds_char* Bs, lds_char* An, lds_char* Bn,
+                                               bool load_next, const PlanA& pa, const PlanB& pb, const char* ta,
+                                               const char* tb, int wm, int wn, f32x16_t (&acc)[TM][TN]) {
         u32x4_t af[2][TM], bfr[2][TN];
 #pragma unroll
         for (int i = 0; i < TM; ++i) af[0][i] = frag<BM, A_KC>(As, wm * WTM + i * 32, 0);
 #pragma unroll
         for (int j = 0; j < TN; ++j) bfr[0][j] = frag<BN, B_KC>(Bs, wn * WTN + j * 32, 0);
+        if (load_next) {
+            pa.issue(An, ta);
+            pb.issue(Bn, tb);
+        }
 #pragma unroll
         for (int ks = 0; ks < BK / 16; ++ks) {
             const int q = ks & 1;
@@ -435,9 +483,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_dma_kernel(GemmParams p) 
     constexpr int NW = WGM * WGN, BK = 64;
     constexpr int WTM = BM / WGM, WTN = BN / WGN, TM = WTM / 32, TN = WTN / 32;
     constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2;
-    // Two stages in four distinct arrays: the loads into one stage and the
-    // reads of the other are then provably disjoint, so the compiler does not
-    // make each LDS read wait for the in-flight loads (vmcnt) of the next tile.
+    // Two stages in four distinct arrays.
     __shared__ __attribute__((aligned(1024))) char sa0[A_BYTES];
     __shared__ __attribute__((aligned(1024))) char sb0[B_BYTES];
     __shared__ __attribute__((aligned(1024))) char sa1[A_BYTES];
@@ -463,8 +509,6 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_dma_kernel(GemmParams p) 
         a_off += coord * p.a_bs[d];
         b_off += coord * p.b_bs[d];
     }
-    const char* a = p.a + a_off * 2;
-    const char* b = p.b + b_off * 2;
     float* c = p.c + c_off;
     const int kbeg = split * p.k_per_split;
     const int kend = min(p.K, kbeg + p.k_per_split);
@@ -472,6 +516,15 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_dma_kernel(GemmParams p) 
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave / WGN, wn = wave % WGN;
+
+    using Step = DmaStep<Tr, BM, BN, WGM, WGN, A_KC, B_KC>;
+    typename Step::PlanA pa;
+    typename Step::PlanB pb;
+    pa.init(p.a_sm, p.a_sk, m0, p.M);
+    pb.init(p.b_sn, p.b_sk, n0, p.N);
+    const char* ta = p.a + a_off * 2 + Step::PlanA::origin(p.a_sm, p.a_sk, m0, kbeg);
+    const char* tb = p.b + b_off * 2 + Step::PlanB::origin(p.b_sn, p.b_sk, n0, kbeg);
+    const long long a_step = Step::PlanA::kstep(p.a_sk), b_step = Step::PlanB::kstep(p.b_sk);
 
     f32x16_t acc[TM][TN];
 #pragma unroll
@@ -482,21 +535,21 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_dma_kernel(GemmParams p) 
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
     if (KT > 0) {
-        dma_tile<BM, A_KC, NW>((lds_char*)sa0, a, p.a_sm, p.a_sk, m0, kbeg, p.M);
-        dma_tile<BN, B_KC, NW>((lds_char*)sb0, b, p.b_sn, p.b_sk, n0, kbeg, p.N);
+        pa.issue((lds_char*)sa0, ta);
+        pb.issue((lds_char*)sb0, tb);
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
-    using Step = DmaStep<Tr, BM, BN, WGM, WGN, A_KC, B_KC>;
     for (int kt = 0; kt < KT; ++kt) {
         const bool odd = kt & 1;
         lds_char* A0 = (lds_char*)sa0;
         lds_char* A1 = (lds_char*)sa1;
         lds_char* B0 = (lds_char*)sb0;
         lds_char* B1 = (lds_char*)sb1;
-        Step::run(odd ? A1 : A0, odd ? B1 : B0, odd ? A0 : A1, odd ? B0 : B1, kt + 1 < KT, a, b, p, m0, n0,
-                  kbeg + (kt + 1) * BK, wm, wn, acc);
+        ta += a_step;
+        tb += b_step;
+        Step::run(odd ? A1 : A0, odd ? B1 : B0, odd ? A0 : A1, odd ? B0 : B1, kt + 1 < KT, pa, pb, ta, tb, wm, wn, acc);
     }
 
 #pragma unroll
@@ -634,9 +687,387 @@ static void run32(int id, const GemmParams& p, dim3 grid, bool even, bool a_kc, 
     }
 }
 
+// ------------------------------------------------------------------------
+// Multi-stage direct-load GEMM. STAGES k-tiles of depth BK live in LDS; the
+// loads of tile kt + STAGES - 1 are issued while tile kt is multiplied, so
+// each tile's loads have STAGES - 2 tiles plus half a tile of matrix work to
+// arrive (LDS holds STAGES tiles; at 256x256x32, 4 stages use 128 KB).
+//
+// Per tile (KS = BK / 16 MFMA k-steps, fragments double-buffered in registers):
+//   ks < KS-1 : read fragments of step ks+1, MFMAs of step ks;
+//   ks = KS-1 : wait until this wave's loads of tile kt+1 have landed (vmcnt),
+//               barrier (every wave's loads of kt+1 landed, every wave done
+//               with tile kt-1's stage), issue the loads of tile kt+STAGES-1
+//               into that freed stage, read step 0 of tile kt+1, MFMAs of
+//               step KS-1.
+// One barrier per tile; the loads are counted per wave (PER instructions per
+// operand per tile), so the vmcnt bound is exact.
+template <int V>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(V >= 0 && V < 64, "vmcnt is a 6-bit counter");
+    // s_waitcnt encoding: vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt[5:4] at [15:14];
+    // expcnt and lgkmcnt at their maxima (no wait).
+    __builtin_amdgcn_s_waitcnt((V & 15) | ((V >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+// Wait until at most n tiles' loads (PER_TILE instructions each) are pending.
+template <int PER_TILE, int MAXN>
+__device__ __forceinline__ void wait_tiles(int n) {
+    if constexpr (MAXN >= 3) { if (n >= 3) { wait_vmcnt<3 * PER_TILE>(); return; } }
+    if constexpr (MAXN >= 2) { if (n >= 2) { wait_vmcnt<2 * PER_TILE>(); return; } }
+    if constexpr (MAXN >= 1) { if (n >= 1) { wait_vmcnt<PER_TILE>(); return; } }
+    wait_vmcnt<0>();
+}
+// Workgroup barrier that orders LDS accesses in program order for the
+// compiler without waiting for outstanding vector-memory loads (a C++
+// __syncthreads() would also drain the direct loads of later stages).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+template <typename Tr, int BM, int BN, int BK, int WGM, int WGN, int STAGES, bool A_KC, bool B_KC>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(GemmParams p) {
+    static_assert(STAGES >= 3 && STAGES <= 5, "3 to 5 stages");
+    constexpr int NW = WGM * WGN, KS = BK / 16;
+    static_assert(KS % 2 == 0, "fragment buffers alternate per k-step");
+    constexpr int WTM = BM / WGM, WTN = BN / WGN, TM = WTM / 32, TN = WTN / 32;
+    constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2, STAGE = A_BYTES + B_BYTES;
+    __shared__ __attribute__((aligned(1024))) char smem[STAGES * STAGE];
+    using PlanA = DmaPlan<BM, A_KC, NW, BK>;
+    using PlanB = DmaPlan<BN, B_KC, NW, BK>;
+    constexpr int PER_TILE = PlanA::PER + PlanB::PER;
+
+    const int T = p.tiles_m * p.tiles_n;
+    int t = blockIdx.x;
+    if ((T & 7) == 0) t = (t & 7) * (T >> 3) + (t >> 3);
+    constexpr int GROUP = 4;
+    const int group_size = GROUP * p.tiles_n;
+    const int g = t / group_size, first_m = g * GROUP;
+    const int gm = min(p.tiles_m - first_m, GROUP);
+    const int m0 = (first_m + (t % group_size) % gm) * BM;
+    const int n0 = ((t % group_size) / gm) * BN;
+
+    const int split = blockIdx.z % p.splits;
+    int bidx = blockIdx.z / p.splits;
+    long long a_off = 0, b_off = 0;
+    const long long c_off = ((long long)split * p.batch + bidx) * p.M * p.N;
+    for (int d = p.batch_ndim - 1; d >= 0; --d) {
+        const int coord = bidx % p.batch_shape[d];
+        bidx /= p.batch_shape[d];
+        a_off += coord * p.a_bs[d];
+        b_off += coord * p.b_bs[d];
+    }
+    float* c = p.c + c_off;
+    const int kbeg = split * p.k_per_split;
+    const int kend = min(p.K, kbeg + p.k_per_split);
+    const int KT = kend > kbeg ? (kend - kbeg) / BK : 0;
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave / WGN, wn = wave % WGN;
+
+    PlanA pa;
+    PlanB pb;
+    pa.init(p.a_sm, p.a_sk, m0, p.M);
+    pb.init(p.b_sn, p.b_sk, n0, p.N);
+    const char* ta = p.a + a_off * 2 + PlanA::origin(p.a_sm, p.a_sk, m0, kbeg);
+    const char* tb = p.b + b_off * 2 + PlanB::origin(p.b_sn, p.b_sk, n0, kbeg);
+    const long long a_step = PlanA::kstep(p.a_sk), b_step = PlanB::kstep(p.b_sk);
+    lds_char* const lds = (lds_char*)smem;
+    // Kernel arguments the epilogue needs are loaded here: a scalar load still
+    // in flight when the loop starts would make every LDS wait in the loop
+    // drain completely (scalar loads return out of order, so the wait-count
+    // pass can no longer count LDS reads precisely).
+    asm volatile("" ::"s"(c), "s"(p.M), "s"(p.N));
+
+    f32x16_t acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    // Prologue: tiles 0 .. STAGES-2 into stages 0 .. STAGES-2.
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s) {
+        if (s < KT) {
+            pa.issue(lds + s * STAGE, ta);
+            pb.issue(lds + s * STAGE + A_BYTES, tb);
+            ta += a_step;
+            tb += b_step;
+        }
+    }
+    int issued = min(KT, STAGES - 1);  // tiles whose loads have been issued
+    u32x4_t af[2][TM], bfr[2][TN];
+    if (KT > 0) {
+        wait_tiles<PER_TILE, STAGES - 2>(issued - 1);
+        lds_barrier();
+#pragma unroll
+        for (int i = 0; i < TM; ++i) af[0][i] = frag<BM, A_KC, BK>(lds, wm * WTM + i * 32, 0);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) bfr[0][j] = frag<BN, B_KC, BK>(lds + A_BYTES, wn * WTN + j * 32, 0);
+    }
+
+    int stage = 0;
+    for (int kt = 0; kt < KT; ++kt) {
+        const lds_char* As = lds + stage * STAGE;
+        const lds_char* Bs = As + A_BYTES;
+        const int next_stage = stage + 1 == STAGES ? 0 : stage + 1;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const int q = ks & 1;
+            if (ks + 1 < KS) {
+#pragma unroll
+                for (int i = 0; i < TM; ++i) af[q ^ 1][i] = frag<BM, A_KC, BK>(As, wm * WTM + i * 32, ks + 1);
+#pragma unroll
+                for (int j = 0; j < TN; ++j) bfr[q ^ 1][j] = frag<BN, B_KC, BK>(Bs, wn * WTN + j * 32, ks + 1);
+            } else if (kt + 1 < KT) {
+                // Tiles issued after kt+1 may stay in flight.
+                wait_tiles<PER_TILE, STAGES - 3>(issued - (kt + 2));
+                lds_barrier();
+                if (issued < KT) {
+                    // The freed stage is the one tile kt-1 used, i.e. (kt + STAGES - 1) % STAGES.
+                    const int fs = next_stage + STAGES - 2 >= STAGES ? next_stage - 2 : next_stage + STAGES - 2;
+                    pa.issue(lds + fs * STAGE, ta);
+                    pb.issue(lds + fs * STAGE + A_BYTES, tb);
+                    ta += a_step;
+                    tb += b_step;
+                    ++issued;
+                }
+                const lds_char* An = lds + next_stage * STAGE;
+#pragma unroll
+                for (int i = 0; i < TM; ++i) af[q ^ 1][i] = frag<BM, A_KC, BK>(An, wm * WTM + i * 32, 0);
+#pragma unroll
+                for (int j = 0; j < TN; ++j) bfr[q ^ 1][j] = frag<BN, B_KC, BK>(An + A_BYTES, wn * WTN + j * 32, 0);
+            }
+            if (ORMI_GEMM_SCHED) __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) Tr::mma(af[q][i], bfr[q][j], acc[i][j]);
+            if (ORMI_GEMM_SCHED) __builtin_amdgcn_sched_barrier(0);
+        }
+        stage = next_stage;
+    }
+
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int col = n0 + wn * WTN + j * 32 + (lane & 31);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (row < p.M && col < p.N) c[(long long)row * p.N + col] = acc[i][j][r];
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------------
+// Interleaved multi-stage GEMM (BK 32, two MFMA k-steps per tile). Same LDS
+// stages and direct loads as gemm_pipe_kernel, but each MFMA of a step is
+// followed by a share of the step's memory instructions — the fragment reads
+// of the next step, then half of the direct loads of tile kt + STAGES - 1 —
+// in a fixed order, so the matrix pipe never waits on a burst of loads and
+// every read is in flight while earlier MFMAs execute. Loads past the last
+// tile re-read the last tile into a stage no step reads, which keeps the
+// per-wave load count of every tile the same and every vmcnt bound a
+// constant: the loop has no branches besides its own.
+//   step 0: MFMAs on k-step 0 | reads of k-step 1 (this stage), loads 0..HALF-1
+//   wait: this wave's loads of tile kt+1 landed, its LDS reads done; barrier
+//   step 1: MFMAs on k-step 1 | reads of k-step 0 (next stage), loads HALF..
+// The barrier publishes tile kt+1 and tells every wave that tile kt-1's
+// stage, refilled during tile kt, has no reads left.
+template <int BMN, bool KC, int BK>
+__device__ __forceinline__ void frag_part(u32x4_t& f, const lds_char* lds, int row0, int ks, int h) {
+    if constexpr (KC) {
+        f = frag<BMN, true, BK>(lds, row0, ks);
+    } else {
+        const int lane = threadIdx.x & 63;
+        const int g = lane >> 4, i = lane & 15;
+        const int nb = row0 + (g & 1) * 16 + 4 * (i & 3);
+        const int k = ks * 16 + (g >> 1) * 8 + h * 4 + (i >> 2);
+        const lds_char* p = lds + k * (BMN * 2) + (((nb >> 3) ^ swz_mn(k)) << 4) + ((nb & 4) << 1);
+        const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4_t*)p);
+        f[2 * h] = (unsigned)(unsigned short)v[0] | ((unsigned)(unsigned short)v[1] << 16);
+        f[2 * h + 1] = (unsigned)(unsigned short)v[2] | ((unsigned)(unsigned short)v[3] << 16);
+    }
+}
+
+template <typename Tr, int BM, int BN, int WGM, int WGN, bool A_KC, bool B_KC>
+struct IlStep {
+    static constexpr int BK = 32, NW = WGM * WGN;
+    static constexpr int WTM = BM / WGM, WTN = BN / WGN, TM = WTM / 32, TN = WTN / 32;
+    static constexpr int A_BYTES = BM * BK * 2;
+    using PlanA = DmaPlan<BM, A_KC, NW, BK>;
+    using PlanB = DmaPlan<BN, B_KC, NW, BK>;
+    static constexpr int PA = PlanA::PER, PB = PlanB::PER, PER_TILE = PA + PB, HALF = PER_TILE / 2;
+    static_assert(PER_TILE % 2 == 0, "loads split evenly over the two steps");
+    static constexpr int RA = A_KC ? 1 : 2, RB = B_KC ? 1 : 2;  // reads per fragment
+    static constexpr int NR = TM * RA + TN * RB;                // reads per step
+    static constexpr int NO = NR + HALF;                        // memory instructions per step
+    static constexpr int NM = TM * TN;                          // MFMAs per step
+
+    // Memory instruction o of a step. Reads come in the order the next step's
+    // MFMAs consume them: A0, B0 .. B(TN-1), A1 .. A(TM-1).
+    __device__ __forceinline__ static void mem_op(int o, int step, u32x4_t (&fa)[TM], u32x4_t (&fb)[TN],
+                                                  const lds_char* rs, int rks, int wm, int wn, lds_char* fs,
+                                                  const char* ta, const char* tb, const PlanA& pa, const PlanB& pb) {
+        if (o < RA) {
+            frag_part<BM, A_KC, BK>(fa[0], rs, wm * WTM, rks, o);
+        } else if (o < RA + TN * RB) {
+            const int j = (o - RA) / RB, h = (o - RA) % RB;
+            frag_part<BN, B_KC, BK>(fb[j], rs + A_BYTES, wn * WTN + j * 32, rks, h);
+        } else if (o < NR) {
+            const int q = o - RA - TN * RB;
+            const int i = 1 + q / RA, h = q % RA;
+            frag_part<BM, A_KC, BK>(fa[i], rs, wm * WTM + i * 32, rks, h);
+        } else {
+            const int d = step * HALF + (o - NR);
+            if (d < PA) pa.issue_one(fs, ta, d);
+            else pb.issue_one(fs + A_BYTES, tb, d - PA);
+        }
+    }
+
+    __device__ __forceinline__ static void run(int step, f32x16_t (&acc)[TM][TN], const u32x4_t (&ua)[TM],
+                                               const u32x4_t (&ub)[TN], u32x4_t (&fa)[TM], u32x4_t (&fb)[TN],
+                                               const lds_char* rs, int rks, int wm, int wn, lds_char* fs,
+                                               const char* ta, const char* tb, const PlanA& pa, const PlanB& pb) {
+#pragma unroll
+        for (int n = 0; n < NM; ++n) {
+            Tr::mma(ua[n / TN], ub[n % TN], acc[n / TN][n % TN]);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int o = n * NO / NM; o < (n + 1) * NO / NM; ++o) {
+                mem_op(o, step, fa, fb, rs, rks, wm, wn, fs, ta, tb, pa, pb);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
+};
+
+template <typename Tr, int BM, int BN, int WGM, int WGN, int STAGES, bool A_KC, bool B_KC>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_il_kernel(GemmParams p) {
+    static_assert(STAGES >= 3 && STAGES <= 5, "3 to 5 stages");
+    using Step = IlStep<Tr, BM, BN, WGM, WGN, A_KC, B_KC>;
+    constexpr int BK = Step::BK, TM = Step::TM, TN = Step::TN, WTM = Step::WTM, WTN = Step::WTN;
+    constexpr int A_BYTES = Step::A_BYTES, STAGE = A_BYTES + BN * BK * 2;
+    constexpr int PER_TILE = Step::PER_TILE, HALF = Step::HALF;
+    __shared__ __attribute__((aligned(1024))) char smem[STAGES * STAGE];
+
+    const int T = p.tiles_m * p.tiles_n;
+    int t = blockIdx.x;
+    if ((T & 7) == 0) t = (t & 7) * (T >> 3) + (t >> 3);
+    constexpr int GROUP = 4;
+    const int group_size = GROUP * p.tiles_n;
+    const int g = t / group_size, first_m = g * GROUP;
+    const int gm = min(p.tiles_m - first_m, GROUP);
+    const int m0 = (first_m + (t % group_size) % gm) * BM;
+    const int n0 = ((t % group_size) / gm) * BN;
+
+    const int split = blockIdx.z % p.splits;
+    int bidx = blockIdx.z / p.splits;
+    long long a_off = 0, b_off = 0;
+    const long long c_off = ((long long)split * p.batch + bidx) * p.M * p.N;
+    for (int d = p.batch_ndim - 1; d >= 0; --d) {
+        const int coord = bidx % p.batch_shape[d];
+        bidx /= p.batch_shape[d];
+        a_off += coord * p.a_bs[d];
+        b_off += coord * p.b_bs[d];
+    }
+    float* c = p.c + c_off;
+    const int kbeg = split * p.k_per_split;
+    const int kend = min(p.K, kbeg + p.k_per_split);
+    const int KT = kend > kbeg ? (kend - kbeg) / BK : 0;
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave / WGN, wn = wave % WGN;
+
+    typename Step::PlanA pa;
+    typename Step::PlanB pb;
+    pa.init(p.a_sm, p.a_sk, m0, p.M);
+    pb.init(p.b_sn, p.b_sk, n0, p.N);
+    const char* ta = p.a + a_off * 2 + Step::PlanA::origin(p.a_sm, p.a_sk, m0, kbeg);
+    const char* tb = p.b + b_off * 2 + Step::PlanB::origin(p.b_sn, p.b_sk, n0, kbeg);
+    const long long a_step = Step::PlanA::kstep(p.a_sk), b_step = Step::PlanB::kstep(p.b_sk);
+    lds_char* const lds = (lds_char*)smem;
+    // Kernel arguments the epilogue needs are loaded here: a scalar load still
+    // in flight when the loop starts would make every LDS wait in the loop
+    // drain completely (scalar loads return out of order).
+    asm volatile("" ::"s"(c), "s"(p.M), "s"(p.N));
+
+    f32x16_t acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    if (KT > 0) {
+        // Prologue: tiles 0 .. STAGES-2 (a tile past the end re-reads the last one).
+        // ta / tb always address tile min(next tile to load, KT - 1).
+#pragma unroll
+        for (int s = 0; s < STAGES - 1; ++s) {
+            pa.issue(lds + s * STAGE, ta);
+            pb.issue(lds + s * STAGE + A_BYTES, tb);
+            if (s + 1 < KT) {
+                ta += a_step;
+                tb += b_step;
+            }
+        }
+        wait_vmcnt<(STAGES - 2) * PER_TILE>();
+        lds_barrier();
+        u32x4_t fa[2][TM], fb[2][TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) fa[0][i] = frag<BM, A_KC, BK>(lds, wm * WTM + i * 32, 0);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) fb[0][j] = frag<BN, B_KC, BK>(lds + A_BYTES, wn * WTN + j * 32, 0);
+
+        int stage = 0, free_stage = STAGES - 1;
+        for (int kt = 0; kt < KT; ++kt) {
+            const int next = stage + 1 == STAGES ? 0 : stage + 1;
+            const lds_char* cur = lds + stage * STAGE;
+            lds_char* fs = lds + free_stage * STAGE;
+            const char* ua = Step::PlanA::uniform(ta);
+            const char* ub = Step::PlanB::uniform(tb);
+            Step::run(0, acc, fa[0], fb[0], fa[1], fb[1], cur, 1, wm, wn, fs, ua, ub, pa, pb);
+            // vmcnt: loads issued after tile kt+1 (STAGES-3 whole tiles and half
+            // of tile kt+STAGES-1) may stay in flight; lgkmcnt(0): own reads done.
+            constexpr int V = (STAGES - 3) * PER_TILE + HALF;
+            __builtin_amdgcn_s_waitcnt((V & 15) | ((V >> 4) << 14) | (7 << 4));
+            lds_barrier();
+            Step::run(1, acc, fa[1], fb[1], fa[0], fb[0], lds + next * STAGE, 0, wm, wn, fs, ua, ub, pa, pb);
+            if (kt + STAGES < KT) {
+                ta += a_step;
+                tb += b_step;
+            }
+            stage = next;
+            free_stage = free_stage + 1 == STAGES ? 0 : free_stage + 1;
+        }
+        // No load may still be writing this workgroup's LDS when it exits.
+        wait_vmcnt<0>();
+    }
+
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int col = n0 + wn * WTN + j * 32 + (lane & 31);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (row < p.M && col < p.N) c[(long long)row * p.N + col] = acc[i][j][r];
+            }
+        }
+    }
+}
+
 // Direct-load 16-bit configurations (ORMI_GEMM_DMA_CFG):
-//   0: 256x256, 2x2 waves (128x128 per wave)   1: 256x256, 2x4 waves (128x64)
-//   2: 256x256, 4x2 waves (64x128)              3: 128x128, 2x2 waves (64x64)
+//   two-stage, BK 64:  0: 256x256, 2x2 waves   1: 256x256, 2x4   2: 256x256, 4x2   3: 128x128, 2x2
+//   multi-stage, BK 32: 4: 256x256, 2x2, 4 stages   5: 256x256, 2x4, 4 stages
+//                       6: 256x256, 2x2, 5 stages   7: 256x256, 4x2, 4 stages
+//   interleaved, BK 32: 8: 256x256, 2x2, 3 stages   9: 256x256, 2x2, 4 stages
+//                       10: 256x256, 2x4, 4 stages  11: 256x256, 4x2, 4 stages
+// The default, 9, measured fastest on MI355X for NN, NT and TN at 4096^3.
 template <typename Tr, int BM, int BN, int WGM, int WGN>
 struct DmaLauncher {
     static constexpr Cfg cfg{BM, BN, 64};
@@ -651,13 +1082,49 @@ struct DmaLauncher {
         else go<false, false>(p, grid);
     }
 };
+template <typename Tr, int BM, int BN, int BK, int WGM, int WGN, int STAGES>
+struct PipeLauncher {
+    static constexpr Cfg cfg{BM, BN, BK};
+    template <bool A_KC, bool B_KC>
+    static void go(const GemmParams& p, dim3 grid) {
+        gemm_pipe_kernel<Tr, BM, BN, BK, WGM, WGN, STAGES, A_KC, B_KC><<<grid, 64 * WGM * WGN>>>(p);
+    }
+    static void run(const GemmParams& p, dim3 grid, bool a_kc, bool b_kc) {
+        if (a_kc && b_kc) go<true, true>(p, grid);
+        else if (a_kc) go<true, false>(p, grid);
+        else if (b_kc) go<false, true>(p, grid);
+        else go<false, false>(p, grid);
+    }
+};
+template <typename Tr, int BM, int BN, int WGM, int WGN, int STAGES>
+struct IlLauncher {
+    static constexpr Cfg cfg{BM, BN, 32};
+    template <bool A_KC, bool B_KC>
+    static void go(const GemmParams& p, dim3 grid) {
+        gemm_il_kernel<Tr, BM, BN, WGM, WGN, STAGES, A_KC, B_KC><<<grid, 64 * WGM * WGN>>>(p);
+    }
+    static void run(const GemmParams& p, dim3 grid, bool a_kc, bool b_kc) {
+        if (a_kc && b_kc) go<true, true>(p, grid);
+        else if (a_kc) go<true, false>(p, grid);
+        else if (b_kc) go<false, true>(p, grid);
+        else go<false, false>(p, grid);
+    }
+};
 template <typename Tr>
 static Cfg cfg_dma(int id) {
     switch (id) {
         case 0: return DmaLauncher<Tr, 256, 256, 2, 2>::cfg;
         case 1: return DmaLauncher<Tr, 256, 256, 2, 4>::cfg;
         case 2: return DmaLauncher<Tr, 256, 256, 4, 2>::cfg;
-        default: return DmaLauncher<Tr, 128, 128, 2, 2>::cfg;
+        case 3: return DmaLauncher<Tr, 128, 128, 2, 2>::cfg;
+        case 4: return PipeLauncher<Tr, 256, 256, 32, 2, 2, 4>::cfg;
+        case 5: return PipeLauncher<Tr, 256, 256, 32, 2, 4, 4>::cfg;
+        case 6: return PipeLauncher<Tr, 256, 256, 32, 2, 2, 5>::cfg;
+        case 7: return PipeLauncher<Tr, 256, 256, 32, 4, 2, 4>::cfg;
+        case 8: return IlLauncher<Tr, 256, 256, 2, 2, 3>::cfg;
+        case 9: return IlLauncher<Tr, 256, 256, 2, 2, 4>::cfg;
+        case 10: return IlLauncher<Tr, 256, 256, 2, 4, 4>::cfg;
+        default: return IlLauncher<Tr, 256, 256, 4, 2, 4>::cfg;
     }
 }
 template <typename Tr>
@@ -666,7 +1133,15 @@ static void run_dma(int id, const GemmParams& p, dim3 grid, bool a_kc, bool b_kc
         case 0: DmaLauncher<Tr, 256, 256, 2, 2>::run(p, grid, a_kc, b_kc); break;
         case 1: DmaLauncher<Tr, 256, 256, 2, 4>::run(p, grid, a_kc, b_kc); break;
         case 2: DmaLauncher<Tr, 256, 256, 4, 2>::run(p, grid, a_kc, b_kc); break;
-        default: DmaLauncher<Tr, 128, 128, 2, 2>::run(p, grid, a_kc, b_kc); break;
+        case 3: DmaLauncher<Tr, 128, 128, 2, 2>::run(p, grid, a_kc, b_kc); break;
+        case 4: PipeLauncher<Tr, 256, 256, 32, 2, 2, 4>::run(p, grid, a_kc, b_kc); break;
+        case 5: PipeLauncher<Tr, 256, 256, 32, 2, 4, 4>::run(p, grid, a_kc, b_kc); break;
+        case 6: PipeLauncher<Tr, 256, 256, 32, 2, 2, 5>::run(p, grid, a_kc, b_kc); break;
+        case 7: PipeLauncher<Tr, 256, 256, 32, 4, 2, 4>::run(p, grid, a_kc, b_kc); break;
+        case 8: IlLauncher<Tr, 256, 256, 2, 2, 3>::run(p, grid, a_kc, b_kc); break;
+        case 9: IlLauncher<Tr, 256, 256, 2, 2, 4>::run(p, grid, a_kc, b_kc); break;
+        case 10: IlLauncher<Tr, 256, 256, 2, 4, 4>::run(p, grid, a_kc, b_kc); break;
+        default: IlLauncher<Tr, 256, 256, 4, 2, 4>::run(p, grid, a_kc, b_kc); break;
     }
 }
 
@@ -769,11 +1244,18 @@ extern "C" int ormi_hip_gemm(const ormi_gemm_desc* d) {
         return ORMI_HIP_OK;
     }
 
-    // Direct-load path: 16-bit, K in whole 64-deep tiles, the mn-contiguous
-    // operand's extent in whole 16-byte chunks.
-    const bool dma = !f32 && env_cfg("ORMI_GEMM_DMA", 1) != 0 && d->K % 64 == 0 && (a_kc || d->M % 8 == 0) &&
-                     (b_kc || d->N % 8 == 0);
-    const int id = dma ? env_cfg("ORMI_GEMM_DMA_CFG", 0) : f32 ? env_cfg("ORMI_GEMM_CFG32", 0) : env_cfg("ORMI_GEMM_CFG16", 0);
+    // Direct-load path: 16-bit, K in whole tiles of the configuration's depth,
+    // the mn-contiguous operand's extent in whole 16-byte chunks.
+    // Per-lane load offsets within one tile are 32-bit: a tile (at most 256
+    // rows of k-contiguous data, or 64 k-rows of mn-contiguous data) spans
+    // less than 4 GB.
+    const long long a_span = a_kc ? 256LL * d->a_stride_m * 2 : 64LL * d->a_stride_k * 2 + 512;
+    const long long b_span = b_kc ? 256LL * d->b_stride_n * 2 : 64LL * d->b_stride_k * 2 + 512;
+    const int dma_id = env_cfg("ORMI_GEMM_DMA_CFG", 9);
+    const int dma_bk = f32 ? 64 : cfg_dma<TrBF16>(dma_id).BK;
+    const bool dma = !f32 && env_cfg("ORMI_GEMM_DMA", 1) != 0 && d->K % dma_bk == 0 && (a_kc || d->M % 8 == 0) &&
+                     (b_kc || d->N % 8 == 0) && a_span < (1LL << 32) && b_span < (1LL << 32);
+    const int id = dma ? dma_id : f32 ? env_cfg("ORMI_GEMM_CFG32", 0) : env_cfg("ORMI_GEMM_CFG16", 0);
     const Cfg cf = dma ? (d->dtype == ORMI_DTYPE_BF16 ? cfg_dma<TrBF16>(id) : cfg_dma<TrF16>(id))
                        : f32 ? cfg32(id) : (d->dtype == ORMI_DTYPE_BF16 ? cfg16<TrBF16>(id) : cfg16<TrF16>(id));
     p.tiles_m = (d->M + cf.BM - 1) / cf.BM;

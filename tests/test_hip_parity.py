@@ -296,6 +296,23 @@ def test_bf16_gemm_vs_oracle(cpu, hip, m, k, n):
     assert np.all(np.abs(got - exact) <= bound)
 
 
+@pytest.mark.parametrize("k", [32, 64, 96, 128, 160, 192, 320, 2048])
+def test_bf16_gemm_k_depths(hip, k):
+    """Short and long K through every layout: pipelines shorter than their stage
+    count, ragged M / N edges (264 x 136 is not a multiple of any tile)."""
+    rng = np.random.default_rng(35 + k)
+    m, n = 264, 136
+    a = bf16_round(rng.normal(0, 1, (m, k)).astype(np.float32))
+    b = bf16_round(rng.normal(0, 1, (k, n)).astype(np.float32))
+    exact = gemm_ref64(a, b)
+    bound = 2 * k * np.finfo(np.float32).eps * (np.abs(a).astype(np.float64) @ np.abs(b))
+    A_n, B_n = T(a, hip, dtype="bfloat16"), T(b, hip, dtype="bfloat16")
+    A_t, B_t = T(a.T.copy(), hip, dtype="bfloat16").transpose(), T(b.T.copy(), hip, dtype="bfloat16").transpose()
+    for name, A, B in (("NN", A_n, B_n), ("NT", A_n, B_t), ("TN", A_t, B_n), ("TT", A_t, B_t)):
+        got = (A @ B).numpy()
+        assert np.all(np.abs(got - exact) <= bound), name
+
+
 def test_gemm_transposed_layouts(cpu, hip):
     """NN, NT, TN, TT through transpose views: the layouts of the forward and the two
     backward GEMMs (reference csrc/core/ops/blas/matmul.cpp:86-124)."""
