@@ -16,6 +16,8 @@ back-to-back launches of pre-built graphs. cpu_baseline: the CPU oracle
 from __future__ import annotations
 
 import argparse
+import collections
+import csv
 import ctypes
 import json
 import math
@@ -130,7 +132,27 @@ def cpu_baseline_c2(target_s: float = 10.0) -> dict:
     }
 
 
+def traffic_from_profile(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary
+    (profiles/hbm_traffic.md, written by `bench.py --pmc-report`), or None."""
+    f = ROOT / "profiles" / "hbm_traffic.md"
+    if not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 4 and cells[0] == kernel:
+            try:
+                return int(cells[3])
+            except ValueError:
+                return None
+    return None
+
+
 def bench_c2(args, ev: Events) -> dict:
+    """Headline workload. A step = build the lazy graph + realize it (one fused
+    kernel). Inputs rotate over 3 resident copies and the last 4 outputs stay
+    alive, so each step reads and writes buffers the 256 MB Infinity Cache does
+    not hold from the step before."""
     from ormi_amd import Tensor
 
     log("C2: generating inputs")
@@ -139,24 +161,42 @@ def bench_c2(args, ev: Events) -> dict:
     for k in range(3):
         xs = x if k == 0 else np.ascontiguousarray(np.roll(x, k, axis=0))
         sets.append((Tensor(xs, "hip"), Tensor(bias, "hip"), Tensor(scale, "hip")))
+    ring = collections.deque(maxlen=4)
     for i in range(args.warmup):
-        c2_graph(*sets[i % 3]).realize()
+        ring.append(c2_graph(*sets[i % 3]).realize())
     ev.sync()
     log("C2: timed steps")
     t0 = time.perf_counter()
     for i in range(args.steps):
-        c2_graph(*sets[i % 3]).realize()
+        ring.append(c2_graph(*sets[i % 3]).realize())
     ev.sync()
     step_s = (time.perf_counter() - t0) / args.steps
-    kernel_ms = timed_launches(ev, lambda i: c2_graph(*sets[i % 3]), max(args.steps, 20))
+    ring.clear()
+    log("C2: kernel timing (HIP events)")
+    n = max(args.steps, 20)
+    kernel_ms = timed_launches(ev, lambda i: c2_graph(*sets[i % 3]), n)
     nbytes = c2_bytes()
+    achieved = nbytes / (kernel_ms * 1e-3) / 1e9
     return {
         "step_s": step_s,
         "value": nbytes / step_s / 1e9,
-        "roofline": {"bound": "hbm", "achieved": round(nbytes / (kernel_ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(nbytes / (kernel_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel_us": round(kernel_ms * 1e3, 2), "bytes_per_launch": nbytes},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile("c2_fused_map"),
+                     "kernel_us": round(kernel_ms * 1e3, 2), "bytes_per_launch": nbytes, "launches_timed": n},
     }
+
+
+def bench_copy(args, ev: Events) -> dict:
+    """Calibration kernel for the --pmc traffic figures: y = -x over (8192, 4096)
+    fp32, a fused map that reads 128 MiB and writes 128 MiB."""
+    from ormi_amd import Tensor
+
+    x = np.random.default_rng(7).normal(0, 1, (8192, 4096)).astype(np.float32)
+    X = [Tensor(x, "hip"), Tensor(x[::-1].copy(), "hip"), Tensor(x[:, ::-1].copy(), "hip")]
+    (-X[0]).realize()
+    ms = timed_launches(ev, lambda i: -X[i % 3], max(args.steps, 20))
+    nbytes = 2 * x.nbytes
+    return {"us": round(ms * 1e3, 2), "GB/s": round(nbytes / ms / 1e6, 1), "bytes": nbytes}
 
 
 def bench_c3(ev: Events, n: int) -> dict:
@@ -294,6 +334,60 @@ def bench_c5(ev: Events, steps: int) -> dict:
             "frac_fp32": round(flops / ms / 1e9 / FP32_PEAK_TFLOPS, 4), "loss_first": first, "loss_last": last}
 
 
+def _pmc_rows(run_dir: Path, counter: str):
+    """(kernel name, value) per dispatch from the rocprofv3 counter CSVs under run_dir."""
+    rows = []
+    for f in sorted(run_dir.rglob("*counter_collection.csv")):
+        with open(f, newline="") as fh:
+            for r in csv.DictReader(fh):
+                if r.get("Counter_Name", "").strip() == counter:
+                    rows.append((r.get("Kernel_Name", "").strip(), float(r.get("Counter_Value", "nan"))))
+    return rows
+
+
+def _pmc_kernel(run_dir: Path, counter: str):
+    """Name, dispatch count and mean counter value of the most-dispatched ormi_ kernel."""
+    by = collections.defaultdict(list)
+    for name, v in _pmc_rows(run_dir, counter):
+        if name.startswith("ormi_"):
+            by[name].append(v)
+    if not by:
+        raise SystemExit(f"--pmc-report: no ormi_ kernel with counter {counter} under {run_dir}")
+    name = max(by, key=lambda k: len(by[k]))
+    return name, len(by[name]), sum(by[name]) / len(by[name])
+
+
+def pmc_report(pmc_dir: Path, out: Path, cmd: str) -> None:
+    """Turn `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE` runs into HBM bytes per
+    launch. Runs live in pmc_dir/<label>_<COUNTER>/; label "copy" is the calibration
+    kernel (y = -x over 8192x4096 fp32: 128 MiB read, 128 MiB written), whose
+    counters scale every other kernel's KiB figures to bytes."""
+    alg = {"copy": (2 ** 27, 2 ** 27), "c2_fused_map": (c2_bytes() - 2 ** 27, 2 ** 27)}
+    got = {}
+    for label in alg:
+        f_name, f_n, f_kib = _pmc_kernel(pmc_dir / f"{label}_FETCH_SIZE", "FETCH_SIZE")
+        w_name, w_n, w_kib = _pmc_kernel(pmc_dir / f"{label}_WRITE_SIZE", "WRITE_SIZE")
+        got[label] = (f_name, f_n, f_kib, w_kib)
+    sf = alg["copy"][0] / (got["copy"][2] * 1024)
+    sw = alg["copy"][1] / (got["copy"][3] * 1024)
+    lines = [
+        "# HBM traffic per launch (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, one run each)",
+        "",
+        f"Command: `{cmd}`",
+        "",
+        f"Scale factors from the copy kernel (y = -x, 8192x4096 fp32, 134217728 B read + 134217728 B written): "
+        f"fetch {sf:.4f}, write {sw:.4f} (algorithmic bytes / (KiB x 1024)).",
+        "",
+        "| kernel | fetch KiB/dispatch | write KiB/dispatch | traffic bytes/launch | algorithmic bytes/launch | dispatches | name |",
+        "|---|---|---|---|---|---|---|",
+    ]
+    for label, (name, n, fk, wk) in got.items():
+        traffic = int(round(fk * 1024 * sf + wk * 1024 * sw))
+        lines.append(f"| {label} | {fk:.1f} | {wk:.1f} | {traffic} | {sum(alg[label])} | {n} | {name} |")
+    out.write_text("\n".join(lines) + "\n")
+    print(out.read_text())
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -301,10 +395,19 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-extra", action="store_true", help="only the headline workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", choices=["c1", "c3", "c4", "c5", "copy"],
+                    help="run one non-headline workload and print its figures (profiling runs)")
+    ap.add_argument("--pmc-report", nargs=2, metavar=("PMC_DIR", "OUT_MD"),
+                    help="summarize rocprofv3 --pmc runs into a traffic table (no GPU needed)")
     args = ap.parse_args()
+    if args.pmc_report:
+        pmc_report(Path(args.pmc_report[0]), Path(args.pmc_report[1]),
+                   "rocprofv3 --pmc FETCH_SIZE|WRITE_SIZE -d <PMC_DIR>/<label>_<COUNTER> -o run --output-format csv "
+                   "-- python3 bench.py --only copy | --no-extra --no-cpu, --steps 5 --warmup 1")
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
-              "multi-GPU sharding is described in DESIGN.md, not implemented.", file=sys.stderr)
+              "the multi-GPU sharding plan is a design note, not an implemented path.", file=sys.stderr)
         sys.exit(2)
 
     import ormi_amd
@@ -312,10 +415,17 @@ def main():
     if not ormi_amd.ormi_backend.hip_available():
         raise SystemExit("bench.py: HIP device unavailable (no GPU visible); refusing to report a number.")
     ev = Events()
+    if args.only:
+        n = max(10, min(args.steps, 30))
+        res = {"copy": lambda: bench_copy(args, ev), "c1": lambda: bench_c1(ev, n), "c3": lambda: bench_c3(ev, n),
+               "c4": lambda: bench_c4(ev, n), "c5": lambda: bench_c5(ev, max(3, min(args.steps // 10, 10)))}[args.only]()
+        print(json.dumps({"only": args.only, **res}), flush=True)
+        return
     main_res = bench_c2(args, ev)
     extra = {}
     if not args.no_extra:
         n = max(10, min(args.steps, 30))
+        extra["copy_calibration_neg_8192x4096"] = bench_copy(args, ev)
         extra["C1_fused_pointwise_rowsum_1024"] = bench_c1(ev, n)
         extra["C3_reductions_16384x8192"] = bench_c3(ev, n)
         extra["C4_gemm"] = bench_c4(ev, n)

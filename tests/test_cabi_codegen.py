@@ -1,0 +1,154 @@
+"""CPU-side checks of the drop-in boundary and the hipRTC code generator.
+
+No GPU is needed: libormi_hip.so loads and reports "no device", hipRTC compiles
+generated kernels to gfx950 code objects offline, and the kernel planner runs on
+graphs whose leaves live on the CPU oracle device.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from conftest import header_functions
+
+ORMI_HIP_OK, ORMI_HIP_ERR_NO_DEVICE, ORMI_HIP_ERR_INVALID, ORMI_HIP_ERR_COMPILE, ORMI_HIP_ERR_UNSUPPORTED = 0, 2, 3, 4, 5
+
+
+def test_library_exports_every_header_symbol(cabi):
+    names = header_functions()
+    assert len(names) >= 20
+    missing = [n for n in names if not hasattr(cabi, n)]
+    assert not missing, f"declared in include/ormi_hip.h but not exported: {missing}"
+
+
+def test_no_gpu_reports_no_device(cabi):
+    """Without a GPU the device is absent the way a throwing CUDAAllocator makes
+    CUDA absent (reference csrc/tests/test_utils.h:17-21)."""
+    import os
+
+    if os.path.exists("/dev/kfd"):
+        pytest.skip("a GPU is visible")
+    n = ctypes.c_int(-1)
+    assert cabi.ormi_hip_device_count(ctypes.byref(n)) == ORMI_HIP_OK and n.value == 0
+    assert cabi.ormi_hip_init(0) == ORMI_HIP_ERR_NO_DEVICE
+    assert b"no GPU" in cabi.ormi_hip_last_error()
+
+
+def test_argument_errors_before_device_use(cabi):
+    assert cabi.ormi_hip_device_count(None) == ORMI_HIP_ERR_INVALID
+    assert cabi.ormi_hip_malloc(None, 16) == ORMI_HIP_ERR_INVALID
+    assert cabi.ormi_hip_fill(None, None, 4, 8) == ORMI_HIP_ERR_INVALID
+    assert cabi.ormi_hip_convert(None, 0, None, 0, 4) == ORMI_HIP_ERR_INVALID
+    assert cabi.ormi_hip_gemm(None) == ORMI_HIP_ERR_INVALID
+    assert b"null" in cabi.ormi_hip_last_error()
+    # Zero-size work is a no-op that succeeds, as an empty launch is.
+    assert cabi.ormi_hip_fill(None, None, 4, 0) == ORMI_HIP_OK
+    assert cabi.ormi_hip_memcpy_h2d(None, None, 0) == ORMI_HIP_OK
+
+
+class GemmDesc(ctypes.Structure):
+    _fields_ = [("dtype", ctypes.c_int), ("M", ctypes.c_int), ("N", ctypes.c_int), ("K", ctypes.c_int),
+                ("a", ctypes.c_void_p), ("a_stride_m", ctypes.c_int64), ("a_stride_k", ctypes.c_int64),
+                ("b", ctypes.c_void_p), ("b_stride_k", ctypes.c_int64), ("b_stride_n", ctypes.c_int64),
+                ("c", ctypes.c_void_p), ("batch_ndim", ctypes.c_int), ("batch_shape", ctypes.c_int * 4),
+                ("a_batch_stride", ctypes.c_int64 * 4), ("b_batch_stride", ctypes.c_int64 * 4)]
+
+
+def test_gemm_descriptor_validation(cabi):
+    d = GemmDesc(dtype=0, M=-1, N=4, K=4)
+    assert cabi.ormi_hip_gemm(ctypes.byref(d)) == ORMI_HIP_ERR_INVALID
+    d = GemmDesc(dtype=5, M=4, N=4, K=4)  # int64 is not a GEMM input type
+    assert cabi.ormi_hip_gemm(ctypes.byref(d)) == ORMI_HIP_ERR_UNSUPPORTED
+    d = GemmDesc(dtype=0, M=4, N=4, K=4, batch_ndim=5)
+    assert cabi.ormi_hip_gemm(ctypes.byref(d)) == ORMI_HIP_ERR_INVALID
+    d = GemmDesc(dtype=0, M=0, N=4, K=4)  # empty output: nothing to do
+    assert cabi.ormi_hip_gemm(ctypes.byref(d)) == ORMI_HIP_OK
+
+
+def _compile_only(cabi, src: str, opts):
+    arr = (ctypes.c_char_p * len(opts))(*[o.encode() for o in opts])
+    size = ctypes.c_size_t(0)
+    rc = cabi.ormi_hip_rtc_compile_only(src.encode(), b"gfx950", arr, len(opts), ctypes.byref(size))
+    return rc, size.value
+
+
+def test_rtc_compile_only_and_compile_errors(cabi, ob):
+    opts = ob._rtc_options()
+    rc, size = _compile_only(cabi, 'extern "C" __global__ void k(float* o) { o[threadIdx.x] = 1.0f; }', opts)
+    assert rc == ORMI_HIP_OK and size > 0
+    rc, _ = _compile_only(cabi, 'extern "C" __global__ void k(float* o) { o[threadIdx.x] = undefined_name; }', opts)
+    assert rc == ORMI_HIP_ERR_COMPILE
+    assert b"undefined_name" in cabi.ormi_hip_last_error()
+
+
+def test_fastdiv_matches_integer_division(ob):
+    rng = np.random.default_rng(0)
+    divisors = [1, 2, 3, 7, 64, 1000, 4096, 8191, 65537, 2 ** 31 - 1, 2 ** 31]
+    divisors += [int(v) for v in rng.integers(1, 2 ** 31, 20)]
+    for d in divisors:
+        m, s = ob._fastdiv(d)
+        n = np.concatenate([rng.integers(0, 2 ** 31, 2000, dtype=np.uint64),
+                            np.array([0, 1, d - 1, d, d + 1, 2 ** 31 - 1], dtype=np.uint64) % (2 ** 31)])
+        q = (((n * np.uint64(m)) >> np.uint64(32)) + n) >> np.uint64(s)
+        assert np.array_equal(q, n // np.uint64(d)), d
+
+
+# ----------------------------------------------------------- code generator
+def _cpu(x):
+    from ormi_amd import Tensor
+
+    return Tensor(np.asarray(x, np.float32), "cpu")
+
+
+def test_generated_map_kernel_structure(ob, cpu, cabi):
+    """The C2 chain is one kernel with 128-bit operand loads, the broadcast
+    operands read per row / per column (no per-element div/mod against literal
+    sizes as in reference compiler.cu:76-101), and it compiles for gfx950."""
+    X, B, S = _cpu(np.zeros((64, 256))), _cpu(np.zeros(256)), _cpu(np.zeros((64, 1)))
+    z = ((X + B) * S).tanh() * X.sigmoid() - 0.1 * X * X
+    d = ob._plan_kernel(z._node)
+    src = d["source"]
+    assert d["plan"].startswith("map") and "vec=4" in d["plan"]
+    assert src.count("ormi_f4*") >= 3  # x and bias loads, the output store
+    for literal in ("256", "64)"):
+        assert f"G = {literal}" not in src
+    assert "tanhf" in src or "ormi_tanh" in src
+    rc, size = _compile_only(cabi, src, ob._rtc_options())
+    assert rc == ORMI_HIP_OK, cabi.ormi_hip_last_error()
+    assert size > 0
+
+
+def test_kernel_source_is_shape_independent(ob, cpu):
+    """Sizes and strides are arguments: the same chain over another shape of the
+    same structure generates the same kernel (one cache entry)."""
+    def plan(r, c):
+        X, B = _cpu(np.zeros((r, c))), _cpu(np.zeros(c))
+        return ob._plan_kernel(((X + B) * 2.0).exp()._node)
+
+    a, b = plan(64, 128), plan(512, 4096)
+    assert a["name"] == b["name"] and a["source"] == b["source"]
+    assert plan(64, 128)["name"] != ob._plan_kernel((_cpu(np.zeros((64, 128))) * 2.0).exp()._node)["name"]
+
+
+@pytest.mark.parametrize("axes,kind", [((1,), "row"), ((0,), "col")])
+def test_generated_reduction_kernels_compile(ob, cpu, cabi, axes, kind):
+    x = _cpu(np.zeros((1024, 2048)))
+    for red in ("sum", "max", "argmax"):
+        node = getattr(ob, red)((x * 2.0)._node, list(axes), False)
+        d = ob._plan_kernel(node)
+        assert kind in d["plan"], d["plan"]
+        rc, _ = _compile_only(cabi, d["source"], ob._rtc_options())
+        assert rc == ORMI_HIP_OK, (red, cabi.ormi_hip_last_error())
+        if d["two_pass"]:
+            rc, _ = _compile_only(cabi, d["second_source"], ob._rtc_options())
+            assert rc == ORMI_HIP_OK, (red, cabi.ormi_hip_last_error())
+
+
+def test_long_axis_reduction_is_two_pass(ob, cpu):
+    """A global reduction (few outputs, long axis) is split across work-groups
+    and finished by a second kernel in part order: deterministic, no atomics
+    (the reference's atomicAdd per element, cuda/kernels/reduce/sum.cu:65)."""
+    x = _cpu(np.zeros((4096, 4096)))
+    d = ob._plan_kernel(ob.sum(x._node, [0, 1], False))
+    assert d["two_pass"] and d["workspace_bytes"] > 0
+    assert "atomic" not in d["source"] and "atomic" not in d["second_source"]
