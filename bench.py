@@ -69,13 +69,27 @@ class Events:
 
 
 def timed_launches(ev: Events, make, n: int) -> float:
-    """Average ms per realize over n back-to-back realizations of pre-built graphs."""
-    graphs = [make(i) for i in range(n)]
+    """Average ms per iteration over n back-to-back realizations of pre-built
+    graphs (make(i) returns a Tensor or a list of Tensors to realize). A first
+    set of n graphs is realized and dropped untimed, so the allocator's pool
+    already holds every output block the timed set needs (steady state, as in a
+    training loop): the timed region issues launches, not hipMalloc calls."""
+    def as_list(g):
+        return g if isinstance(g, (list, tuple)) else [g]
+
+    warm = [as_list(make(i)) for i in range(n)]
+    for gs in warm:
+        for g in gs:
+            g.realize()
+    ev.sync()
+    del warm
+    graphs = [as_list(make(i)) for i in range(n)]
     ev.sync()
     a, b = ev.new(), ev.new()
     ev.record(a)
-    for g in graphs:
-        g.realize()
+    for gs in graphs:
+        for g in gs:
+            g.realize()
     ev.record(b)
     return ev.elapsed_ms(a, b) / n
 
@@ -225,6 +239,9 @@ def bench_c3(ev: Events, n: int) -> dict:
 
 
 def bench_c1(ev: Events, n: int) -> dict:
+    """C1: y = sum(relu(a*b + c) * 0.5, axis=1) and the gradients of sum(y) with
+    respect to a, b, c. Kernel figures come from pre-built graphs; the step
+    figure is the host-inclusive loop (graph build + backward + realize)."""
     from ormi_amd import Tensor
 
     rng = np.random.default_rng(0)
@@ -234,31 +251,26 @@ def bench_c1(ev: Events, n: int) -> dict:
     def fwd(i):
         return ((A * B + C).relu() * 0.5).sum(1)
 
-    fwd(0).realize()
-    ms_f = timed_launches(ev, fwd, n)
-
-    def grads():
+    def grads(i):
         for t in (A, B, C):
             t.zero_grad()
-        y = fwd(0)
-        y.sum().backward()
+        fwd(i).sum().backward()
         return [A.grad, B.grad, C.grad]
 
-    [g.realize() for g in grads()]
-    gs = [grads() for _ in range(n)]
+    ms_f = timed_launches(ev, fwd, n)
+    ms_b = timed_launches(ev, grads, n)
     ev.sync()
-    e0, e1 = ev.new(), ev.new()
-    ev.record(e0)
-    for trio in gs:
-        for g in trio:
-            g.realize()
-    ev.record(e1)
-    ms_b = ev.elapsed_ms(e0, e1) / n
+    t0 = time.perf_counter()
+    for i in range(n):
+        [g.realize() for g in grads(i)]
+    ev.sync()
+    step_ms = (time.perf_counter() - t0) / n * 1e3
     fb, bb = 12587008, 50331648
     return {"fwd_us": round(ms_f * 1e3, 2), "fwd_GB/s": round(fb / ms_f / 1e6, 1),
             "bwd_us": round(ms_b * 1e3, 2), "bwd_GB/s": round(bb / ms_b / 1e6, 1),
-            "note": "fwd one fused reduce kernel (incl. the y.sum() realize of forward y in bwd); "
-                    "bwd three fused kernels (one per gradient root)"}
+            "bwd_step_wall_us": round(step_ms * 1e3, 1),
+            "note": "fwd: one fused reduce kernel; bwd: three fused kernels, one per gradient root "
+                    "(50,331,648 B); bwd_step_wall_us adds building the graphs and the backward pass on the host"}
 
 
 def bench_c4(ev: Events, n: int) -> dict:

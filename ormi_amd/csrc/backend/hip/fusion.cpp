@@ -47,7 +47,7 @@ namespace ormi::hip {
         RegisterLowering l_cos(OpEnum::COS, [](A v) { return "cosf(" + v[0] + ")"; });
         RegisterLowering l_relu(OpEnum::RELU, [](A v) { return "ormi_relu(" + v[0] + ")"; });
         RegisterLowering l_step(OpEnum::STEP, [](A v) { return "ormi_step(" + v[0] + ")"; });
-        RegisterLowering l_tanh(OpEnum::TANH, [](A v) { return "tanhf(" + v[0] + ")"; });
+        RegisterLowering l_tanh(OpEnum::TANH, [](A v) { return "ormi_tanh(" + v[0] + ")"; });
         RegisterLowering l_tanhg(OpEnum::TANH_GRAD, [](A v) { return "ormi_tanh_grad(" + v[0] + ")"; });
         RegisterLowering l_sig(OpEnum::SIGMOID, [](A v) { return "ormi_sigmoid(" + v[0] + ")"; });
         RegisterLowering l_sigg(OpEnum::SIGMOID_GRAD, [](A v) { return "ormi_sigmoid_grad(" + v[0] + ")"; });

@@ -140,6 +140,35 @@ def test_pointwise_ops_match_oracle(cpu, hip):
         np.testing.assert_allclose(outs[0], outs[1], rtol=2e-6, atol=1e-6)
 
 
+def _ulp_error(got, truth64):
+    ulp = np.spacing(np.abs(truth64).astype(np.float32)).astype(np.float64)
+    return np.abs(got.astype(np.float64) - truth64) / ulp
+
+
+def test_device_tanh_sigmoid_accuracy(cpu, hip):
+    """The device tanh and sigmoid (hardware exp/rcp plus a fitted polynomial)
+    stay within 3 ulp of float64 over a dense sweep, and within rtol 1e-6 of the
+    oracle (glibc) with no absolute floor."""
+    rng = np.random.default_rng(31)
+    x = np.concatenate([np.linspace(-12, 12, 2_000_001, dtype=np.float32),
+                        rng.standard_normal(1_000_000).astype(np.float32),
+                        np.float32(0.625) + np.arange(-512, 512, dtype=np.float32) * np.float32(2 ** -24)])
+    t = T(x, hip).tanh().numpy()
+    assert _ulp_error(t, np.tanh(x.astype(np.float64))).max() <= 3.0
+    np.testing.assert_allclose(t, T(x, cpu).tanh().numpy(), rtol=1e-6, atol=0)
+    xs = np.concatenate([x, np.linspace(-80, 30, 1_000_001, dtype=np.float32)])
+    s = T(xs, hip).sigmoid().numpy()
+    truth = 1.0 / (1.0 + np.exp(-xs.astype(np.float64)))
+    assert _ulp_error(s, truth).max() <= 3.0
+    np.testing.assert_allclose(s, T(xs, cpu).sigmoid().numpy(), rtol=1e-6, atol=0)
+    special = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-30, -1e-30, 200.0, -200.0], np.float32)
+    ts = T(special, hip).tanh().numpy()
+    assert np.array_equal(np.signbit(ts[:2]), [False, True]) and ts[0] == 0 and ts[1] == 0
+    assert ts[2] == 1 and ts[3] == -1 and np.isnan(ts[4]) and ts[5] == np.float32(1e-30) and ts[7] == 1 and ts[8] == -1
+    ss = T(special, hip).sigmoid().numpy()
+    assert ss[0] == 0.5 and ss[2] == 1 and ss[3] == 0 and np.isnan(ss[4]) and ss[7] == 1 and ss[8] == 0
+
+
 def test_views_and_strides_as_leaves(cpu, hip):
     rng = np.random.default_rng(22)
     x = rng.standard_normal((16, 24)).astype(np.float32)
