@@ -334,6 +334,9 @@ namespace ormi::hip {
                         o << ind << "const float s" << L << " = " << to_f32(e.leaves[L].dtype, "L" + std::to_string(L) + "[0]") << ";\n";
             }
 
+            // Value names of expr.roots after the last eval().
+            std::vector<std::string> root_names;
+
             // SSA evaluation for vector element k: leaf values come from
             // x<L>[u][k] (or the hoisted scalar). Returns the root value name.
             std::string eval(std::ostringstream& o, const std::string& ind, const std::string& u, const std::string& k) {
@@ -356,6 +359,8 @@ namespace ormi::hip {
                     name[id] = "t" + std::to_string(i);
                     o << ind << "const float " << name[id] << " = " << expr << ";\n";
                 }
+                root_names.clear();
+                for (int r : e.roots) root_names.push_back(name[r]);
                 return name[e.root];
             }
 
@@ -421,6 +426,7 @@ namespace ormi::hip {
             s << '|';
             for (const auto& in : g.e.insts) s << (int)in.op << ',' << in.a << ',' << in.b << ',' << (int)in.cast << ';';
             s << g.e.root;
+            for (int r : g.e.roots) s << ',' << r;
             return s.str();
         }
 
@@ -474,6 +480,14 @@ namespace ormi::hip {
 
     // ------------------------------------------------------------------ map --
     KernelLaunch plan_map(const Expr& expr, const std::vector<int>& shape, void* out, DType out_dtype, int cu) {
+        return plan_map_multi(expr, shape, {out}, {out_dtype}, cu);
+    }
+
+    KernelLaunch plan_map_multi(const Expr& expr, const std::vector<int>& shape, const std::vector<void*>& outs,
+                                const std::vector<DType>& out_dtypes, int cu) {
+        if (outs.size() != expr.roots.size() || outs.size() != out_dtypes.size() || outs.empty())
+            throw std::runtime_error("HIP codegen: one output buffer and dtype per root.");
+        const size_t nout = outs.size();
         const Tuning& tn = tuning();
         const int block = 256, unroll = tn.map_unroll;
         Gen g(expr);
@@ -487,7 +501,8 @@ namespace ormi::hip {
         }
         const int n = (int)g.c.dims.size();
         g.choose_vec(n - 1);
-        if (!vector_dtype(out_dtype) || ((uintptr_t)out % 16) != 0) g.vec = 1;
+        for (size_t r = 0; r < nout; ++r)
+            if (!vector_dtype(out_dtypes[r]) || ((uintptr_t)outs[r] % 16) != 0) g.vec = 1;
         long long numel = 1;
         for (auto& d : g.c.dims) numel *= d.size;
         const long long G = numel / g.vec;
@@ -497,8 +512,11 @@ namespace ormi::hip {
         // The grid-stride cursor reaches G + grid * tile before the loop exits.
         g.choose_idx(G + grid * tile);
 
+        // A single output keeps the name "out"; several are out0, out1, ...
+        auto out_name = [&](size_t r) { return nout == 1 ? std::string("out") : "out" + std::to_string(r); };
         KernelLaunch k;
-        g.args.ptr(std::string(storage_type(out_dtype)) + "* __restrict__ out", out);
+        for (size_t r = 0; r < nout; ++r)
+            g.args.ptr(std::string(storage_type(out_dtypes[r])) + "* __restrict__ " + out_name(r), outs[r]);
         g.declare_leaves();
         g.args.i64("G", G);
         g.declare_dims();
@@ -507,6 +525,7 @@ namespace ormi::hip {
         {
             std::ostringstream plan;
             plan << "map ndim=" << n << " vec=" << g.vec << " idx=" << (g.idx32 ? 32 : 64) << " groups=" << G << " unroll=" << unroll;
+            if (nout > 1) plan << " outputs=" << nout;
             k.plan = plan.str();
         }
         resolve(g, "map", block, k, [&] {
@@ -533,23 +552,27 @@ namespace ormi::hip {
             }
             b << "    }\n";
             b << "#pragma unroll\n    for (int u = 0; u < " << unroll << "; ++u) {\n";
-            b << "      float res[" << V << "];\n";
+            auto res = [&](size_t r) { return nout == 1 ? std::string("res") : "res" + std::to_string(r); };
+            for (size_t r = 0; r < nout; ++r) b << "      float " << res(r) << "[" << V << "];\n";
             b << "#pragma unroll\n      for (int k = 0; k < " << V << "; ++k) {\n";
-            const std::string root = g.eval(b, "        ", "u", "k");
-            b << "        res[k] = " << root << ";\n      }\n";
+            g.eval(b, "        ", "u", "k");
+            for (size_t r = 0; r < nout; ++r) b << "        " << res(r) << "[k] = " << g.root_names[r] << ";\n";
+            b << "      }\n";
             b << "      if (gi[u] < (" << t << ")G) {\n";
             const bool nt = tn.map_nt_stores;
-            if (V == 4) {
-                const bool f32 = out_dtype == DType::Float32;
-                const char* vt = f32 ? "ormi_f4" : "ormi_u16x4";
-                std::string val = std::string(vt) + "{";
-                for (int q = 0; q < 4; ++q) val += (q ? ", " : "") + from_f32(out_dtype, "res[" + std::to_string(q) + "]");
-                val += "}";
-                const std::string addr = std::string("(") + vt + "*)(out + gi[u] * 4)";
-                if (nt) b << "        __builtin_nontemporal_store(" << val << ", " << addr << ");\n";
-                else b << "        *" << addr << " = " << val << ";\n";
-            } else {
-                b << "        out[gi[u]] = " << from_f32(out_dtype, "res[0]") << ";\n";
+            for (size_t r = 0; r < nout; ++r) {
+                const DType odt = out_dtypes[r];
+                if (V == 4) {
+                    const char* vt = odt == DType::Float32 ? "ormi_f4" : "ormi_u16x4";
+                    std::string val = std::string(vt) + "{";
+                    for (int q = 0; q < 4; ++q) val += (q ? ", " : "") + from_f32(odt, res(r) + "[" + std::to_string(q) + "]");
+                    val += "}";
+                    const std::string addr = std::string("(") + vt + "*)(" + out_name(r) + " + gi[u] * 4)";
+                    if (nt) b << "        __builtin_nontemporal_store(" << val << ", " << addr << ");\n";
+                    else b << "        *" << addr << " = " << val << ";\n";
+                } else {
+                    b << "        " << out_name(r) << "[gi[u]] = " << from_f32(odt, res(r) + "[0]") << ";\n";
+                }
             }
             b << "      }\n    }\n  }\n";
         });

@@ -115,46 +115,60 @@ namespace ormi::hip {
     }
 
     Expr build_expr(const NodePtr& root, const std::vector<int>& shape, bool plan_only) {
+        return build_expr_multi({root}, shape, plan_only);
+    }
+
+    Expr build_expr_multi(const std::vector<NodePtr>& roots, const std::vector<int>& shape, bool plan_only) {
         Expr e;
         std::unordered_map<Node*, int> value_of;
-        std::vector<std::pair<NodePtr, int>> order;  // interior nodes in post-order
-        // Post-order DFS over the region: leaves get ids as first seen, interior
-        // nodes after all their operands.
+        std::unordered_set<Node*> root_set;
+        for (const auto& r : roots) root_set.insert(r.get());
+        // Post-order DFS over the union of the roots' regions: leaves get ids as
+        // first seen, interior nodes after all their operands. A node shared by
+        // several roots (or a root inside another root's region) is one value.
         struct Frame { NodePtr n; size_t next; };
         std::vector<Frame> stack;
-        auto is_interior = [&](const NodePtr& n) { return n == root ? fusible_root(*n) : fusible_interior(*n); };
+        auto is_interior = [&](const NodePtr& n) {
+            return root_set.count(n.get()) ? fusible_root(*n) : fusible_interior(*n);
+        };
         auto visit_leaf = [&](const NodePtr& n) {
             const int id = (int)e.leaves.size();
             e.leaves.push_back(make_leaf(n, shape, plan_only));
             value_of[n.get()] = id;
         };
-        if (!is_interior(root)) {
+        if (roots.size() == 1 && !is_interior(roots[0])) {
             // A realized node (or a reduction input that is already a buffer):
             // the tape is the identity on one leaf.
-            visit_leaf(root);
+            visit_leaf(roots[0]);
             e.root = 0;
+            e.roots = {0};
             return e;
         }
         std::vector<NodePtr> interior_post;
-        std::unordered_set<Node*> on_stack{root.get()};
-        stack.push_back({root, 0});
-        while (!stack.empty()) {
-            Frame& f = stack.back();
-            if (f.next < f.n->parents.size()) {
-                NodePtr p = f.n->parents[f.next++];
-                if (value_of.count(p.get()) || on_stack.count(p.get())) continue;
-                if (!p->is_realized() && is_interior(p)) {
-                    on_stack.insert(p.get());
-                    stack.push_back({p, 0});
+        std::unordered_set<Node*> on_stack;
+        for (const auto& root : roots) {
+            if (!is_interior(root)) throw std::runtime_error("HIP codegen: a grouped root is not an element-wise node.");
+            if (value_of.count(root.get())) continue;  // inside an earlier root's region
+            on_stack.insert(root.get());
+            stack.push_back({root, 0});
+            while (!stack.empty()) {
+                Frame& f = stack.back();
+                if (f.next < f.n->parents.size()) {
+                    NodePtr p = f.n->parents[f.next++];
+                    if (value_of.count(p.get()) || on_stack.count(p.get())) continue;
+                    if (!p->is_realized() && is_interior(p)) {
+                        on_stack.insert(p.get());
+                        stack.push_back({p, 0});
+                    } else {
+                        if (!p->is_realized()) throw std::runtime_error("HIP codegen: region input was not realized first.");
+                        visit_leaf(p);
+                    }
                 } else {
-                    if (!p->is_realized()) throw std::runtime_error("HIP codegen: region input was not realized first.");
-                    visit_leaf(p);
+                    interior_post.push_back(f.n);
+                    value_of[f.n.get()] = -1;  // assigned below
+                    on_stack.erase(f.n.get());
+                    stack.pop_back();
                 }
-            } else {
-                interior_post.push_back(f.n);
-                value_of[f.n.get()] = -1;  // assigned below
-                on_stack.erase(f.n.get());
-                stack.pop_back();
             }
         }
         const int nleaves = (int)e.leaves.size();
@@ -167,7 +181,8 @@ namespace ormi::hip {
             if (n->op == OpEnum::CAST) in.cast = std::get<CastAttrs>(n->attrs).dtype;
             e.insts.push_back(in);
         }
-        e.root = value_of.at(root.get());
+        for (const auto& r : roots) e.roots.push_back(value_of.at(r.get()));
+        e.root = e.roots[0];
         return e;
     }
 }

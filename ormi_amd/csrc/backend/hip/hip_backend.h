@@ -48,10 +48,12 @@ namespace ormi::hip {
     };
 
     // Values 0..leaves-1 are leaves; value leaves.size()+k is insts[k].
+    // roots lists the output values (one per output buffer); root == roots[0].
     struct Expr {
         std::vector<Leaf> leaves;
         std::vector<Inst> insts;
         int root = -1;
+        std::vector<int> roots;
     };
 
     bool fusible_interior(const Node& n);
@@ -63,6 +65,9 @@ namespace ormi::hip {
     // plan_only accepts realized operands of any device (kernel planning for
     // code generator tests; such an Expr is never launched).
     Expr build_expr(const NodePtr& root, const std::vector<int>& shape, bool plan_only = false);
+    // One tape for several element-wise roots of the same shape: shared leaves
+    // and interior nodes are evaluated once, each root is one output.
+    Expr build_expr_multi(const std::vector<NodePtr>& roots, const std::vector<int>& shape, bool plan_only = false);
 
     // --------------------------------------------------------- kernels --
     struct FastDiv { uint32_t d, m, s; };
@@ -97,6 +102,9 @@ namespace ormi::hip {
 
     // Element-wise map of expr over `shape` into out (contiguous, out_dtype).
     KernelLaunch plan_map(const Expr& expr, const std::vector<int>& shape, void* out, DType out_dtype, int compute_units);
+    // The same with one contiguous output per expr.roots entry (multi-output fusion).
+    KernelLaunch plan_map_multi(const Expr& expr, const std::vector<int>& shape, const std::vector<void*>& outs,
+                                const std::vector<DType>& out_dtypes, int compute_units);
 
     // Reduction of expr (evaluated over in_shape) over `axes` (sorted; empty =
     // all). out holds prod(kept dims) values, fp32 (Sum/Max) or int64 (Argmax).
@@ -123,5 +131,8 @@ namespace ormi::hip {
     // kernel, reductions fuse their pointwise producer as a prologue, views
     // alias, matmuls call the MFMA GEMM.
     void realize(const NodePtr& root);
+    // Realize several nodes together: element-wise roots of the same shape share
+    // one multi-output kernel (each input read once); the rest realize in order.
+    void realize_group(const std::vector<NodePtr>& roots);
     int device_compute_units();
 }

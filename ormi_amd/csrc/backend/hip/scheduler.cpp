@@ -17,8 +17,10 @@
 //   * MATMUL      -> both operands realized, MFMA GEMM.
 // Reductions and MATMUL are registered as graph breakers for DeviceEnum::HIP
 // (the reference's plugin point, csrc/backend/graph_breakers.h:12-14).
+#include <algorithm>
 #include <mutex>
 #include <unordered_map>
+#include <unordered_set>
 #include <vector>
 
 #include "backend/hip/hip_backend.h"
@@ -254,11 +256,60 @@ namespace ormi::hip {
         throw std::runtime_error(std::string("HIP scheduler: no lowering for op ") + ops::op_name(root->op));
     }
 
+    void realize_group(const std::vector<NodePtr>& roots) {
+        // Element-wise roots with float results that can share one kernel,
+        // grouped by shape in first-seen order; everything else realizes alone.
+        std::vector<std::pair<std::vector<int>, std::vector<NodePtr>>> groups;
+        std::vector<NodePtr> rest;
+        std::unordered_set<Node*> seen;
+        for (const auto& r : roots) {
+            if (!r || r->is_realized() || !seen.insert(r.get()).second) continue;
+            if (r->device.type != DeviceEnum::HIP) throw std::runtime_error("HIP scheduler: node belongs to another device.");
+            if (!fusible_interior(*r)) {
+                rest.push_back(r);
+                continue;
+            }
+            auto it = std::find_if(groups.begin(), groups.end(), [&](const auto& g) { return g.first == r->view.shape; });
+            if (it == groups.end()) groups.push_back({r->view.shape, {r}});
+            else it->second.push_back(r);
+        }
+        for (auto& [shape, members] : groups) {
+            for (const auto& m : members)
+                for (const auto& f : region_frontier(m)) realize(f);
+            std::vector<NodePtr> live;
+            for (const auto& m : members)
+                if (!m->is_realized()) live.push_back(m);
+            if (live.empty()) continue;
+            if (live.size() == 1) {
+                run_map(live[0]);
+                continue;
+            }
+            // The tape is built while every member is still unrealized, so a
+            // member inside another's region stays an instruction, not a leaf.
+            const Expr e = build_expr_multi(live, shape);
+            std::vector<std::shared_ptr<Buffer>> bufs;
+            std::vector<void*> outs;
+            std::vector<DType> dts;
+            for (const auto& m : live) {
+                bufs.push_back(empty(m->view.shape, DeviceEnum::HIP, m->dtype));
+                outs.push_back(bufs.back()->ptr);
+                dts.push_back(m->dtype);
+            }
+            if (shape_numel(shape) > 0) launch(plan_map_multi(e, shape, outs, dts, device_compute_units()));
+            for (size_t i = 0; i < live.size(); ++i) {
+                live[i]->data = bufs[i];
+                live[i]->view.strides = calc_contiguous_strides(live[i]->view.shape);
+            }
+        }
+        for (const auto& r : rest) realize(r);
+    }
+
     static RegisterGraphBreaker reg_sum(DeviceEnum::HIP, OpEnum::SUM, [](std::shared_ptr<Node> n) { reduce_handler(n, ReduceOp::Sum); });
     static RegisterGraphBreaker reg_max(DeviceEnum::HIP, OpEnum::MAX, [](std::shared_ptr<Node> n) { reduce_handler(n, ReduceOp::Max); });
     static RegisterGraphBreaker reg_argmax(DeviceEnum::HIP, OpEnum::ARGMAX, [](std::shared_ptr<Node> n) { reduce_handler(n, ReduceOp::Argmax); });
     static RegisterGraphBreaker reg_matmul(DeviceEnum::HIP, OpEnum::MATMUL, matmul_handler);
     static RegisterScheduler reg_sched(DeviceEnum::HIP, [](std::shared_ptr<Node> n) { realize(n); });
+    static RegisterGroupScheduler reg_group(DeviceEnum::HIP, [](const std::vector<std::shared_ptr<Node>>& ns) { realize_group(ns); });
     // Element-wise JIT entry for a node whose parents are realized: the
     // reference's execute_jit slot (csrc/backend/runtime.cpp:29-38).
     static RegisterJit reg_jit(DeviceEnum::HIP, [](std::shared_ptr<Node> n) { run_map(n); });

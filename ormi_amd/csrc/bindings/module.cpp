@@ -174,6 +174,25 @@ namespace {
         d["num_args"] = k.args.size();
         return d;
     }
+
+    // The multi-output kernel realize_all would launch for these element-wise
+    // roots of one shape (planning only: operands may live on any device).
+    py::dict plan_group(const std::vector<std::shared_ptr<Node>>& roots) {
+        if (roots.empty()) throw std::runtime_error("_plan_group: no roots");
+        const auto& shape = roots[0]->view.shape;
+        const hip::Expr e = hip::build_expr_multi(roots, shape, true);
+        std::vector<void*> outs(roots.size(), (void*)(uintptr_t)0x100000);
+        std::vector<DType> dts;
+        for (const auto& r : roots) dts.push_back(r->dtype);
+        const hip::KernelLaunch k = hip::plan_map_multi(e, shape, outs, dts, 256);
+        py::dict d;
+        d["source"] = k.source;
+        d["name"] = k.name;
+        d["plan"] = k.plan;
+        d["num_leaves"] = e.leaves.size();
+        d["num_insts"] = e.insts.size();
+        return d;
+    }
 }
 
 PYBIND11_MODULE(ormi_backend, m) {
@@ -307,6 +326,9 @@ PYBIND11_MODULE(ormi_backend, m) {
     });
     m.def("synchronize", [] { ORMI_HIP_CHECK(ormi_hip_synchronize()); });
     m.def("_plan_kernel", &plan_kernel);
+    m.def("_plan_group", &plan_group);
+    m.def("realize_all", &execute_graph_group,
+          "Realize several nodes together; on the HIP device same-shape element-wise roots share one kernel.");
     m.def("_fastdiv", [](uint32_t d) {
         auto f = hip::make_fastdiv(d);
         return py::make_tuple(f.m, f.s);

@@ -10,7 +10,10 @@ namespace ormi {
     static std::map<DeviceEnum, JitFunc>& jit_table() { static std::map<DeviceEnum, JitFunc> t; return t; }
     static std::map<DeviceEnum, SchedulerFunc>& sched_table() { static std::map<DeviceEnum, SchedulerFunc> t; return t; }
 
+    static std::map<DeviceEnum, GroupSchedulerFunc>& group_table() { static std::map<DeviceEnum, GroupSchedulerFunc> t; return t; }
+
     void register_jit(DeviceEnum d, JitFunc f) { jit_table()[d] = std::move(f); }
+    void register_group_scheduler(DeviceEnum d, GroupSchedulerFunc f) { group_table()[d] = std::move(f); }
     void register_scheduler(DeviceEnum d, SchedulerFunc f) { sched_table()[d] = std::move(f); }
     bool has_jit(DeviceEnum d) { return jit_table().count(d) > 0; }
 
@@ -58,5 +61,22 @@ namespace ormi {
         auto it = sched_table().find(root->device.type);
         if (it != sched_table().end()) it->second(root);
         else execute_graph_eager(root);
+    }
+
+    void execute_graph_group(const std::vector<std::shared_ptr<Node>>& roots) {
+        std::map<DeviceEnum, std::vector<std::shared_ptr<Node>>> by_device;
+        std::vector<DeviceEnum> order;
+        for (const auto& r : roots) {
+            if (!r || r->is_realized()) continue;
+            auto& v = by_device[r->device.type];
+            if (v.empty()) order.push_back(r->device.type);
+            v.push_back(r);
+        }
+        for (DeviceEnum d : order) {
+            auto it = group_table().find(d);
+            if (it != group_table().end()) it->second(by_device[d]);
+            else
+                for (const auto& r : by_device[d]) execute_graph(r);
+        }
     }
 }

@@ -249,3 +249,13 @@ class Tensor:
     def __repr__(self):
         state = "realized" if (self._node and self._node.is_realized) else "lazy"
         return f"Tensor(op={self.op.name}, shape={self.shape}, state={state}, device={self.device.type.name})"
+
+
+def realize_all(*tensors: Tensor) -> None:
+    """Realize several tensors together. On the HIP device, element-wise roots
+    of the same shape (for example the gradients of one backward pass, or the
+    updated parameters of an SGD step) become one multi-output kernel that reads
+    each shared input once; other tensors are realized one by one, in order."""
+    nodes = [t._node for t in tensors if t is not None and t._node is not None]
+    ormi_backend.realize_all(nodes)
+

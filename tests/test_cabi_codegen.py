@@ -152,3 +152,35 @@ def test_long_axis_reduction_is_two_pass(ob, cpu):
     d = ob._plan_kernel(ob.sum(x._node, [0, 1], False))
     assert d["two_pass"] and d["workspace_bytes"] > 0
     assert "atomic" not in d["source"] and "atomic" not in d["second_source"]
+
+
+def test_multi_output_group_plan(ob, cpu, cabi):
+    """Sibling element-wise roots of one shape plan as ONE kernel with one output
+    each; shared interior nodes are computed once (fewer instructions than the
+    separate tapes), and the kernel compiles for gfx950."""
+    rng = np.random.default_rng(5)
+    a, b, c = (_cpu(rng.standard_normal((64, 256))) for _ in range(3))
+    h = a * b + c
+    roots = [h.relu() * b, h.relu() * a, h.relu(), a - c]
+    d = ob._plan_group([r._node for r in roots])
+    assert "outputs=4" in d["plan"], d["plan"]
+    assert d["num_leaves"] == 3
+    separate = sum(ob._plan_group([r._node])["num_insts"] for r in roots)
+    assert d["num_insts"] < separate
+    for r in range(4):
+        assert f"out{r}" in d["source"]
+    rc, _ = _compile_only(cabi, d["source"], ob._rtc_options())
+    assert rc == ORMI_HIP_OK, cabi.ormi_hip_last_error()
+    # A single root keeps the single-output kernel (same source as _plan_kernel).
+    assert ob._plan_group([roots[0]._node])["source"] == ob._plan_kernel(roots[0]._node)["source"]
+
+
+def test_realize_all_on_cpu_realizes_each(cpu):
+    """Devices without a group scheduler (the CPU oracle) realize each node."""
+    from ormi_amd import Tensor, realize_all
+
+    x = Tensor(np.arange(6, dtype=np.float32).reshape(2, 3), "cpu")
+    y, z = x * 2.0, (x + 1.0).sum(1)
+    realize_all(y, z, y)
+    assert y._node.is_realized and z._node.is_realized
+    assert y.numpy().tolist() == [[0, 2, 4], [6, 8, 10]] and z.numpy().tolist() == [6, 15]

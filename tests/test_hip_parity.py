@@ -289,6 +289,54 @@ def test_c1_forward_backward(cpu, hip):
         assert_bits_equal(gh.numpy(), gc.numpy())  # products of exact values and a mask
 
 
+def test_c1_grads_realized_together(cpu, hip):
+    """realize_all puts the three gradients in one multi-output kernel; the
+    results are the same bits as realizing them one by one and as the oracle."""
+    from ormi_amd import realize_all
+
+    rng = np.random.default_rng(0)
+    a, b, c = (rng.uniform(-1, 1, (1024, 1024)).astype(np.float32) for _ in range(3))
+    Ah, Bh, Ch, yh = c1_graph(hip, a, b, c)
+    yh.sum().backward()
+    grads = [Ah.grad, Bh.grad, Ch.grad]
+    realize_all(*grads)
+    assert all(g._node.is_realized for g in grads)
+    A1, B1, C1, y1 = c1_graph(hip, a, b, c)
+    y1.sum().backward()
+    Ac, Bc, Cc, yc = c1_graph(cpu, a, b, c)
+    yc.sum().backward()
+    for g, g1, gc in zip(grads, (A1.grad, B1.grad, C1.grad), (Ac.grad, Bc.grad, Cc.grad)):
+        assert_bits_equal(g.numpy(), g1.numpy())
+        assert_bits_equal(g.numpy(), gc.numpy())
+
+
+def test_realize_all_mixed_group(cpu, hip):
+    """Mixed requests: two shapes, a reduction, a root inside another root's
+    region, a duplicate, an already-realized tensor and a bf16 output."""
+    from ormi_amd import realize_all
+
+    rng = np.random.default_rng(41)
+    x = rng.standard_normal((37, 130)).astype(np.float32)
+    v = rng.standard_normal((130,)).astype(np.float32)
+
+    def graph(dev):
+        X, V = T(x, dev), T(v, dev)
+        h = (X * V).tanh()
+        return [h, h * 2.0 - X, (X + V).sigmoid().astype("bfloat16"), h.sum(1), V * V, X.max(0), h]
+
+    got = graph(hip)
+    got[4].realize()
+    realize_all(*got)
+    want = graph(cpu)
+    for i, (g, w) in enumerate(zip(got, want)):
+        assert g._node.is_realized
+        gn, wn = g.numpy(), w.numpy()
+        assert gn.dtype == wn.dtype and gn.shape == wn.shape
+        # entry 2 is rounded to bf16: a 1-ulp fp32 difference may move it by one bf16 ulp (2^-8)
+        rtol = 2 ** -8 if i == 2 else 1e-5
+        np.testing.assert_allclose(gn.astype(np.float32), wn.astype(np.float32), rtol=rtol, atol=1e-5)
+
+
 # ---------------------------------------------------------------- config 4: GEMM
 def gemm_ref64(a, b):
     return a.astype(np.float64) @ b.astype(np.float64)
