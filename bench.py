@@ -176,6 +176,9 @@ def bench_c2(args, ev: Events) -> dict:
         xs = x if k == 0 else np.ascontiguousarray(np.roll(x, k, axis=0))
         sets.append((Tensor(xs, "hip"), Tensor(bias, "hip"), Tensor(scale, "hip")))
     ring = collections.deque(maxlen=4)
+    # Give the allocator pool the blocks the ring cycles through (the ring's 4
+    # outputs plus the one being written), so no timed step calls hipMalloc.
+    [c2_graph(*sets[i % 3]).realize() for i in range(ring.maxlen + 1)]
     for i in range(args.warmup):
         ring.append(c2_graph(*sets[i % 3]).realize())
     ev.sync()

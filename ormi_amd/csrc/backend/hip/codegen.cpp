@@ -660,7 +660,10 @@ namespace ormi::hip {
                 b << "  const " << t << " rg0 = p * (" << t << ")CH;\n";
                 b << "  const " << t << " rg1 = rg0 + (" << t << ")CH < (" << t << ")RG ? rg0 + (" << t << ")CH : (" << t << ")RG;\n";
                 if (is_sum) b << "  float acc[" << V << "];\n#pragma unroll\n  for (int k = 0; k < " << V << "; ++k) acc[k] = 0.0f;\n";
-                else b << "  float bv = -__builtin_inff(); int bi = 0x7fffffff;\n";
+                // max / argmax: one (value, index) chain per vector slot, so
+                // the V chains advance independently.
+                else b << "  float mv[" << V << "]; int mi[" << V << "];\n#pragma unroll\n  for (int k = 0; k < " << V
+                       << "; ++k) { mv[k] = -__builtin_inff(); mi[k] = 0x7fffffff; }\n";
                 // UNR groups per lane starting at rg, 64 groups apart.
                 auto emit_step = [&](int UNR, const std::string& ind) {
                     g.declare_leaf_regs(b, ind, UNR);
@@ -679,7 +682,7 @@ namespace ormi::hip {
                     b << ind << "#pragma unroll\n" << ind << "  for (int k = 0; k < " << V << "; ++k) {\n";
                     const std::string v = g.eval(b, ind + "    ", "u", "k");
                     if (is_sum) b << ind << "    acc[k] += " << v << ";\n";
-                    else b << ind << "    ormi_am_take(bv, bi, " << v << ", (int)((rg + u * 64) * " << V << " + k));\n";
+                    else b << ind << "    ormi_am_step(mv[k], mi[k], " << v << ", (int)((rg + u * 64) * " << V << " + k));\n";
                     b << ind << "  }\n" << ind << "}\n";
                 };
                 b << "  " << t << " rg = rg0 + lane;\n";
@@ -696,6 +699,13 @@ namespace ormi::hip {
                     b << "  s = ormi_wave_sum(s);\n";
                     b << "  if (lane == 0) ((float*)outp)[wid] = s;\n";
                 } else {
+                    // A chain of only -inf still holds the empty marker: its first element
+                    // is the first maximum. (An empty chain gets an index past the part's
+                    // elements, which loses every tie.)
+                    b << "#pragma unroll\n  for (int k = 0; k < " << V << "; ++k) if (mi[k] == 0x7fffffff) mi[k] = (int)((rg0 + lane) * "
+                      << V << " + k);\n";
+                    b << "  float bv = mv[0]; int bi = mi[0];\n";
+                    b << "#pragma unroll\n  for (int k = 1; k < " << V << "; ++k) ormi_am_take(bv, bi, mv[k], mi[k]);\n";
                     b << "  ormi_wave_argmax(bv, bi);\n";
                     b << "  if (lane == 0) {\n";
                     if (is_arg) b << "    if (NP == 1) ((long long*)outp)[wid] = (long long)bi; else { ((float*)outp)[wid] = bv; outi[wid] = bi; }\n";
@@ -811,7 +821,7 @@ namespace ormi::hip {
                 b << ind << "#pragma unroll\n" << ind << "  for (int k = 0; k < " << V << "; ++k) {\n";
                 const std::string v = g.eval(b, ind + "    ", "u", "k");
                 if (is_sum) b << ind << "    acc[k] += " << v << ";\n";
-                else b << ind << "    ormi_am_take(bv[k], bx[k], " << v << ", (int)(r + u * " << W << "));\n";
+                else b << ind << "    ormi_am_step(bv[k], bx[k], " << v << ", (int)(r + u * " << W << "));\n";
                 b << ind << "  }\n" << ind << "}\n";
             };
             b << "  " << t << " r = r0 + w;\n";
@@ -822,6 +832,8 @@ namespace ormi::hip {
             b << "    for (; r < r1; r += " << W << ") {\n";
             emit_cstep(1, "      ");
             b << "    }\n  }\n";
+            if (!is_sum)  // all -inf chain: its first element r0 + w (see the row kernel)
+                b << "#pragma unroll\n  for (int k = 0; k < " << V << "; ++k) if (bx[k] == 0x7fffffff) bx[k] = (int)(r0 + w);\n";
             b << "#pragma unroll\n  for (int k = 0; k < " << V << "; ++k) {";
             if (is_sum) b << " sv[w][lane][k] = acc[k]; }\n";
             else b << " sv[w][lane][k] = bv[k]; si[w][lane][k] = bx[k]; }\n";

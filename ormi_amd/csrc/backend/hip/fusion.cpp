@@ -41,7 +41,7 @@ namespace ormi::hip {
         RegisterLowering l_pow(OpEnum::POW, [](A v) { return "powf(" + v[0] + ", " + v[1] + ")"; });
         RegisterLowering l_eq(OpEnum::EQ, [](A v) { return "ormi_eq(" + v[0] + ", " + v[1] + ")"; });
         RegisterLowering l_neg(OpEnum::NEG, [](A v) { return "(-" + v[0] + ")"; });
-        RegisterLowering l_exp(OpEnum::EXP, [](A v) { return "expf(" + v[0] + ")"; });
+        RegisterLowering l_exp(OpEnum::EXP, [](A v) { return "ormi_exp(" + v[0] + ")"; });
         RegisterLowering l_log(OpEnum::LOG, [](A v) { return "logf(" + v[0] + ")"; });
         RegisterLowering l_sin(OpEnum::SIN, [](A v) { return "sinf(" + v[0] + ")"; });
         RegisterLowering l_cos(OpEnum::COS, [](A v) { return "cosf(" + v[0] + ")"; });

@@ -6,10 +6,10 @@
 // Numeric contract with the CPU oracle: generated code is compiled with
 // -ffp-contract=off and IEEE division, so the user-visible + - * / agree bit
 // for bit; the helpers below are the oracle's fp32 formulas, with the device
-// math library for exp, log, sin, cos and erf (a few ulp from the host's).
+// math library for log, sin, cos and erf (a few ulp from the host's). exp,
 // tanh and sigmoid, which dominate VALU-bound fused chains, are written here
-// from the hardware V_EXP_F32 / V_RCP_F32 in half the instructions of the
-// library versions, within 3 ulp of the exact values (the oracle's glibc
+// from the hardware V_EXP_F32 / V_RCP_F32 in about half the instructions of
+// the library versions, within 3 ulp of the exact values (the oracle's glibc
 // results are within 1 ulp), so parity holds at rtol 1e-6.
 #pragma once
 #ifndef __HIPCC_RTC__
@@ -95,6 +95,22 @@ __device__ __forceinline__ float ormi_sigmoid(float x) {
     return r == r ? c : s;
 }
 __device__ __forceinline__ float ormi_sigmoid_grad(float y) { return y * (1.0f - y); }
+
+// e^x in about 7 VALU instructions (the device library's expf takes about 13),
+// within 2 ulp for results in the normal range: e^x = 2^hi e^r with
+// hi = fl(x log2 e), r = x - hi ln 2 from two FMAs (Cody-Waite, ln 2 split into
+// an fp32 head and tail), and e^r = 1 + r to within r^2/2 < 2^-34. When the
+// correction is NaN (x = +-inf, where r is NaN, or 2^hi = inf times a negative
+// r) the uncorrected 2^hi is already the answer (inf or 0); NaN x stays NaN.
+// Results below the normal range (x < -87.3) come from V_EXP_F32 as they are.
+__device__ __forceinline__ float ormi_exp(float x) {
+    const float hi = x * 1.44269502f;
+    float r = __builtin_fmaf(-hi, 0.693147182f, x);
+    r = __builtin_fmaf(-hi, -1.90465432e-09f, r);
+    const float e = __builtin_amdgcn_exp2f(hi);
+    const float c = __builtin_fmaf(e, r, e);
+    return c == c ? c : e;
+}
 // GELU, erf form: 0.5 x (1 + erf(x / sqrt 2)).
 __device__ __forceinline__ float ormi_gelu(float a) {
     return (0.5f * a) * (1.0f + erff(a * 0.70710678118654752f));
@@ -102,7 +118,7 @@ __device__ __forceinline__ float ormi_gelu(float a) {
 // d/dx GELU = Phi(x) + x phi(x).
 __device__ __forceinline__ float ormi_gelu_grad(float a) {
     const float cdf = 0.5f * (1.0f + erff(a * 0.70710678118654752f));
-    const float pdf = 0.39894228040143268f * expf((-0.5f * a) * a);
+    const float pdf = 0.39894228040143268f * ormi_exp((-0.5f * a) * a);
     return cdf + a * pdf;
 }
 __device__ __forceinline__ float ormi_eq(float a, float b) { return a == b ? 1.0f : 0.0f; }
@@ -143,15 +159,29 @@ __device__ __forceinline__ float ormi_wave_sum(float v) {
 // Ordering for max/argmax: NaN above every number; equal values (+0 == -0)
 // prefer the smaller index. It is a total order on (value, index) pairs, so
 // the reduced pair is the first occurrence of the maximum whatever the tree.
+// Written as one boolean expression so it compiles to compares and selects,
+// not to divergent branches.
 __device__ __forceinline__ bool ormi_am_better(float a, int ia, float b, int ib) {
-    const bool an = a != a, bn = b != b;
-    if (an || bn) return (an && bn) ? (ia < ib) : an;
-    if (a != b) return a > b;
-    return ia < ib;
+    const bool an = a != a, bn = b != b, earlier = ia < ib;
+    return an ? (!bn | earlier) : (!bn & ((a > b) | ((a == b) & earlier)));
 }
 
 __device__ __forceinline__ void ormi_am_take(float& v, int& i, float ov, int oi) {
-    if (ormi_am_better(ov, oi, v, i)) { v = ov; i = oi; }
+    const bool t = ormi_am_better(ov, oi, v, i);
+    v = t ? ov : v;
+    i = t ? oi : i;
+}
+
+// One element of a chain whose indices increase (a lane's own elements):
+// only a strictly larger value, or the first NaN, replaces the current pair,
+// so ties keep the earlier element without comparing indices. !(x <= v) is
+// "x > v, or either is NaN"; (v == v) keeps a NaN already held. A chain
+// starts at (-inf, 0x7fffffff); one whose elements are all -inf keeps that
+// index, and the caller replaces it with the chain's first index after the loop.
+__device__ __forceinline__ void ormi_am_step(float& v, int& i, float x, int ix) {
+    const bool t = !(x <= v) & (v == v);
+    v = t ? x : v;
+    i = t ? ix : i;
 }
 
 template <int CTRL>

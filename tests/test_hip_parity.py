@@ -146,9 +146,9 @@ def _ulp_error(got, truth64):
 
 
 def test_device_tanh_sigmoid_accuracy(cpu, hip):
-    """The device tanh and sigmoid (hardware exp/rcp plus a fitted polynomial)
-    stay within 3 ulp of float64 over a dense sweep, and within rtol 1e-6 of the
-    oracle (glibc) with no absolute floor."""
+    """The device exp, tanh and sigmoid (hardware exp/rcp plus a fitted
+    polynomial) stay within 2-3 ulp of float64 over dense sweeps, and within
+    rtol 1e-6 of the oracle (glibc) with no absolute floor."""
     rng = np.random.default_rng(31)
     x = np.concatenate([np.linspace(-12, 12, 2_000_001, dtype=np.float32),
                         rng.standard_normal(1_000_000).astype(np.float32),
@@ -165,6 +165,13 @@ def test_device_tanh_sigmoid_accuracy(cpu, hip):
     ts = T(special, hip).tanh().numpy()
     assert np.array_equal(np.signbit(ts[:2]), [False, True]) and ts[0] == 0 and ts[1] == 0
     assert ts[2] == 1 and ts[3] == -1 and np.isnan(ts[4]) and ts[5] == np.float32(1e-30) and ts[7] == 1 and ts[8] == -1
+    # exp: 2 ulp wherever the result is a normal float (x >= -87.3)
+    xe = np.concatenate([np.linspace(-87.3, 88.7, 2_000_001, dtype=np.float32), x])
+    e = T(xe, hip).exp().numpy()
+    assert _ulp_error(e, np.exp(xe.astype(np.float64))).max() <= 2.0
+    np.testing.assert_allclose(e, T(xe, cpu).exp().numpy(), rtol=1e-6, atol=0)
+    es = T(np.array([np.inf, -np.inf, np.nan, 0.0, 89.0, -200.0], np.float32), hip).exp().numpy()
+    assert es[0] == np.inf and es[1] == 0 and np.isnan(es[2]) and es[3] == 1 and es[4] == np.inf and es[5] == 0
     ss = T(special, hip).sigmoid().numpy()
     assert ss[0] == 0.5 and ss[2] == 1 and ss[3] == 0 and np.isnan(ss[4]) and ss[7] == 1 and ss[8] == 0
 
@@ -267,6 +274,31 @@ def test_argmax_ties_and_nan(cpu, hip):
         assert np.array_equal(got, want)
     assert np.array_equal(T(x, hip).argmax(1).numpy(), np.argmax(x, axis=1))
     assert_bits_equal(T(x, hip).max(1).numpy(), T(x, cpu).max(1).numpy())
+
+
+@pytest.mark.parametrize("shape,axis", [((3, 1 << 20), 1), ((1 << 16, 6), 0), ((5, 1003), 1), ((1003, 70), 0)])
+def test_argmax_edge_cases_all_paths(cpu, hip, shape, axis):
+    """Row, column and two-pass (split) reductions: the first maximum wins across
+    lanes, vector slots and parts; all -inf, NaN first / later, +-0 first."""
+    rng = np.random.default_rng(43)
+    x = rng.standard_normal(shape).astype(np.float32)
+    xm = np.moveaxis(x, axis, -1)  # view: reduced axis last
+    n = xm.shape[-1]
+    xm[0, :] = -np.inf
+    xm[1, :] = 0.0
+    xm[1, 0] = -0.0                           # first zero is -0.0: max keeps its bits
+    xm[1, n // 3] = -0.0
+    xm[2, n - 1] = np.nan
+    xm[2, n - 2] = np.nan                     # the first NaN (n-2) wins
+    if xm.shape[0] > 3:
+        xm[3, :] = 1.0
+        xm[3, n - 5] = 7.0
+        xm[3, 3] = 7.0                        # ties across the row: index 3
+    for red in ("argmax", "max"):
+        got = getattr(T(x, hip), red)(axis).numpy()
+        want = getattr(T(x, cpu), red)(axis).numpy()
+        assert_bits_equal(got, want)
+    assert np.array_equal(T(x, hip).argmax(axis).numpy(), np.argmax(x, axis=axis))
 
 
 # ------------------------------------------ config 1: fused pointwise + row sum
