@@ -261,10 +261,13 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_kernel(GemmParams p)
             for (int i = 0; i < TM; ++i)
 #pragma unroll
                 for (int j = 0; j < TN; ++j) Tr::mma(af[q][i], bfr[q][j], acc[i][j]);
-        }
-        if (more) {
-            la.store(As[cur ^ 1]);
-            lb.store(Bs[cur ^ 1]);
+            // The next tile goes to the other LDS buffer halfway through this
+            // tile's MFMAs: every wave finished reading that buffer before the
+            // previous barrier, and its write latency now overlaps matrix work.
+            if (ks == KCH / 4 - 1 && more) {
+                la.store(As[cur ^ 1]);
+                lb.store(Bs[cur ^ 1]);
+            }
         }
         __syncthreads();
     }
