@@ -422,6 +422,45 @@ def pmc_report(pmc_dir: Path, out: Path, cmd: str) -> None:
     print(out.read_text())
 
 
+def mfma_report(pmc_dir: Path, out: Path, cmd: str) -> None:
+    """MFMA utilisation per GEMM kernel from one `rocprofv3 --pmc
+    SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_MFMA SQ_LDS_BANK_CONFLICT GRBM_GUI_ACTIVE` run:
+    busy cycles summed over SIMDs / (SIMDs x the kernel's active cycles per XCC),
+    the formula of rocprofv3's derived MfmaUtil. SIMD and XCC counts come from the
+    run's agent info."""
+    agent = {}
+    for f in sorted(pmc_dir.rglob("*agent_info.csv")):
+        for r in csv.DictReader(open(f, newline="")):
+            if r.get("Name", "").startswith("gfx"):
+                agent = r
+    simds, xcc = int(agent.get("Simd_Count", 1024)), int(agent.get("Num_Xcc", 8))
+    per = collections.defaultdict(lambda: collections.defaultdict(list))
+    for f in sorted(pmc_dir.rglob("*counter_collection.csv")):
+        for r in csv.DictReader(open(f, newline="")):
+            name = r.get("Kernel_Name", "").strip()
+            if "gemm" in name:
+                per[name][r["Counter_Name"].strip()].append(float(r["Counter_Value"]))
+    lines = [
+        "# GEMM MFMA utilisation (rocprofv3 counters)", "",
+        f"Command (from the repo root): `{cmd}`", "",
+        f"Device: {agent.get('Name', '?')}, {simds} SIMDs, {xcc} XCCs. util = SQ_VALU_MFMA_BUSY_CYCLES / "
+        f"(SIMDs x GRBM_GUI_ACTIVE / XCCs), averaged over dispatches; counters serialize kernels, so this is the "
+        "busy fraction of the matrix pipes while the kernel runs.", "",
+        "| kernel | dispatches | MFMA util | MFMA instructions / dispatch | LDS bank conflicts / dispatch |",
+        "|---|---|---|---|---|",
+    ]
+    for name, cs in sorted(per.items()):
+        busy, act = cs.get("SQ_VALU_MFMA_BUSY_CYCLES", []), cs.get("GRBM_GUI_ACTIVE", [])
+        if not busy or not act:
+            continue
+        util = sum(b / (simds * a / xcc) for b, a in zip(busy, act)) / len(busy)
+        mf = cs.get("SQ_INSTS_MFMA", [0.0])
+        bc = cs.get("SQ_LDS_BANK_CONFLICT", [0.0])
+        lines.append(f"| `{name[:110]}` | {len(busy)} | {util * 100:.1f}% | {sum(mf) / len(mf):.4g} | {sum(bc) / len(bc):.4g} |")
+    out.write_text("\n".join(lines) + "\n")
+    print(out.read_text())
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -433,7 +472,15 @@ def main():
                     help="run one non-headline workload and print its figures (profiling runs)")
     ap.add_argument("--pmc-report", nargs=2, metavar=("PMC_DIR", "OUT_MD"),
                     help="summarize rocprofv3 --pmc runs into a traffic table (no GPU needed)")
+    ap.add_argument("--mfma-report", nargs=2, metavar=("PMC_DIR", "OUT_MD"),
+                    help="summarize a rocprofv3 --pmc run of --only c4 into MFMA utilisation (no GPU needed)")
     args = ap.parse_args()
+    if args.mfma_report:
+        mfma_report(Path(args.mfma_report[0]), Path(args.mfma_report[1]),
+                    "rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_MFMA SQ_LDS_BANK_CONFLICT GRBM_GUI_ACTIVE "
+                    "-d gpurun_out/pmc_mfma -o run --output-format csv -- python3 bench.py --only c4 --steps 5 --warmup 1; "
+                    "python3 bench.py --mfma-report gpurun_out/pmc_mfma profiles/gemm_mfma_util.md")
+        return
     if args.pmc_report:
         pmc_report(Path(args.pmc_report[0]), Path(args.pmc_report[1]),
                    "rocprofv3 --pmc FETCH_SIZE|WRITE_SIZE -d <PMC_DIR>/<label>_<COUNTER> -o run --output-format csv "
