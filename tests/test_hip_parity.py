@@ -59,6 +59,14 @@ def test_reference_kats_on_hip(cpu, hip):
     assert np.allclose(s, 1.0, atol=1e-5)
 
 
+def test_golden_kats_on_hip(ob, hip):
+    """Every vector of tests/golden/reference_kats.json on the HIP device."""
+    from kat_runner import cases, run_case
+
+    for case in cases():
+        run_case(ob, case, ob.DeviceEnum.HIP)
+
+
 def test_matmul_kats_on_hip(ob, hip):
     def view(vals, shape, strides):
         buf = ob.numpy_to_buffer(np.array(vals, np.float32), ob.DeviceEnum.HIP)

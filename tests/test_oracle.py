@@ -258,3 +258,19 @@ def test_mlp_grads_against_float64(cpu):
     gW1 = X64.T @ (dh * gelu_p)
     assert np.allclose(w2.grad.numpy(), gW2, rtol=1e-4, atol=1e-5)
     assert np.allclose(w1.grad.numpy(), gW1, rtol=1e-4, atol=1e-5)
+
+
+# ------------------------------------------------- golden vectors (data fixtures)
+def _kat_ids():
+    from kat_runner import cases
+
+    return [c["name"] for c in cases()]
+
+
+@pytest.mark.parametrize("name", _kat_ids())
+def test_golden_kats_on_oracle(ob, cpu, name):
+    """tests/golden/reference_kats.json: the reference's own known answers."""
+    from kat_runner import cases, run_case
+
+    case = next(c for c in cases() if c["name"] == name)
+    run_case(ob, case, ob.DeviceEnum.CPU)
