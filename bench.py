@@ -349,10 +349,16 @@ def bench_c5(ev: Events, steps: int) -> dict:
         for w in ws:
             u = (w - w.grad * 1e-3).realize()
             out.append(Tensor(_node=Node(u._node.data, True, u._node.device), device="hip"))
+        # backward stored a gradient on every node and gradient graphs point at
+        # forward nodes (reference csrc/core/autograd.cpp:24-47): clearing them
+        # (zero_grad_graph, :49-58) lets the step's buffers return to the pool.
+        loss.zero_grad_graph()
         return loss, out
 
     loss0, ws = step(ws)
     first = float(loss0.numpy())
+    del loss0
+    _, ws = step(ws)  # second untimed step: the pool now holds a step's blocks
     ev.sync()
     e0, e1 = ev.new(), ev.new()
     ev.record(e0)

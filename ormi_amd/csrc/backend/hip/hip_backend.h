@@ -134,5 +134,20 @@ namespace ormi::hip {
     // Realize several nodes together: element-wise roots of the same shape share
     // one multi-output kernel (each input read once); the rest realize in order.
     void realize_group(const std::vector<NodePtr>& roots);
+
+    // ------------------------------------------------------- allocator --
+    struct AllocatorStats {
+        size_t live_bytes = 0;      // in blocks handed out
+        size_t cached_bytes = 0;    // in blocks waiting for reuse
+        size_t device_bytes = 0;    // held from the device (live + cached)
+        uint64_t device_mallocs = 0;
+        uint64_t device_frees = 0;
+        uint64_t reuses = 0;        // requests served from the cache
+    };
+    // Bytes a request of `bytes` occupies: powers of two from 512 B to 1 MiB,
+    // then multiples of 2 MiB.
+    size_t size_class(size_t bytes);
+    AllocatorStats allocator_stats();  // throws when the HIP device is absent
+    void empty_cache();                // return every cached block to the device
     int device_compute_units();
 }

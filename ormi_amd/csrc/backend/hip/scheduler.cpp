@@ -1,8 +1,5 @@
-// HIP device: allocator, fusion scheduler and graph breakers.
-//
-// Allocator: HIPAllocator implements the reference's IAllocator
-// (csrc/core/allocator.h:7-21) over libormi_hip, with the same exact-size
-// free-list pool as CUDAAllocator (csrc/backend/cuda/allocator.cu:36-55).
+// HIP device: fusion scheduler and graph breakers (the allocator is in
+// allocator.cpp).
 //
 // Scheduler: the reference realizes every parent before compiling a node
 // (csrc/backend/runtime.cpp:16-18), so each op is its own kernel and every
@@ -28,72 +25,6 @@
 #include "core/memory.h"
 #include "runtime/graph_breakers.h"
 #include "runtime/runtime.h"
-
-namespace ormi {
-    class HIPAllocator : public IAllocator {
-        std::mutex mu_;
-        std::unordered_map<size_t, std::vector<void*>> free_blocks_;
-
-    public:
-        HIPAllocator() { ORMI_HIP_CHECK(ormi_hip_init(0)); }
-
-        void* allocate(size_t bytes) override {
-            {
-                std::lock_guard<std::mutex> lock(mu_);
-                auto it = free_blocks_.find(bytes);
-                if (it != free_blocks_.end() && !it->second.empty()) {
-                    void* p = it->second.back();
-                    it->second.pop_back();
-                    return p;
-                }
-            }
-            void* p = nullptr;
-            if (ormi_hip_malloc(&p, bytes) != ORMI_HIP_OK) {
-                // Out of memory: give cached blocks back to the device and retry once.
-                release_cached();
-                ORMI_HIP_CHECK(ormi_hip_malloc(&p, bytes));
-            }
-            return p;
-        }
-
-        void free(void* ptr, size_t bytes) override {
-            if (!ptr) return;
-            std::lock_guard<std::mutex> lock(mu_);
-            free_blocks_[bytes].push_back(ptr);
-        }
-
-        void release_cached() {
-            ormi_hip_synchronize();
-            std::lock_guard<std::mutex> lock(mu_);
-            for (auto& kv : free_blocks_)
-                for (void* p : kv.second) ormi_hip_free(p);
-            free_blocks_.clear();
-        }
-
-        void memset(void* ptr, int value, size_t bytes) override {
-            ORMI_HIP_CHECK(ormi_hip_memset_d8(ptr, (unsigned char)value, bytes));
-        }
-        void memcpy(void* dst, const void* src, size_t size) override { ORMI_HIP_CHECK(ormi_hip_memcpy_d2d(dst, src, size)); }
-        void fill_n(void* dst, const void* val, size_t elements, DType dtype) override {
-            ORMI_HIP_CHECK(ormi_hip_fill(dst, val, dtype_size(dtype), elements));
-        }
-        void copy_device_to_host(void* dst, const void* src, size_t bytes) override {
-            ORMI_HIP_CHECK(ormi_hip_memcpy_d2h(dst, src, bytes));
-        }
-        void copy_host_to_device(void* dst, const void* src, size_t bytes) override {
-            ORMI_HIP_CHECK(ormi_hip_memcpy_h2d(dst, src, bytes));
-        }
-        bool is_host_visible() const override { return false; }
-    };
-
-    // Constructed on first use; a constructor that throws (no GPU) leaves the
-    // HIP device unavailable, as a throwing CUDAAllocator does for CUDA.
-    static IAllocator* hip_allocator_instance() {
-        static HIPAllocator* inst = new HIPAllocator();  // outlives every Buffer
-        return inst;
-    }
-    static const bool hip_allocator_registered = (register_allocator(DeviceEnum::HIP, hip_allocator_instance), true);
-}
 
 namespace ormi::hip {
     using ops::OpEnum;

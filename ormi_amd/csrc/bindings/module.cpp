@@ -325,6 +325,19 @@ PYBIND11_MODULE(ormi_backend, m) {
         }
     });
     m.def("synchronize", [] { ORMI_HIP_CHECK(ormi_hip_synchronize()); });
+    m.def("_size_class", &hip::size_class);
+    m.def("allocator_stats", [] {
+        const hip::AllocatorStats st = hip::allocator_stats();
+        py::dict d;
+        d["live_bytes"] = st.live_bytes;
+        d["cached_bytes"] = st.cached_bytes;
+        d["device_bytes"] = st.device_bytes;
+        d["device_mallocs"] = st.device_mallocs;
+        d["device_frees"] = st.device_frees;
+        d["reuses"] = st.reuses;
+        return d;
+    }, "HIP caching allocator counters.");
+    m.def("empty_cache", &hip::empty_cache, "Return every cached HIP block to the device.");
     m.def("_plan_kernel", &plan_kernel);
     m.def("_plan_group", &plan_group);
     m.def("realize_all", &execute_graph_group,

@@ -184,3 +184,16 @@ def test_realize_all_on_cpu_realizes_each(cpu):
     realize_all(y, z, y)
     assert y._node.is_realized and z._node.is_realized
     assert y.numpy().tolist() == [[0, 2, 4], [6, 8, 10]] and z.numpy().tolist() == [6, 15]
+
+
+def test_allocator_size_classes(ob):
+    """Powers of two from 512 B to 1 MiB, then multiples of 2 MiB."""
+    MiB = 1 << 20
+    cases = {0: 512, 1: 512, 512: 512, 513: 1024, 4000: 4096, 4096: 4096, 4097: 8192, MiB: MiB,
+             MiB + 1: 2 * MiB, 3 * MiB: 4 * MiB, 128 * MiB: 128 * MiB, 128 * MiB + 16384: 130 * MiB}
+    for n, c in cases.items():
+        assert ob._size_class(n) == c, (n, ob._size_class(n), c)
+    rng = np.random.default_rng(3)
+    for n in rng.integers(1, 1 << 31, 200):
+        c = ob._size_class(int(n))
+        assert c >= n and (c < 2 * n or c == 512 or c - n < 2 * MiB)
