@@ -146,6 +146,77 @@ def cpu_baseline_c2(target_s: float = 10.0) -> dict:
     }
 
 
+def cpu_baselines_extra() -> dict:
+    """The reference's CPU path beside the other configs, each on a bounded sample
+    of a few seconds: the oracle (restatement of Ormi's CPU backend, one core, as
+    its loops are unthreaded) for C1 and the C3 reductions, and numpy float32
+    matmul (its bundled OpenBLAS, all host threads) standing in for the
+    reference's cblas_sgemm for the C4 GEMMs."""
+    import oracle
+    from ormi_amd import Tensor
+
+    oracle.load()
+    out = {}
+
+    def timed(fn, reps):
+        fn()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        return (time.perf_counter() - t0) / reps
+
+    rng = np.random.default_rng(0)
+    a, b, c = (rng.uniform(-1, 1, (1024, 1024)).astype(np.float32) for _ in range(3))
+    A, B, C = (Tensor(v, "cpu", requires_grad=True) for v in (a, b, c))
+    f = timed(lambda: ((A * B + C).relu() * 0.5).sum(1).realize(), 3)
+
+    def grads():
+        for t in (A, B, C):
+            t.zero_grad()
+        ((A * B + C).relu() * 0.5).sum(1).sum().backward()
+        for g in (A.grad, B.grad, C.grad):
+            g.realize()
+
+    g = timed(grads, 2)
+    out["C1"] = {"kind": "port", "cores": 1, "fwd_ms": round(f * 1e3, 2), "fwd_GB/s": round(12587008 / f / 1e9, 4),
+                 "bwd_ms": round(g * 1e3, 2), "bwd_GB/s": round(50331648 / g / 1e9, 4),
+                 "sample": "full (1024,1024), per-node execute_graph"}
+    rows, cols = 256, 8192
+    x = np.random.default_rng(2).normal(0, 2, (rows, cols)).astype(np.float32)
+    X = Tensor(x, "cpu")
+    M = X.max(1, keepdims=True).realize()
+    nb = rows * cols * 4
+    red = {"row_max": lambda: X.max(1).realize(), "row_sumexp": lambda: (X - M).exp().sum(1).realize(),
+           "row_mean": lambda: X.mean(1).realize(), "row_argmax": lambda: X.argmax(1).realize(),
+           "col_sum": lambda: X.sum(0).realize()}
+    c3 = {"kind": "port", "cores": 1, "sample": f"rows 0..{rows} of (16384,8192) (1/64), per-node execute_graph"}
+    for k, fn in red.items():
+        t = timed(fn, 2)
+        c3[k] = {"ms": round(t * 1e3, 2), "GB/s": round(nb / t / 1e9, 4)}
+    out["C3"] = c3
+    try:
+        from threadpoolctl import threadpool_info
+
+        blas = [i for i in threadpool_info() if i.get("user_api") == "blas"]
+        threads = blas[0]["num_threads"] if blas else None
+        lib = f"{blas[0].get('internal_api')} {blas[0].get('version')}" if blas else "unknown"
+    except ImportError:
+        threads, lib = None, "unknown"
+    rng = np.random.default_rng(3)
+    a16 = rng.normal(0, 1 / 64, (4096, 4096)).astype(np.float32)
+    b16 = rng.normal(0, 1 / 64, (4096, 4096)).astype(np.float32)
+    t16 = timed(lambda: a16 @ b16, 2)
+    a32 = rng.normal(0, 1 / 64, (2048, 1024)).astype(np.float32)
+    b32 = rng.normal(0, 1 / 64, (1024, 4096)).astype(np.float32)
+    t32 = timed(lambda: a32 @ b32, 3)
+    out["C4"] = {"kind": "stand-in: numpy float32 matmul for cblas_sgemm", "cores": threads, "blas": lib,
+                 "sgemm_4096_ms": round(t16 * 1e3, 1), "sgemm_4096_TFLOP/s": round(2 * 4096 ** 3 / t16 / 1e12, 3),
+                 "sgemm_2048x1024x4096_ms": round(t32 * 1e3, 1),
+                 "sgemm_2048x1024x4096_TFLOP/s": round(2 * 2048 * 1024 * 4096 / t32 / 1e12, 3),
+                 "sample": "full shapes; the bf16 config as sgemm on fp32 values"}
+    return out
+
+
 def traffic_from_profile(kernel: str):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary
     (profiles/hbm_traffic.md, written by `bench.py --pmc-report`), or None."""
@@ -518,6 +589,9 @@ def main():
         extra["C4_gemm"] = bench_c4(ev, n)
         extra["C5_mlp_step_ms"] = bench_c5(ev, max(3, min(args.steps // 10, 10)))
     cpu = None if args.no_cpu else cpu_baseline_c2()
+    if not args.no_cpu and not args.no_extra:
+        log("CPU baselines of the other configs")
+        extra["cpu_baselines"] = cpu_baselines_extra()
     line = {
         "metric": METRIC,
         "value": round(main_res["value"], 1),
