@@ -699,10 +699,10 @@ namespace ormi::hip {
                     b << "  s = ormi_wave_sum(s);\n";
                     b << "  if (lane == 0) ((float*)outp)[wid] = s;\n";
                 } else {
-                    // A chain of only -inf still holds the empty marker: its first element
-                    // is the first maximum. (An empty chain gets an index past the part's
-                    // elements, which loses every tie.)
-                    b << "#pragma unroll\n  for (int k = 0; k < " << V << "; ++k) if (mi[k] == 0x7fffffff) mi[k] = (int)((rg0 + lane) * "
+                    // A non-empty chain of only -inf still holds the empty marker: its first
+                    // element is the first maximum. An empty chain keeps the marker, an
+                    // index above every real one (R < 2^31), so it loses every tie.
+                    b << "#pragma unroll\n  for (int k = 0; k < " << V << "; ++k) if (mi[k] == 0x7fffffff && rg0 + lane < rg1) mi[k] = (int)((rg0 + lane) * "
                       << V << " + k);\n";
                     b << "  float bv = mv[0]; int bi = mi[0];\n";
                     b << "#pragma unroll\n  for (int k = 1; k < " << V << "; ++k) ormi_am_take(bv, bi, mv[k], mi[k]);\n";
@@ -832,8 +832,8 @@ namespace ormi::hip {
             b << "    for (; r < r1; r += " << W << ") {\n";
             emit_cstep(1, "      ");
             b << "    }\n  }\n";
-            if (!is_sum)  // all -inf chain: its first element r0 + w (see the row kernel)
-                b << "#pragma unroll\n  for (int k = 0; k < " << V << "; ++k) if (bx[k] == 0x7fffffff) bx[k] = (int)(r0 + w);\n";
+            if (!is_sum)  // a non-empty all -inf chain: its first element r0 + w (see the row kernel)
+                b << "#pragma unroll\n  for (int k = 0; k < " << V << "; ++k) if (bx[k] == 0x7fffffff && r0 + w < r1) bx[k] = (int)(r0 + w);\n";
             b << "#pragma unroll\n  for (int k = 0; k < " << V << "; ++k) {";
             if (is_sum) b << " sv[w][lane][k] = acc[k]; }\n";
             else b << " sv[w][lane][k] = bv[k]; si[w][lane][k] = bx[k]; }\n";

@@ -74,17 +74,41 @@ namespace ormi::hip {
         std::vector<NodePtr> frontier;
         std::unordered_set<Node*> seen{root.get()};
         std::vector<NodePtr> stack{root};
+        size_t interior = 1;
         while (!stack.empty()) {
             NodePtr n = stack.back();
             stack.pop_back();
             for (const auto& p : n->parents) {
                 if (!seen.insert(p.get()).second) continue;
                 if (p->is_realized()) continue;
-                if (fusible_interior(*p)) stack.push_back(p);
-                else frontier.push_back(p);
+                // Past kMaxRegion interior nodes, element-wise nodes become frontier:
+                // they are realized first, as regions of their own.
+                if (fusible_interior(*p) && interior < kMaxRegion) {
+                    stack.push_back(p);
+                    ++interior;
+                } else {
+                    frontier.push_back(p);
+                }
             }
         }
         return frontier;
+    }
+
+    size_t region_size(const NodePtr& root, size_t limit) {
+        if (root->is_realized() || !fusible_root(*root)) return 0;
+        std::unordered_set<Node*> seen{root.get()};
+        std::vector<NodePtr> stack{root};
+        size_t interior = 1;
+        while (!stack.empty() && interior <= limit) {
+            NodePtr n = stack.back();
+            stack.pop_back();
+            for (const auto& p : n->parents) {
+                if (!seen.insert(p.get()).second || p->is_realized() || !fusible_interior(*p)) continue;
+                stack.push_back(p);
+                ++interior;
+            }
+        }
+        return interior;
     }
 
     static Leaf make_leaf(const NodePtr& n, const std::vector<int>& shape, bool plan_only) {

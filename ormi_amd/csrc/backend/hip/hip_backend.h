@@ -58,8 +58,20 @@ namespace ormi::hip {
 
     bool fusible_interior(const Node& n);
     bool fusible_root(const Node& n);
-    // Unrealized, non-fusible nodes the pointwise region rooted at root reads.
+    // Most element-wise nodes one generated kernel evaluates: a longer chain is
+    // cut into regions of at most this size, realized innermost first.
+    constexpr size_t kMaxRegion = 256;
+    // Unrealized nodes the pointwise region rooted at root reads: non-fusible
+    // ones, and fusible ones beyond the region's kMaxRegion interior nodes.
     std::vector<NodePtr> region_frontier(const NodePtr& root);
+    // Interior nodes of the region rooted at root, counted up to limit + 1
+    // (0 when root is realized or not element-wise).
+    size_t region_size(const NodePtr& root, size_t limit);
+    // A reduction fuses its element-wise input as a prologue only up to this
+    // many ops; a larger input is realized first, so a chain whose values feed
+    // both a reduction and later element-wise ops is evaluated once, not once
+    // per consumer kernel.
+    constexpr size_t kMaxPrologue = 64;
     // SSA tape of the region (every frontier node must be realized), leaves
     // broadcast right-aligned to `shape`.
     // plan_only accepts realized operands of any device (kernel planning for

@@ -47,11 +47,16 @@ namespace ormi::hip {
         launch(plan_map(e, root->view.shape, out->ptr, root->dtype, device_compute_units()));
     }
 
-    // Realize what a reduction reads: a pointwise producer stays unrealized
-    // (it becomes the prologue); anything else is realized.
+    // Realize what a reduction reads: a pointwise producer of at most
+    // kMaxPrologue ops stays unrealized (it becomes the prologue); anything
+    // else is realized.
+    static bool fuse_as_prologue(const NodePtr& x) {
+        return !x->is_realized() && fusible_root(*x) && region_size(x, kMaxPrologue) <= kMaxPrologue;
+    }
+
     static void prepare_input(const NodePtr& x) {
         if (x->is_realized()) return;
-        if (fusible_root(*x)) {
+        if (fuse_as_prologue(x)) {
             for (const auto& f : region_frontier(x)) realize(f);
         } else {
             realize(x);
@@ -170,21 +175,62 @@ namespace ormi::hip {
         ORMI_HIP_CHECK(ormi_hip_gemm(&d));
     }
 
+    // Nodes that must hold buffers before `n` can run as one step: a view's
+    // parent, an element-wise region's frontier, the frontier (or the input)
+    // of a reduction, a matmul's operands.
+    static std::vector<NodePtr> dependencies(const NodePtr& n) {
+        if (is_view_op(n->op)) return {n->parents[0]};
+        if (fusible_root(*n)) return region_frontier(n);
+        if (ops::is_reduction(n->op)) {
+            const NodePtr& x = n->parents[0];
+            if (fuse_as_prologue(x)) return region_frontier(x);
+            return {x};
+        }
+        return n->parents;
+    }
+
+    // One node whose dependencies are realized.
+    static void realize_one(const NodePtr& n) {
+        if (n->device.type != DeviceEnum::HIP) throw std::runtime_error("HIP scheduler: node belongs to another device.");
+        if (is_view_op(n->op)) {
+            n->data = n->parents[0]->data;
+            return;
+        }
+        if (fusible_root(*n)) {
+            run_map(n);
+            return;
+        }
+        if (try_execute_graph_break(n)) return;
+        if (n->op == OpEnum::LEAF || n->op == OpEnum::CONST) throw std::runtime_error("HIP scheduler: leaf without a buffer.");
+        throw std::runtime_error(std::string("HIP scheduler: no lowering for op ") + ops::op_name(n->op));
+    }
+
+    // Post-order over dependencies with an explicit stack, so chains of any
+    // length (an unrolled recurrence of matmuls and reductions) need no deep
+    // recursion. A region's frontier only shrinks as nodes get buffers, so the
+    // dependencies pushed for a node still cover it when it runs.
     void realize(const NodePtr& root) {
         if (!root || root->is_realized()) return;
-        if (root->device.type != DeviceEnum::HIP) throw std::runtime_error("HIP scheduler: node belongs to another device.");
-        if (is_view_op(root->op)) {
-            realize(root->parents[0]);
-            root->data = root->parents[0]->data;
-            return;
+        std::vector<NodePtr> stack{root};
+        std::unordered_set<Node*> expanded;
+        while (!stack.empty()) {
+            const NodePtr n = stack.back();
+            if (n->is_realized()) {
+                stack.pop_back();
+                continue;
+            }
+            if (expanded.insert(n.get()).second) {
+                bool pushed = false;
+                for (const auto& d : dependencies(n)) {
+                    if (d->is_realized()) continue;
+                    stack.push_back(d);
+                    pushed = true;
+                }
+                if (pushed) continue;
+            }
+            stack.pop_back();
+            realize_one(n);
         }
-        if (fusible_root(*root)) {
-            run_map(root);
-            return;
-        }
-        if (try_execute_graph_break(root)) return;
-        if (root->op == OpEnum::LEAF || root->op == OpEnum::CONST) throw std::runtime_error("HIP scheduler: leaf without a buffer.");
-        throw std::runtime_error(std::string("HIP scheduler: no lowering for op ") + ops::op_name(root->op));
     }
 
     void realize_group(const std::vector<NodePtr>& roots) {

@@ -522,3 +522,43 @@ def test_mlp_step_small_vs_oracle(cpu, hip):
     np.testing.assert_allclose(lh, lc, rtol=1e-5)
     for a, b in zip(wh, wc):
         np.testing.assert_allclose(a, b, rtol=1e-5, atol=1e-6)
+
+
+def test_long_elementwise_chain_is_cut_into_regions(ob, hip, cabi):
+    """A 3001-op chain becomes regions of at most 256 ops (a handful of cached
+    kernels, not one 3001-op kernel); the result is exact."""
+    import ctypes
+
+    x = np.random.default_rng(51).standard_normal((4, 1000)).astype(np.float32)
+    before = ctypes.c_uint64(0)
+    cabi.ormi_hip_rtc_cache_size(ctypes.byref(before))
+    y = T(x, hip)
+    for _ in range(3001):
+        y = -y
+    got = y.numpy()
+    after = ctypes.c_uint64(0)
+    cabi.ormi_hip_rtc_cache_size(ctypes.byref(after))
+    assert np.array_equal(got, -x)
+    assert after.value - before.value <= 3
+
+
+def test_deep_chain_of_graph_breakers(ob, hip):
+    """Long lazy chains through reductions and matmuls realize with an explicit
+    stack, and a value feeding both a reduction and later element-wise ops is
+    evaluated once (a 64-op prologue cap), so the work stays linear."""
+    x = np.random.default_rng(52).standard_normal((64,)).astype(np.float32)
+    y = T(x, hip)
+    for _ in range(2000):
+        y = y - y.max()          # after the first step the max is 0: exact
+    assert np.array_equal(y.numpy(), x - x.max())
+    m = T(np.array(x.max(), np.float32), hip)
+    X = T(x, hip)
+    y = X
+    for _ in range(20000):
+        y = X + (y.max() - m)    # every level is x again, exactly
+    assert np.array_equal(y.numpy(), x)
+    eye = T(np.eye(8, dtype=np.float32), hip)
+    z = T(x.reshape(8, 8), hip)
+    for _ in range(5000):
+        z = z @ eye
+    assert np.array_equal(z.numpy(), x.reshape(8, 8))
