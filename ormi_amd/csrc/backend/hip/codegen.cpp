@@ -276,14 +276,15 @@ namespace ormi::hip {
                 if (dims.empty()) return;
                 const std::string t = idx();
                 o << ind << "{ " << t << " rem_ = " << var << ";\n";
+                // One scope per dim: each step declares its own quotient.
                 for (size_t k = dims.size() - 1; k >= 1; --k) {
                     const std::string d = std::to_string(dims[k]);
                     if (idx32)
-                        o << ind << "  const int q_ = (int)ormi_fdiv((unsigned)rem_, (unsigned)M" << d << ", (unsigned)(M" << d
-                          << " >> 32));\n";
+                        o << ind << "  { const int q_ = (int)ormi_fdiv((unsigned)rem_, (unsigned)M" << d << ", (unsigned)(M" << d
+                          << " >> 32));";
                     else
-                        o << ind << "  const long long q_ = rem_ / D" << d << ";\n";
-                    o << ind << "  c" << d << " = rem_ - q_ * (" << t << ")D" << d << "; rem_ = q_;\n";
+                        o << ind << "  { const long long q_ = rem_ / D" << d << ";";
+                    o << " c" << d << " = rem_ - q_ * (" << t << ")D" << d << "; rem_ = q_; }\n";
                 }
                 o << ind << "  c" << dims[0] << " = rem_; }\n";
                 for (int d : dims)

