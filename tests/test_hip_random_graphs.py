@@ -101,3 +101,42 @@ def test_random_graph_matches_oracle(cpu, hip, seed):
     tol = 2 ** -7 if last == "bf16" else 1e-4
     np.testing.assert_allclose(got.astype(np.float64), want.astype(np.float64), rtol=tol, atol=tol, equal_nan=True,
                                err_msg=str(spec["ops"]))
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_random_matmul_matches_oracle(cpu, hip, seed):
+    """Random GEMM shapes (ragged ones included) with transposed operands,
+    broadcast batch dims and fp32 or bf16 inputs, against the oracle's k-ordered
+    fp32 loop. Tolerance: fp32 accumulation-order bound (n eps sum|a||b|), and
+    for bf16 the same on the bf16-rounded inputs the oracle also uses."""
+    from ormi_amd import Tensor
+
+    rng = np.random.default_rng(1000 + seed)
+    m, k, n = (int(rng.choice([1, 7, 16, 33, 64, 100, 128, 250, 256])) for _ in range(3))
+    nb = int(rng.integers(0, 3))
+    batch = [int(rng.choice([1, 2, 3])) for _ in range(nb)]
+    ta, tb = bool(rng.random() < 0.4), bool(rng.random() < 0.4)
+    dtype = "bfloat16" if rng.random() < 0.35 else None
+    a_batch = [b if rng.random() < 0.7 else 1 for b in batch]
+    b_batch = [b if rng.random() < 0.7 else 1 for b in batch]
+    a = rng.standard_normal(a_batch + ([k, m] if ta else [m, k])).astype(np.float32)
+    b = rng.standard_normal(b_batch + ([n, k] if tb else [k, n])).astype(np.float32)
+
+    def run(dev):
+        A, B = Tensor(a, dev, dtype=dtype), Tensor(b, dev, dtype=dtype)
+        if ta:
+            A = A.transpose(tuple(range(nb)) + (nb + 1, nb))
+        if tb:
+            B = B.transpose(tuple(range(nb)) + (nb + 1, nb))
+        return (A @ B).numpy()
+
+    got, want = run(hip), run(cpu)
+    assert got.shape == want.shape
+    aa = np.abs(a.astype(np.float64))
+    bb = np.abs(b.astype(np.float64))
+    if ta:
+        aa = np.swapaxes(aa, -1, -2)
+    if tb:
+        bb = np.swapaxes(bb, -1, -2)
+    bound = (k + 2) * np.finfo(np.float32).eps * (aa @ bb)
+    assert np.all(np.abs(got.astype(np.float64) - want) <= bound + 1e-6), (m, k, n, batch, ta, tb, dtype)
