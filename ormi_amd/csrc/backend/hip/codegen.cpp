@@ -25,6 +25,8 @@
 // partial results go to a workspace, and a second kernel combines them in part
 // order (two-pass; deterministic, no atomics).
 #include <algorithm>
+#include <charconv>
+#include <memory>
 #include <cstdlib>
 #include <mutex>
 #include <sstream>
@@ -157,18 +159,44 @@ namespace ormi::hip {
             c = std::move(out);
         }
 
+        // A kernel parameter. Its declaration text is rendered only when a
+        // source is generated (a cache miss); signatures use the fields.
+        struct ArgDecl {
+            bool is_const;
+            const char* type;  // storage type literal: "float", "long long", ...
+            bool is_ptr;
+            const char* name;  // name literal, followed by i and _j when >= 0
+            int i, j;
+        };
+        std::string render(const ArgDecl& d) {
+            std::string r = d.is_const ? "const " : "";
+            r += d.type;
+            r += d.is_ptr ? "* __restrict__ " : " ";
+            r += d.name;
+            if (d.i >= 0) r += std::to_string(d.i);
+            if (d.j >= 0) r += "_" + std::to_string(d.j);
+            return r;
+        }
+
         struct ArgList {
-            std::vector<std::string> decls;
+            std::vector<ArgDecl> decls;
             std::vector<uint64_t> vals;
-            void ptr(const std::string& decl, const void* p) {
-                decls.push_back(decl);
+            void ptr(bool is_const, const char* type, const char* name, const void* p, int i = -1) {
+                decls.push_back({is_const, type, true, name, i, -1});
                 vals.push_back((uint64_t)(uintptr_t)p);
             }
-            void i64(const std::string& name, long long v) {
-                decls.push_back("const long long " + name);
+            void i64(const char* name, long long v, int i = -1, int j = -1) {
+                decls.push_back({true, "long long", false, name, i, j});
                 vals.push_back((uint64_t)v);
             }
         };
+
+        // Appends without stream machinery (the signature is built per launch).
+        void append_int(std::string& s, long long v) {
+            char buf[24];
+            auto r = std::to_chars(buf, buf + sizeof(buf), v);
+            s.append(buf, r.ptr);
+        }
 
         std::string hex_hash(const std::string& s) {
             uint64_t h = 1469598103934665603ull;
@@ -191,7 +219,12 @@ namespace ormi::hip {
             int vec_dim = -1;  // dim whose coordinate advances by VEC
             bool nt_loads = false;
             ArgList args;
-            std::ostringstream body;
+            std::unique_ptr<std::ostringstream> body_;  // created when a source is generated
+
+            std::ostringstream& body() {
+                if (!body_) body_ = std::make_unique<std::ostringstream>();
+                return *body_;
+            }
 
             explicit Gen(const Expr& ex) : e(ex) {
                 for (const auto& L : e.leaves) scalar.push_back(L.scalar);
@@ -236,18 +269,17 @@ namespace ormi::hip {
 
             void declare_leaves() {
                 for (size_t L = 0; L < e.leaves.size(); ++L)
-                    args.ptr(std::string("const ") + storage_type(e.leaves[L].dtype) + "* __restrict__ L" + std::to_string(L),
-                             e.leaves[L].ptr);
+                    args.ptr(true, storage_type(e.leaves[L].dtype), "L", e.leaves[L].ptr, (int)L);
             }
 
             // Size (in VEC groups for the vector dim) and fastdiv magic of each dim.
             void declare_dims() {
                 for (size_t d = 0; d < c.dims.size(); ++d) {
                     const long long n = (int)d == vec_dim ? c.dims[d].size / vec : c.dims[d].size;
-                    args.i64("D" + std::to_string(d), n);
+                    args.i64("D", n, (int)d);
                     if (idx32) {
                         const FastDiv f = make_fastdiv((uint32_t)n);
-                        args.i64("M" + std::to_string(d), (long long)((uint64_t)f.m | ((uint64_t)f.s << 32)));
+                        args.i64("M", (long long)((uint64_t)f.m | ((uint64_t)f.s << 32)), (int)d);
                     }
                 }
             }
@@ -258,7 +290,7 @@ namespace ormi::hip {
                     if (scalar[L]) continue;
                     for (size_t d = 0; d < c.dims.size(); ++d) {
                         const long long s = c.st[L][d];
-                        if (s != 0 && s != 1) args.i64("S" + std::to_string(L) + "_" + std::to_string(d), s);
+                        if (s != 0 && s != 1) args.i64("S", s, (int)L, (int)d);
                     }
                 }
             }
@@ -372,8 +404,8 @@ namespace ormi::hip {
 
             std::string finish(const std::string& kind, int block, KernelLaunch& k) {
                 std::ostringstream sig;
-                for (size_t i = 0; i < args.decls.size(); ++i) sig << (i ? ",\n    " : "    ") << args.decls[i];
-                const std::string kernel_body = body.str();
+                for (size_t i = 0; i < args.decls.size(); ++i) sig << (i ? ",\n    " : "    ") << render(args.decls[i]);
+                const std::string kernel_body = body().str();
                 k.name = "ormi_" + kind + "_" + hex_hash(kernel_body + sig.str());
                 std::ostringstream src;
                 src << kDeviceHeader << "\n\nextern \"C\" __global__ __launch_bounds__(" << block << ") void " << k.name << "(\n"
@@ -401,7 +433,7 @@ namespace ormi::hip {
             return e;
         }
 
-        std::string reduce_name(ReduceOp op) {
+        const char* reduce_name(ReduceOp op) {
             return op == ReduceOp::Sum ? "sum" : op == ReduceOp::Max ? "max" : "argmax";
         }
 
@@ -409,26 +441,61 @@ namespace ormi::hip {
         // pointers: kernel kind, parameter list, which strides are 0 / 1 /
         // general, group layout, vector width, index width, tuning and the tape.
         std::string signature(const Gen& g, const std::string& kind) {
-            std::ostringstream s;
+            std::string s;
+            s.reserve(256);
             const Tuning& t = tuning();
-            s << kind << '|' << t.map_unroll << t.row_unroll << t.col_waves << t.map_nt_loads << t.map_nt_stores << t.reduce_nt_loads << '|';
-            for (const auto& d : g.args.decls) s << d << ';';
-            s << '|';
-            for (const auto& d : g.c.dims) s << (int)d.group;
-            s << '|' << g.vec << ',' << g.vec_dim << ',' << g.idx32 << '|';
+            s += kind;
+            s += '|';
+            for (long long v : {(long long)t.map_unroll, (long long)t.row_unroll, (long long)t.col_waves}) {
+                append_int(s, v);
+                s += ',';
+            }
+            s += char('0' + t.map_nt_loads);
+            s += char('0' + t.map_nt_stores);
+            s += char('0' + t.reduce_nt_loads);
+            s += '|';
+            for (const auto& d : g.args.decls) {
+                s += d.is_const ? 'c' : 'm';
+                s += d.type;
+                s += d.is_ptr ? '*' : ' ';
+                s += d.name;
+                append_int(s, d.i);
+                s += '_';
+                append_int(s, d.j);
+                s += ';';
+            }
+            s += '|';
+            for (const auto& d : g.c.dims) s += char('0' + (int)d.group);
+            s += '|';
+            append_int(s, g.vec);
+            s += ',';
+            append_int(s, g.vec_dim);
+            s += g.idx32 ? ",32|" : ",64|";
             for (size_t L = 0; L < g.e.leaves.size(); ++L) {
                 if (g.scalar[L]) {
-                    s << 'S';
+                    s += 'S';
                     continue;
                 }
-                for (long long v : g.c.st[L]) s << (v == 0 ? '0' : v == 1 ? '1' : 'x');
-                s << ',';
+                for (long long v : g.c.st[L]) s += v == 0 ? '0' : v == 1 ? '1' : 'x';
+                s += ',';
             }
-            s << '|';
-            for (const auto& in : g.e.insts) s << (int)in.op << ',' << in.a << ',' << in.b << ',' << (int)in.cast << ';';
-            s << g.e.root;
-            for (int r : g.e.roots) s << ',' << r;
-            return s.str();
+            s += '|';
+            for (const auto& in : g.e.insts) {
+                append_int(s, (int)in.op);
+                s += ',';
+                append_int(s, in.a);
+                s += ',';
+                append_int(s, in.b);
+                s += ',';
+                append_int(s, (int)in.cast);
+                s += ';';
+            }
+            append_int(s, g.e.root);
+            for (int r : g.e.roots) {
+                s += ',';
+                append_int(s, r);
+            }
+            return s;
         }
 
         // Generated kernels by signature: name and source once emitted, and
@@ -479,6 +546,21 @@ namespace ormi::hip {
         }
     }  // namespace
 
+    std::string PlanInfo::text() const {
+        std::string s = kind;
+        if (op) {
+            s += ' ';
+            s += op;
+        }
+        for (int i = 0; i < n; ++i) {
+            s += ' ';
+            s += field[i].first;
+            s += '=';
+            s += std::to_string(field[i].second);
+        }
+        return s;
+    }
+
     // ------------------------------------------------------------------ map --
     KernelLaunch plan_map(const Expr& expr, const std::vector<int>& shape, void* out, DType out_dtype, int cu) {
         return plan_map_multi(expr, shape, {out}, {out_dtype}, cu);
@@ -517,24 +599,25 @@ namespace ormi::hip {
         auto out_name = [&](size_t r) { return nout == 1 ? std::string("out") : "out" + std::to_string(r); };
         KernelLaunch k;
         for (size_t r = 0; r < nout; ++r)
-            g.args.ptr(std::string(storage_type(out_dtypes[r])) + "* __restrict__ " + out_name(r), outs[r]);
+            g.args.ptr(false, storage_type(out_dtypes[r]), "out", outs[r], nout == 1 ? -1 : (int)r);
         g.declare_leaves();
         g.args.i64("G", G);
         g.declare_dims();
         g.declare_strides();
         k.grid[0] = (uint32_t)grid;
-        {
-            std::ostringstream plan;
-            plan << "map ndim=" << n << " vec=" << g.vec << " idx=" << (g.idx32 ? 32 : 64) << " groups=" << G << " unroll=" << unroll;
-            if (nout > 1) plan << " outputs=" << nout;
-            k.plan = plan.str();
-        }
+        k.plan.kind = "map";
+        k.plan.add("ndim", n);
+        k.plan.add("vec", g.vec);
+        k.plan.add("idx", g.idx32 ? 32 : 64);
+        k.plan.add("groups", G);
+        k.plan.add("unroll", unroll);
+        if (nout > 1) k.plan.add("outputs", (long long)nout);
         resolve(g, "map", block, k, [&] {
             std::vector<int> all;
             for (int d = 0; d < n; ++d) all.push_back(d);
             const std::string t = g.idx();
             const int V = g.vec;
-            std::ostringstream& b = g.body;
+            std::ostringstream& b = g.body();
             g.hoist_scalars(b, "  ");
             b << "  const " << t << " tile = " << tile << ";\n";
             b << "  for (" << t << " base = (" << t << ")blockIdx.x * tile; base < (" << t << ")G; base += (" << t << ")gridDim.x * tile) {\n";
@@ -614,11 +697,10 @@ namespace ormi::hip {
 
         ReducePlan plan;
         KernelLaunch& k = plan.first;
-        const std::string name = reduce_name(op);
+        const char* name = reduce_name(op);
         const bool is_sum = op == ReduceOp::Sum;
         const bool is_arg = op == ReduceOp::Argmax;
         const int V = g.vec;
-        std::ostringstream summary;
 
         if (!column) {
             // ---------------------------------------------------------- row --
@@ -631,8 +713,8 @@ namespace ormi::hip {
             P = RG == 0 ? 1 : (RG + CH - 1) / CH;  // drop empty parts
             g.choose_idx(O * P * 64 + RG * V + 64 * V * RU);
             plan.two_pass = P > 1;
-            g.args.ptr("void* __restrict__ outp", plan.two_pass ? nullptr : out);  // workspace bound later
-            g.args.ptr("int* __restrict__ outi", nullptr);
+            g.args.ptr(false, "void", "outp", plan.two_pass ? nullptr : out);  // workspace bound later
+            g.args.ptr(false, "int", "outi", nullptr);
             g.declare_leaves();
             g.args.i64("NO", O);
             g.args.i64("NP", P);
@@ -641,11 +723,13 @@ namespace ormi::hip {
             g.declare_dims();
             g.declare_strides();
             k.grid[0] = (uint32_t)std::max(1LL, (O * P + 3) / 4);
-            summary << "row " << name << " O=" << O << " R=" << R << " vec=" << V << " parts=" << P << " idx=" << (g.idx32 ? 32 : 64);
-            k.plan = summary.str();
-            resolve(g, "row" + name, 256, k, [&] {
+            k.plan.kind = "row";
+            k.plan.op = name;
+            for (auto [key, v] : {std::pair<const char*, long long>{"O", O}, {"R", R}, {"vec", V}, {"parts", P}, {"idx", g.idx32 ? 32 : 64}})
+                k.plan.add(key, v);
+            resolve(g, std::string("row") + name, 256, k, [&] {
                 const std::string t = g.idx();
-                std::ostringstream& b = g.body;
+                std::ostringstream& b = g.body();
                 g.hoist_scalars(b, "  ");
                 b << "  const int lane = threadIdx.x & 63;\n";
                 b << "  const " << t << " wid = (" << t << ")blockIdx.x * 4 + (" << t << ")(threadIdx.x >> 6);\n";
@@ -719,15 +803,16 @@ namespace ormi::hip {
                 // Second pass: one wave per output row over its P partials, in part order.
                 KernelLaunch& s2 = plan.second;
                 Gen g2(no_expr());  // reads only the workspace
-                g2.args.ptr("void* __restrict__ outp", out);
-                g2.args.ptr("const float* __restrict__ pvals", nullptr);
-                g2.args.ptr("const int* __restrict__ pidx", nullptr);
+                g2.args.ptr(false, "void", "outp", out);
+                g2.args.ptr(true, "float", "pvals", nullptr);
+                g2.args.ptr(true, "int", "pidx", nullptr);
                 g2.args.i64("NO", O);
                 g2.args.i64("NP", P);
                 s2.grid[0] = (uint32_t)std::max(1LL, (O + 3) / 4);
-                s2.plan = "row-finish " + name;
-                resolve(g2, "rowfin" + name, 256, s2, [&] {
-                    std::ostringstream& sb = g2.body;
+                s2.plan.kind = "row-finish";
+                s2.plan.op = name;
+                resolve(g2, std::string("rowfin") + name, 256, s2, [&] {
+                    std::ostringstream& sb = g2.body();
                     sb << "  const int lane = threadIdx.x & 63;\n";
                     sb << "  const long long o = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);\n";
                     sb << "  if (o >= NO) return;\n";
@@ -762,8 +847,8 @@ namespace ormi::hip {
         P = R == 0 ? 1 : (R + CH - 1) / CH;
         g.choose_idx(O * I * P + R + 4LL * W * 4);
         plan.two_pass = P > 1;
-        g.args.ptr("void* __restrict__ outp", plan.two_pass ? nullptr : out);
-        g.args.ptr("int* __restrict__ outi", nullptr);
+        g.args.ptr(false, "void", "outp", plan.two_pass ? nullptr : out);
+        g.args.ptr(false, "int", "outi", nullptr);
         g.declare_leaves();
         g.args.i64("NO", O);
         g.args.i64("NI", I);
@@ -774,12 +859,14 @@ namespace ormi::hip {
         g.declare_dims();
         g.declare_strides();
         k.grid[0] = (uint32_t)std::max(1LL, BI * O * P);
-        summary << "column " << name << " O=" << O << " R=" << R << " I=" << I << " vec=" << V << " waves=" << W << " parts=" << P
-                << " idx=" << (g.idx32 ? 32 : 64);
-        k.plan = summary.str();
-        resolve(g, "col" + name, block, k, [&] {
+        k.plan.kind = "column";
+        k.plan.op = name;
+        for (auto [key, v] : {std::pair<const char*, long long>{"O", O}, {"R", R}, {"I", I}, {"vec", V}, {"waves", W}, {"parts", P},
+                              {"idx", g.idx32 ? 32 : 64}})
+            k.plan.add(key, v);
+        resolve(g, std::string("col") + name, block, k, [&] {
             const std::string t = g.idx();
-            std::ostringstream& b = g.body;
+            std::ostringstream& b = g.body();
             const int CU = 4;  // rows in flight per wave
             g.hoist_scalars(b, "  ");
             b << "  __shared__ float sv[" << W << "][64][" << V << "];\n";
@@ -859,15 +946,16 @@ namespace ormi::hip {
             plan.workspace_bytes = (size_t)(P * O * I) * (sizeof(float) + sizeof(int));
             KernelLaunch& s2 = plan.second;
             Gen g2(no_expr());  // reads only the workspace
-            g2.args.ptr("void* __restrict__ outp", out);
-            g2.args.ptr("const float* __restrict__ pvals", nullptr);
-            g2.args.ptr("const int* __restrict__ pidx", nullptr);
+            g2.args.ptr(false, "void", "outp", out);
+            g2.args.ptr(true, "float", "pvals", nullptr);
+            g2.args.ptr(true, "int", "pidx", nullptr);
             g2.args.i64("NE", O * I);
             g2.args.i64("NP", P);
             s2.grid[0] = (uint32_t)std::max(1LL, (O * I + 255) / 256);
-            s2.plan = "column-finish " + name;
-            resolve(g2, "colfin" + name, 256, s2, [&] {
-                std::ostringstream& sb = g2.body;
+            s2.plan.kind = "column-finish";
+            s2.plan.op = name;
+            resolve(g2, std::string("colfin") + name, 256, s2, [&] {
+                std::ostringstream& sb = g2.body();
                 sb << "  const long long e = (long long)blockIdx.x * 256 + threadIdx.x;\n";
                 sb << "  if (e >= NE) return;\n";
                 if (is_sum) {

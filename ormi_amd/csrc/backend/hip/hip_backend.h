@@ -87,6 +87,19 @@ namespace ormi::hip {
 
     enum class ReduceOp { Sum, Max, Argmax };
 
+    // Summary of a launch plan (tests, debugging), formatted only on request:
+    // "<kind>[ <op>] key=value ...".
+    struct PlanInfo {
+        const char* kind = "";
+        const char* op = nullptr;
+        int n = 0;
+        std::pair<const char*, long long> field[10];
+        void add(const char* key, long long v) {
+            if (n < 10) field[n++] = {key, v};
+        }
+        std::string text() const;
+    };
+
     // A generated kernel: source, entry name, launch shape, packed arguments.
     struct KernelLaunch {
         std::string source;          // empty when the kernel came from the cache
@@ -96,7 +109,7 @@ namespace ormi::hip {
         uint32_t grid[3] = {1, 1, 1};
         uint32_t block[3] = {256, 1, 1};
         std::vector<uint64_t> args;  // every parameter is 8 bytes
-        std::string plan;            // human-readable summary (tests, debugging)
+        PlanInfo plan;
     };
 
     // Launch-shape knobs of the generated kernels. Defaults are the values

@@ -169,7 +169,7 @@ namespace {
         }
         d["source"] = k.source;
         d["name"] = k.name;
-        d["plan"] = k.plan;
+        d["plan"] = k.plan.text();
         d["grid"] = std::vector<uint32_t>{k.grid[0], k.grid[1], k.grid[2]};
         d["num_args"] = k.args.size();
         return d;
@@ -188,7 +188,7 @@ namespace {
         py::dict d;
         d["source"] = k.source;
         d["name"] = k.name;
-        d["plan"] = k.plan;
+        d["plan"] = k.plan.text();
         d["num_leaves"] = e.leaves.size();
         d["num_insts"] = e.insts.size();
         return d;
