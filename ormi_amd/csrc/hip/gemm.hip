@@ -82,22 +82,58 @@ struct TrF32 {
 };
 
 // Fetch one BMN x BK operand tile (rows = m or n, columns = k) into registers
-// and store it to LDS as [BMN][KCH + 1] 16-byte chunks.
-// KC: k is the unit-stride index. NT: threads per block.
+// and store it to LDS. KC: k is the unit-stride index. NT: threads per block.
+// LDS layouts, both giving each lane a 16-byte MFMA fragment of 4 consecutive
+// k (chunk ch holds k = 4 ch .. 4 ch + 3) of one m / n row:
+//   KC, and 16-bit mn-contiguous: [BMN][KCH + 1] 16-byte chunks; 16-bit
+//       mn-contiguous tiles are transposed in registers on the way.
+//   32-bit mn-contiguous (KMN): [BK][BMN + 8] floats, stored as loaded (each
+//       k-row is one contiguous run, so the stores cannot conflict); a
+//       fragment is 4 dword reads. The lane halves of a read sit 4 k-rows =
+//       4 (BMN + 8) dwords apart, an odd multiple of 32 banks of the 64, so
+//       they do not conflict either.
 template <typename Tr, int BMN, int BK, bool KC, bool EVEN, int NT>
 struct TileLoader {
     static constexpr int VE = Tr::VE, ES = Tr::ESIZE;
     static constexpr int KCH = BK / VE;  // 16-byte chunks per row
+    static constexpr bool KMN = !KC && ES == 4;
+    static constexpr int PITCH = BMN + 8;  // KMN row pitch in floats
+    static_assert(!KMN || (4 * PITCH) % 64 == 32, "KMN pitch must put lane halves 32 banks apart");
+    static constexpr int LDS_BYTES = KMN ? BK * PITCH * 4 : BMN * (KCH + 1) * 16;
     // Direct copy: 16-byte chunks per thread.
     static constexpr int NCHUNK = (BMN * KCH) / NT;
     // Transposed copy: each thread owns VE k-rows x MC mn-elements.
     static constexpr int MC = (BMN * BK) / (VE * NT);
     static constexpr int MCW = MC * ES / 4;  // dwords per k-row
+    static constexpr int MCU = BMN / (MC > 0 ? MC : 1);  // mn units per k-row (KMN)
     static constexpr int NREG = KC ? NCHUNK * 4 : VE * MCW;
     static_assert(KC ? (NCHUNK >= 1 && NCHUNK * NT == BMN * KCH) : (KCH == 8 && MC >= 1 && MC * VE * NT == BMN * BK && MCW >= 1),
                   "tile / thread-count combination not supported");
+    static_assert(!KMN || (MCU % 32 == 0 && MCU * MC == BMN), "KMN needs whole half-waves per k-row");
 
     unsigned r[NREG];
+
+    // Thread -> (mn unit of MC elements, k block of VE rows) for mn-contiguous tiles.
+    __device__ static int unit_mn() {
+        const int tid = threadIdx.x;
+        if constexpr (KMN) return tid % MCU;
+        else return (tid >> 6) * 8 + (tid & 7);
+    }
+    __device__ static int unit_kb() {
+        const int tid = threadIdx.x;
+        if constexpr (KMN) return tid / MCU;
+        else return (tid & 63) >> 3;
+    }
+
+    // The 16-byte fragment of mn-row `row`, chunk `ch`.
+    __device__ static u32x4_t frag(const char* lds, int row, int ch) {
+        if constexpr (KMN) {
+            const unsigned* f = (const unsigned*)lds + ch * 4 * PITCH + row;
+            return u32x4_t{f[0], f[PITCH], f[2 * PITCH], f[3 * PITCH]};
+        } else {
+            return ((const u32x4_t*)lds)[row * (KCH + 1) + ch];
+        }
+    }
 
     __device__ void load(const char* base, long long s_mn, long long s_k, int mn0, int k0, int MN, int K) {
         const int tid = threadIdx.x;
@@ -113,9 +149,7 @@ struct TileLoader {
                 for (int e = 0; e < 4; ++e) r[i * 4 + e] = v[e];
             }
         } else {
-            const int lane = tid & 63, wave = tid >> 6;
-            const int mc = wave * 8 + (lane & 7);  // mn unit of MC elements
-            const int kb = lane >> 3;              // k block of VE rows
+            const int mc = unit_mn(), kb = unit_kb();
             const int mn = mn0 + mc * MC;
 #pragma unroll
             for (int j = 0; j < VE; ++j) {
@@ -140,30 +174,43 @@ struct TileLoader {
         }
     }
 
-    __device__ void store(u32x4_t (*lds)[KCH + 1]) const {
+    __device__ void store(char* smem) const {
         const int tid = threadIdx.x;
         if constexpr (KC) {
+            u32x4_t (*lds)[KCH + 1] = (u32x4_t (*)[KCH + 1])smem;
 #pragma unroll
             for (int i = 0; i < NCHUNK; ++i) {
                 const int idx = i * NT + tid;
                 lds[idx / KCH][idx % KCH] = u32x4_t{r[i * 4], r[i * 4 + 1], r[i * 4 + 2], r[i * 4 + 3]};
             }
+        } else if constexpr (KMN) {
+            const int mc = unit_mn(), kb = unit_kb();
+            unsigned* row0 = (unsigned*)smem + (kb * VE) * PITCH + mc * MC;
+#pragma unroll
+            for (int j = 0; j < VE; ++j) {
+                unsigned* d = row0 + j * PITCH;
+                if constexpr (MCW == 4) {
+                    *(u32x4_t*)d = u32x4_t{r[j * 4], r[j * 4 + 1], r[j * 4 + 2], r[j * 4 + 3]};
+                } else if constexpr (MCW == 2) {
+                    typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+                    *(u32x2_t*)d = u32x2_t{r[j * 2], r[j * 2 + 1]};
+                } else {
+                    *d = r[j];
+                }
+            }
         } else {
-            const int lane = tid & 63, wave = tid >> 6;
-            const int mc = wave * 8 + (lane & 7), kb = lane >> 3;
+            // 16-bit mn-contiguous: element i of k-row j is half (i & 1) of
+            // dword i / 2 of that row.
+            static_assert(ES == 2, "32-bit mn-contiguous tiles use the KMN layout");
+            u32x4_t (*lds)[KCH + 1] = (u32x4_t (*)[KCH + 1])smem;
+            const int mc = unit_mn(), kb = unit_kb();
 #pragma unroll
             for (int i = 0; i < MC; ++i) {
                 u32x4_t t;
-                if constexpr (ES == 2) {
-                    // Element i of k-row j is half (i & 1) of dword i / 2 of that row.
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const unsigned x = r[(2 * e) * MCW + (i >> 1)], y = r[(2 * e + 1) * MCW + (i >> 1)];
-                        t[e] = (i & 1) ? ((x >> 16) | (y & 0xffff0000u)) : ((x & 0xffffu) | (y << 16));
-                    }
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) t[e] = r[e * MCW + i];
+                for (int e = 0; e < 4; ++e) {
+                    const unsigned x = r[(2 * e) * MCW + (i >> 1)], y = r[(2 * e + 1) * MCW + (i >> 1)];
+                    t[e] = (i & 1) ? ((x >> 16) | (y & 0xffff0000u)) : ((x & 0xffffu) | (y << 16));
                 }
                 lds[mc * MC + i][kb] = t;
             }
@@ -180,8 +227,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_kernel(GemmParams p)
     using LA = TileLoader<Tr, BM, BK, A_KC, EVEN, NT>;
     using LB = TileLoader<Tr, BN, BK, B_KC, EVEN, NT>;
 
-    __shared__ u32x4_t As[2][BM][KCH + 1];
-    __shared__ u32x4_t Bs[2][BN][KCH + 1];
+    __shared__ __attribute__((aligned(16))) char As[2][LA::LDS_BYTES];
+    __shared__ __attribute__((aligned(16))) char Bs[2][LB::LDS_BYTES];
 
     // ---- tile index: XCD-aware remap, then groups of 4 tile rows.
     const int T = p.tiles_m * p.tiles_n;
@@ -244,18 +291,18 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_kernel(GemmParams p)
         u32x4_t af[2][TM], bfr[2][TN];
         const int half = lane >> 5, row = lane & 31;
 #pragma unroll
-        for (int i = 0; i < TM; ++i) af[0][i] = As[cur][wm * WTM + i * 32 + row][half];
+        for (int i = 0; i < TM; ++i) af[0][i] = LA::frag(As[cur], wm * WTM + i * 32 + row, half);
 #pragma unroll
-        for (int j = 0; j < TN; ++j) bfr[0][j] = Bs[cur][wn * WTN + j * 32 + row][half];
+        for (int j = 0; j < TN; ++j) bfr[0][j] = LB::frag(Bs[cur], wn * WTN + j * 32 + row, half);
 #pragma unroll
         for (int ks = 0; ks < KCH / 2; ++ks) {
             const int q = ks & 1;
             if (ks + 1 < KCH / 2) {
                 const int chunk = (ks + 1) * 2 + half;
 #pragma unroll
-                for (int i = 0; i < TM; ++i) af[q ^ 1][i] = As[cur][wm * WTM + i * 32 + row][chunk];
+                for (int i = 0; i < TM; ++i) af[q ^ 1][i] = LA::frag(As[cur], wm * WTM + i * 32 + row, chunk);
 #pragma unroll
-                for (int j = 0; j < TN; ++j) bfr[q ^ 1][j] = Bs[cur][wn * WTN + j * 32 + row][chunk];
+                for (int j = 0; j < TN; ++j) bfr[q ^ 1][j] = LB::frag(Bs[cur], wn * WTN + j * 32 + row, chunk);
             }
 #pragma unroll
             for (int i = 0; i < TM; ++i)
