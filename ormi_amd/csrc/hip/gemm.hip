@@ -695,11 +695,14 @@ struct Launcher {
 //   1: 256x256x64, 2x4 waves (128x64 per wave, 2 waves/SIMD)
 //   2: 256x256x64, 4x2 waves (64x128 per wave, 2 waves/SIMD)
 //   3: 128x128x64, 2x2 waves (64x64 per wave, 2 blocks/CU)
-// fp32 configurations (ORMI_GEMM_CFG32; the default, 2, measured fastest on MI355X
-// for the forward and both backward layouts of the benchmark shapes):
+// fp32 configurations (ORMI_GEMM_CFG32 forces one; by default 2, measured fastest
+// on MI355X for the forward and both backward layouts of the benchmark shapes,
+// and 3 for short-K shapes that 128x256 tiles cannot spread over the CUs):
 //   0: 128x128x32, 2x2 waves (64x64 per wave)
 //   1: 256x128x32, 4x2 waves (64x64 per wave)
 //   2: 128x256x32, 2x4 waves (64x64 per wave)
+//   3: 128x128x32, 2x4 waves (64x32 per wave)
+//   4: 128x128x32, 4x2 waves (32x64 per wave)
 static int env_cfg(const char* name, int dflt) {
     const char* v = std::getenv(name);
     return v && *v ? std::atoi(v) : dflt;
@@ -727,6 +730,8 @@ static Cfg cfg32(int id) {
     switch (id) {
         case 1: return Launcher<TrF32, 256, 128, 32, 4, 2>::cfg;
         case 2: return Launcher<TrF32, 128, 256, 32, 2, 4>::cfg;
+        case 3: return Launcher<TrF32, 128, 128, 32, 2, 4>::cfg;
+        case 4: return Launcher<TrF32, 128, 128, 32, 4, 2>::cfg;
         default: return Launcher<TrF32, 128, 128, 32, 2, 2>::cfg;
     }
 }
@@ -734,6 +739,8 @@ static void run32(int id, const GemmParams& p, dim3 grid, bool even, bool a_kc, 
     switch (id) {
         case 1: Launcher<TrF32, 256, 128, 32, 4, 2>::run(p, grid, even, a_kc, b_kc); break;
         case 2: Launcher<TrF32, 128, 256, 32, 2, 4>::run(p, grid, even, a_kc, b_kc); break;
+        case 3: Launcher<TrF32, 128, 128, 32, 2, 4>::run(p, grid, even, a_kc, b_kc); break;
+        case 4: Launcher<TrF32, 128, 128, 32, 4, 2>::run(p, grid, even, a_kc, b_kc); break;
         default: Launcher<TrF32, 128, 128, 32, 2, 2>::run(p, grid, even, a_kc, b_kc); break;
     }
 }
@@ -1306,7 +1313,18 @@ extern "C" int ormi_hip_gemm(const ormi_gemm_desc* d) {
     const int dma_bk = f32 ? 64 : cfg_dma<TrBF16>(dma_id).BK;
     const bool dma = !f32 && env_cfg("ORMI_GEMM_DMA", 1) != 0 && d->K % dma_bk == 0 && (a_kc || d->M % 8 == 0) &&
                      (b_kc || d->N % 8 == 0) && a_span < (1LL << 32) && b_span < (1LL << 32);
-    const int id = dma ? dma_id : f32 ? env_cfg("ORMI_GEMM_CFG32", 2) : env_cfg("ORMI_GEMM_CFG16", 0);
+    int id = dma ? dma_id : f32 ? env_cfg("ORMI_GEMM_CFG32", -1) : env_cfg("ORMI_GEMM_CFG16", 0);
+    if (f32 && id < 0) {
+        // 128x256 tiles (config 2) unless they cannot fill the compute units
+        // and K is short: then 128x128 tiles (config 3) fill them without a
+        // K split, whose partial round trip and second kernel cost more than
+        // the smaller tiles lose at K <= 1024 (measured: 1024x4096x1024 86 us
+        // against 94 us split; at K = 2048 the split is 4% faster).
+        const long long cus_ll = compute_units();
+        const long long t2 = (long long)((d->M + 127) / 128) * ((d->N + 255) / 256) * batch;
+        const long long t3 = (long long)((d->M + 127) / 128) * ((d->N + 127) / 128) * batch;
+        id = (t2 < cus_ll && t3 >= cus_ll && d->K <= 1024) ? 3 : 2;
+    }
     const Cfg cf = dma ? (d->dtype == ORMI_DTYPE_BF16 ? cfg_dma<TrBF16>(id) : cfg_dma<TrF16>(id))
                        : f32 ? cfg32(id) : (d->dtype == ORMI_DTYPE_BF16 ? cfg16<TrBF16>(id) : cfg16<TrF16>(id));
     p.tiles_m = (d->M + cf.BM - 1) / cf.BM;
