@@ -139,6 +139,54 @@ typedef struct ormi_gemm_desc {
 } ormi_gemm_desc;
 int ormi_hip_gemm(const ormi_gemm_desc* desc);
 
+/* GEMM with an element-wise epilogue: each output element v = (A B)[b][m][n]
+ * is transformed before it is stored, so a pointwise consumer of the product
+ * needs no second pass over it. The reference's cublasSgemmBatched call fixes
+ * alpha = 1, beta = 0 (matmul.cu:94-103); these kinds generalize that
+ * C = alpha A B + beta C step to the consumers autograd and an SGD update put
+ * on a matmul. Arithmetic is fp32 in exactly the order written below, with
+ * no fused multiply-add, so the result matches the unfused element-wise
+ * kernel bit for bit.
+ *   ORMI_GEMM_EPI_NONE       C = v
+ *   ORMI_GEMM_EPI_ADD        t = (s ? v * s[0] : v);
+ *                            form 0: C = D + t   1: C = D - t   2: C = t - D
+ *   ORMI_GEMM_EPI_UNARY      C = fn(v); aux (when not NULL) = v, laid out like C
+ *   ORMI_GEMM_EPI_MUL_FN_D   C = v * fn(D)
+ * D[b][m][n] is read at d + sum(coord[i] * d_batch_stride[i]) + m*d_stride_m
+ * + n*d_stride_n (fp32; a stride of 0 broadcasts), s at s[0] (fp32, device
+ * memory). fn is one of the ORMI_GEMM_FN_* functions, with the same device
+ * code the fused element-wise kernels use. NULL epi is ORMI_GEMM_EPI_NONE.
+ * C, aux and D must not overlap unless D == C with C's own layout (an
+ * in-place update reads each element before writing it). */
+enum {
+    ORMI_GEMM_EPI_NONE = 0,
+    ORMI_GEMM_EPI_ADD = 1,
+    ORMI_GEMM_EPI_UNARY = 2,
+    ORMI_GEMM_EPI_MUL_FN_D = 3
+};
+enum {
+    ORMI_GEMM_FN_IDENTITY = 0,
+    ORMI_GEMM_FN_RELU = 1,
+    ORMI_GEMM_FN_STEP = 2,
+    ORMI_GEMM_FN_TANH = 3,
+    ORMI_GEMM_FN_TANH_GRAD = 4,
+    ORMI_GEMM_FN_SIGMOID = 5,
+    ORMI_GEMM_FN_SIGMOID_GRAD = 6,
+    ORMI_GEMM_FN_GELU = 7,
+    ORMI_GEMM_FN_GELU_GRAD = 8
+};
+typedef struct ormi_gemm_epilogue {
+    int          kind;   /* ORMI_GEMM_EPI_* */
+    int          fn;     /* ORMI_GEMM_FN_*: UNARY and MUL_FN_D */
+    int          form;   /* ADD: 0, 1 or 2 */
+    const float* s;      /* ADD: scale, or NULL for none */
+    const float* d;      /* ADD and MUL_FN_D */
+    int64_t      d_stride_m, d_stride_n;
+    int64_t      d_batch_stride[ORMI_GEMM_MAX_BATCH_DIMS];
+    float*       aux;    /* UNARY: also store v here, or NULL */
+} ormi_gemm_epilogue;
+int ormi_hip_gemm_ex(const ormi_gemm_desc* desc, const ormi_gemm_epilogue* epi);
+
 /* ---------------------------------------------------------------- timing --
  * HIP events on the library's stream, for measuring kernel time from
  * outside (benchmarks). */

@@ -32,9 +32,11 @@ ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 HIPCC = str(ROCM / "bin" / "hipcc")
 ARCH = os.environ.get("ORMI_HIP_ARCH", "gfx950")
 
-# Every HIP translation unit: gfx950 only, packed-FP32 instructions disabled.
+# Every HIP translation unit: gfx950 only, packed-FP32 instructions disabled,
+# no FP contraction (the generated kernels' setting, so GEMM epilogues round
+# like the element-wise kernels they replace).
 HIP_FLAGS = [
-    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-ffp-contract=off", "-Wall", "-Wno-unused-function"]
@@ -82,6 +84,13 @@ def _compile_cxx(src: Path, includes: list[Path], extra: list[str] | None = None
     return obj
 
 
+def _compile_hip(src: Path) -> Path:
+    obj = OBJDIR / "obj" / (str(src.relative_to(ROOT)).replace(os.sep, "__") + ".o")
+    obj.parent.mkdir(parents=True, exist_ok=True)
+    _run([HIPCC, *HIP_FLAGS, f"-I{INCLUDE}", f"-I{CSRC / 'hip'}", "-c", str(src), "-o", str(obj)])
+    return obj
+
+
 def build(verbose: bool = False) -> None:
     if verbose:
         os.environ["ORMI_BUILD_VERBOSE"] = "1"
@@ -97,19 +106,18 @@ def build(verbose: bool = False) -> None:
     jobs = max(1, min(jobs, 16))
 
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        hip_job = ex.submit(
-            _run,
-            [HIPCC, *HIP_FLAGS, "-shared", f"-I{INCLUDE}", f"-I{CSRC / 'hip'}", *map(str, HIP_SOURCES),
-             "-o", str(HIP_LIB), "-lhiprtc", f"-Wl,-rpath,{ROCM / 'lib'}"],
-        )
+        # One object per HIP translation unit, compiled in parallel (the GEMM
+        # units take the longest), then linked into the shared library.
+        hip_objs = [ex.submit(_compile_hip, s) for s in HIP_SOURCES]
         core_objs = [ex.submit(_compile_cxx, s, core_inc) for s in CORE_SOURCES]
         bind_objs = [ex.submit(_compile_cxx, s, core_inc + py_inc) for s in BINDING_SOURCES]
         oracle_objs = [ex.submit(_compile_cxx, s, core_inc) for s in ORACLE_SOURCES]
-        hip_job.result()
+        hip = [f.result() for f in hip_objs]
         core = [f.result() for f in core_objs]
         binds = [f.result() for f in bind_objs]
         oracle = [f.result() for f in oracle_objs]
 
+    _run([HIPCC, *HIP_FLAGS, "-shared", *map(str, hip), "-o", str(HIP_LIB), "-lhiprtc", f"-Wl,-rpath,{ROCM / 'lib'}"])
     _run(["g++", "-shared", *map(str, core), "-o", str(CORE_LIB), "-Wl,-soname,libormi_core.so", f"-L{LIBDIR}", "-lormi_hip",
           "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{ROCM / 'lib'}", "-Wl,--no-undefined"])
     _run(["g++", "-shared", *map(str, binds), "-o", str(MODULE_PATH), f"-L{LIBDIR}", "-lormi_core", "-lormi_hip",

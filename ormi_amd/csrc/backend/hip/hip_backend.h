@@ -159,6 +159,10 @@ namespace ormi::hip {
     // Realize several nodes together: element-wise roots of the same shape share
     // one multi-output kernel (each input read once); the rest realize in order.
     void realize_group(const std::vector<NodePtr>& roots);
+    // Element-wise nodes run as a GEMM epilogue so far (ormi_hip_gemm_ex), and
+    // the switch for that matching (on unless ORMI_GEMM_EPILOGUE=0).
+    uint64_t gemm_epilogue_count();
+    void set_gemm_epilogue(bool on);
 
     // ------------------------------------------------------- allocator --
     struct AllocatorStats {

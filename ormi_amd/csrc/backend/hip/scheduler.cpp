@@ -15,6 +15,8 @@
 // Reductions and MATMUL are registered as graph breakers for DeviceEnum::HIP
 // (the reference's plugin point, csrc/backend/graph_breakers.h:12-14).
 #include <algorithm>
+#include <atomic>
+#include <cstdlib>
 #include <mutex>
 #include <unordered_map>
 #include <unordered_set>
@@ -35,16 +37,6 @@ namespace ormi::hip {
             return ormi_hip_get_props(&p) == ORMI_HIP_OK && p.compute_units > 0 ? p.compute_units : 256;
         }();
         return cu;
-    }
-
-    static void run_map(const NodePtr& root) {
-        for (const auto& f : region_frontier(root)) realize(f);
-        const Expr e = build_expr(root, root->view.shape);
-        auto out = empty(root->view.shape, DeviceEnum::HIP, root->dtype);
-        root->data = out;
-        root->view.strides = calc_contiguous_strides(root->view.shape);
-        if (out->numel() == 0) return;
-        launch(plan_map(e, root->view.shape, out->ptr, root->dtype, device_compute_units()));
     }
 
     // Realize what a reduction reads: a pointwise producer of at most
@@ -104,10 +96,10 @@ namespace ormi::hip {
         return c;
     }
 
-    // MATMUL on the HIP device (replaces cuda::matmul, csrc/backend/cuda/kernels/blas/
-    // matmul.cu:19-122): same shape rule, trans/ld derived from strides, batch
-    // dims broadcast with stride 0, contiguous fp32 output.
-    static void matmul_handler(const NodePtr& root) {
+    // The product of MATMUL node `root` into `out` (contiguous fp32, root's
+    // shape), with an optional epilogue: same shape rule as the reference,
+    // trans/ld derived from strides, batch dims broadcast with stride 0.
+    static void gemm_into(const NodePtr& root, float* out, const ormi_gemm_epilogue* epi) {
         NodePtr A = root->parents[0], B = root->parents[1];
         realize(A);
         realize(B);
@@ -121,10 +113,6 @@ namespace ormi::hip {
         const auto& vb = B->view;
         const auto& vo = root->view;
         const int na = (int)va.shape.size(), nb = (int)vb.shape.size(), no = (int)vo.shape.size();
-        auto out = empty(vo.shape, DeviceEnum::HIP, DType::Float32);
-        root->data = out;
-        root->view.strides = calc_contiguous_strides(vo.shape);
-        if (out->numel() == 0) return;
 
         ormi_gemm_desc d{};
         d.dtype = dt == DType::Float32 ? ORMI_DTYPE_F32 : dt == DType::BFloat16 ? ORMI_DTYPE_BF16 : ORMI_DTYPE_F16;
@@ -137,7 +125,7 @@ namespace ormi::hip {
         d.b = B->data->ptr;
         d.b_stride_k = vb.strides[nb - 2];
         d.b_stride_n = vb.strides[nb - 1];
-        d.c = (float*)out->ptr;
+        d.c = out;
         // Batch dims: drop extent-1 dims, then each operand's batch stride is its
         // own stride where it has that dim with extent > 1, else 0 (broadcast).
         std::vector<int> bshape;
@@ -172,7 +160,219 @@ namespace ormi::hip {
             d.a_batch_stride[i] = abs[i];
             d.b_batch_stride[i] = bbs[i];
         }
-        ORMI_HIP_CHECK(ormi_hip_gemm(&d));
+        ORMI_HIP_CHECK(ormi_hip_gemm_ex(&d, epi));
+    }
+
+    // MATMUL on the HIP device (replaces cuda::matmul, csrc/backend/cuda/kernels/blas/
+    // matmul.cu:19-122).
+    static void matmul_handler(const NodePtr& root) {
+        realize(root->parents[0]);
+        realize(root->parents[1]);
+        auto out = empty(root->view.shape, DeviceEnum::HIP, DType::Float32);
+        root->data = out;
+        root->view.strides = calc_contiguous_strides(root->view.shape);
+        if (out->numel() == 0) return;
+        gemm_into(root, (float*)out->ptr, nullptr);
+    }
+
+    // ------------------------------------------------ GEMM epilogue fusion --
+    // An element-wise node whose expression is one of ormi_hip_gemm_ex's
+    // epilogues applied to an unrealized 2-D fp32 MATMUL runs as that GEMM,
+    // and the product never makes its own round trip through HBM:
+    //   D + p*s, D - p*s, p*s - D (and without s)  the SGD update w - grad*lr
+    //   f(p), f in relu/tanh/sigmoid/gelu           a forward activation; p is
+    //                                               also stored as the
+    //                                               MATMUL's buffer (autograd
+    //                                               reads it again)
+    //   p * f'(D), f' in step/tanh'/sigmoid'/gelu'  an activation's backward
+    //   (and p * D)                                 on the dX GEMM
+    // D is a realized or non-element-wise node (leaf, view, matmul, reduction),
+    // s a one-element fp32 node. The epilogue rounds each operation as the
+    // element-wise kernel would, so results are identical either way. A
+    // MATMUL left unrealized is computed again if something reads it later.
+    // ORMI_GEMM_EPILOGUE=0 (or set_gemm_epilogue(false)) turns the matching off.
+    struct EpilogueMatch {
+        NodePtr g, d, s;
+        int kind = ORMI_GEMM_EPI_NONE, fn = ORMI_GEMM_FN_IDENTITY, form = 0;
+    };
+
+    static std::atomic<bool>& epilogue_switch() {
+        static std::atomic<bool> on{[] {
+            const char* v = std::getenv("ORMI_GEMM_EPILOGUE");
+            return !(v && *v && std::atoi(v) == 0);
+        }()};
+        return on;
+    }
+    static bool epilogue_enabled() { return epilogue_switch().load(); }
+    void set_gemm_epilogue(bool on) { epilogue_switch().store(on); }
+
+    static std::atomic<uint64_t> g_epilogue_gemms{0};
+    uint64_t gemm_epilogue_count() { return g_epilogue_gemms.load(); }
+
+    static bool is_open_product(const NodePtr& x, const std::vector<int>& shape) {
+        return x->op == OpEnum::MATMUL && !x->is_realized() && x->device.type == DeviceEnum::HIP && x->view.shape == shape &&
+               shape.size() == 2 && x->parents[0]->view.shape.size() == 2 && x->parents[1]->view.shape.size() == 2;
+    }
+    static bool is_scale(const NodePtr& x) {
+        return x->dtype == DType::Float32 && shape_numel(x->view.shape) == 1 && (x->is_realized() || !fusible_root(*x));
+    }
+    // D operand: fp32, broadcasts right-aligned to the 2-D output, already a
+    // buffer or produced by a non-element-wise op.
+    static bool is_operand(const NodePtr& x, const std::vector<int>& shape) {
+        if (x->dtype != DType::Float32 || (!x->is_realized() && fusible_root(*x))) return false;
+        const auto& xs = x->view.shape;
+        if (xs.size() > shape.size()) return false;
+        for (size_t i = 0; i < xs.size(); ++i) {
+            const int v = xs[xs.size() - 1 - i];
+            if (v != 1 && v != shape[shape.size() - 1 - i]) return false;
+        }
+        return true;
+    }
+    static int unary_fn(OpEnum op) {
+        switch (op) {
+            case OpEnum::RELU: return ORMI_GEMM_FN_RELU;
+            case OpEnum::TANH: return ORMI_GEMM_FN_TANH;
+            case OpEnum::SIGMOID: return ORMI_GEMM_FN_SIGMOID;
+            case OpEnum::GELU: return ORMI_GEMM_FN_GELU;
+            default: return -1;
+        }
+    }
+    static int grad_fn(OpEnum op) {
+        switch (op) {
+            case OpEnum::STEP: return ORMI_GEMM_FN_STEP;
+            case OpEnum::TANH_GRAD: return ORMI_GEMM_FN_TANH_GRAD;
+            case OpEnum::SIGMOID_GRAD: return ORMI_GEMM_FN_SIGMOID_GRAD;
+            case OpEnum::GELU_GRAD: return ORMI_GEMM_FN_GELU_GRAD;
+            default: return -1;
+        }
+    }
+
+    static bool match_epilogue(const NodePtr& n, EpilogueMatch& m) {
+        if (!epilogue_enabled() || n->is_realized() || !fusible_root(*n) || n->dtype != DType::Float32) return false;
+        const auto& shape = n->view.shape;
+        if (shape.size() != 2) return false;
+        const NodePtr& x = n->parents[0];
+        // p, or p * s / s * p as an unrealized element-wise MUL.
+        auto term = [&](const NodePtr& t, NodePtr& g, NodePtr& sc) {
+            if (is_open_product(t, shape)) {
+                g = t;
+                sc = nullptr;
+                return true;
+            }
+            if (t->op != OpEnum::MUL || t->is_realized() || !fusible_interior(*t) || t->dtype != DType::Float32) return false;
+            for (int k = 0; k < 2; ++k) {
+                const NodePtr &u = t->parents[k], &v = t->parents[1 - k];
+                if (is_open_product(u, shape) && is_scale(v)) {
+                    g = u;
+                    sc = v;
+                    return true;
+                }
+            }
+            return false;
+        };
+        if (n->op == OpEnum::ADD || n->op == OpEnum::SUB) {
+            const NodePtr& y = n->parents[1];
+            NodePtr g, sc;
+            m.kind = ORMI_GEMM_EPI_ADD;
+            if (term(y, g, sc) && is_operand(x, shape) && x != g) {
+                m.form = n->op == OpEnum::ADD ? 0 : 1;  // D + t, D - t
+                m.d = x;
+            } else if (term(x, g, sc) && is_operand(y, shape) && y != g) {
+                m.form = n->op == OpEnum::ADD ? 0 : 2;  // t + D (= D + t), t - D
+                m.d = y;
+            } else {
+                return false;
+            }
+            m.g = g;
+            m.s = sc;
+            return true;
+        }
+        if (ops::op_arity(n->op) == 1) {
+            const int fn = unary_fn(n->op);
+            if (fn < 0 || !is_open_product(x, shape)) return false;
+            m.kind = ORMI_GEMM_EPI_UNARY;
+            m.fn = fn;
+            m.g = x;
+            return true;
+        }
+        if (n->op == OpEnum::MUL) {
+            for (int k = 0; k < 2; ++k) {
+                const NodePtr &u = n->parents[k], &v = n->parents[1 - k];
+                if (!is_open_product(u, shape)) continue;
+                if (is_operand(v, shape) && v != u) {
+                    m.kind = ORMI_GEMM_EPI_MUL_FN_D;
+                    m.fn = ORMI_GEMM_FN_IDENTITY;
+                    m.g = u;
+                    m.d = v;
+                    return true;
+                }
+                const int fn = v->is_realized() || !fusible_interior(*v) ? -1 : grad_fn(v->op);
+                if (fn >= 0 && v->dtype == DType::Float32 && is_operand(v->parents[0], shape) && v->parents[0] != u) {
+                    m.kind = ORMI_GEMM_EPI_MUL_FN_D;
+                    m.fn = fn;
+                    m.g = u;
+                    m.d = v->parents[0];
+                    return true;
+                }
+            }
+        }
+        return false;
+    }
+
+    // Run n as its matched GEMM; false (nothing launched) when a realized
+    // operand turns out not to be fp32.
+    static bool run_gemm_epilogue(const NodePtr& n, const EpilogueMatch& m) {
+        if (m.d) realize(m.d);
+        if (m.s) realize(m.s);
+        if ((m.d && m.d->data->dtype != DType::Float32) || (m.s && m.s->data->dtype != DType::Float32)) return false;
+        ormi_gemm_epilogue e{};
+        e.kind = m.kind;
+        e.fn = m.fn;
+        e.form = m.form;
+        if (m.s) e.s = (const float*)m.s->data->ptr;
+        if (m.d) {
+            e.d = (const float*)m.d->data->ptr;
+            const auto& ds = m.d->view.shape;
+            const auto& dst = m.d->view.strides;
+            const bool scalar = ds.empty() || m.d->data->numel() == 1;
+            int64_t st[2] = {0, 0};
+            for (size_t i = 0; i < ds.size() && !scalar; ++i) {
+                const size_t p = 2 - ds.size() + i;
+                if (ds[i] != 1) st[p] = dst[i];
+            }
+            e.d_stride_m = st[0];
+            e.d_stride_n = st[1];
+        }
+        auto out = empty(n->view.shape, DeviceEnum::HIP, DType::Float32);
+        std::shared_ptr<Buffer> aux;
+        if (m.kind == ORMI_GEMM_EPI_UNARY) {
+            aux = empty(m.g->view.shape, DeviceEnum::HIP, DType::Float32);
+            e.aux = (float*)aux->ptr;
+        }
+        if (out->numel() > 0) gemm_into(m.g, (float*)out->ptr, &e);
+        n->data = out;
+        n->view.strides = calc_contiguous_strides(n->view.shape);
+        if (aux) {
+            m.g->data = aux;
+            m.g->view.strides = calc_contiguous_strides(m.g->view.shape);
+        }
+        g_epilogue_gemms.fetch_add(1);
+        return true;
+    }
+
+    // An element-wise region: a matched GEMM epilogue, else one fused kernel.
+    static void run_map(const NodePtr& root) {
+        {
+            EpilogueMatch m;
+            if (match_epilogue(root, m) && run_gemm_epilogue(root, m)) return;
+        }
+        for (const auto& f : region_frontier(root)) realize(f);
+        const Expr e = build_expr(root, root->view.shape);
+        auto out = empty(root->view.shape, DeviceEnum::HIP, root->dtype);
+        root->data = out;
+        root->view.strides = calc_contiguous_strides(root->view.shape);
+        if (out->numel() == 0) return;
+        launch(plan_map(e, root->view.shape, out->ptr, root->dtype, device_compute_units()));
     }
 
     // Nodes that must hold buffers before `n` can run as one step: a view's
@@ -180,7 +380,16 @@ namespace ormi::hip {
     // of a reduction, a matmul's operands.
     static std::vector<NodePtr> dependencies(const NodePtr& n) {
         if (is_view_op(n->op)) return {n->parents[0]};
-        if (fusible_root(*n)) return region_frontier(n);
+        if (fusible_root(*n)) {
+            EpilogueMatch m;
+            if (match_epilogue(n, m)) {
+                std::vector<NodePtr> deps{m.g->parents[0], m.g->parents[1]};
+                if (m.d) deps.push_back(m.d);
+                if (m.s) deps.push_back(m.s);
+                return deps;
+            }
+            return region_frontier(n);
+        }
         if (ops::is_reduction(n->op)) {
             const NodePtr& x = n->parents[0];
             if (fuse_as_prologue(x)) return region_frontier(x);
@@ -242,7 +451,8 @@ namespace ormi::hip {
         for (const auto& r : roots) {
             if (!r || r->is_realized() || !seen.insert(r.get()).second) continue;
             if (r->device.type != DeviceEnum::HIP) throw std::runtime_error("HIP scheduler: node belongs to another device.");
-            if (!fusible_interior(*r)) {
+            EpilogueMatch m;
+            if (!fusible_interior(*r) || match_epilogue(r, m)) {
                 rest.push_back(r);
                 continue;
             }

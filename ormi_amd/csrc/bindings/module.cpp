@@ -338,6 +338,10 @@ PYBIND11_MODULE(ormi_backend, m) {
         return d;
     }, "HIP caching allocator counters.");
     m.def("empty_cache", &hip::empty_cache, "Return every cached HIP block to the device.");
+    m.def("gemm_epilogue_count", &hip::gemm_epilogue_count,
+          "Element-wise nodes realized as a GEMM epilogue (ormi_hip_gemm_ex) in this process.");
+    m.def("set_gemm_epilogue", &hip::set_gemm_epilogue, py::arg("on"),
+          "Turn GEMM epilogue fusion on or off (default: on unless ORMI_GEMM_EPILOGUE=0).");
     m.def("_plan_kernel", &plan_kernel);
     m.def("_plan_group", &plan_group);
     m.def("realize_all", &execute_graph_group,

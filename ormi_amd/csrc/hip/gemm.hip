@@ -6,17 +6,23 @@
 //   * Block tile BM x BN x BK, WGM x WGN wave64s; each wave owns a
 //     (BM/WGM) x (BN/WGN) sub-tile of 32x32 MFMA tiles
 //     (v_mfma_f32_32x32x16_{bf16,f16}, or v_mfma_f32_32x32x2_f32).
-//   * Both operands sit in LDS as [mn][k] rows of BK elements plus 16 bytes of
+//   * Operands sit in LDS as [mn][k] rows of BK elements plus 16 bytes of
 //     padding (144-byte rows), so every MFMA operand fragment is one
-//     conflict-free 16-byte ds_read per lane. LDS is double-buffered: the next
+//     conflict-free 16-byte ds_read per lane (fp32 mn-contiguous operands:
+//     [k][mn] rows, below). LDS is double-buffered: the next
 //     k-tile is fetched from HBM into registers while the current one feeds the
 //     MFMAs, and fragments for the next k-step are read from LDS while the
 //     current k-step's MFMAs issue.
 //   * An operand whose k index is contiguous in memory ("N" for A, "T" for B)
 //     is copied 16 bytes at a time. One whose m/n index is contiguous is
-//     fetched as VE x MC blocks (VE = elements per 16 bytes) and transposed in
-//     registers before the LDS store, so NN, NT and TN (the forward and the
-//     two backward GEMMs autograd issues) all run the same MFMA loop.
+//     fetched as VE x MC blocks (VE = elements per 16 bytes); 16-bit blocks
+//     are transposed in registers before the LDS store, 32-bit ones stay
+//     k-major in LDS and form fragments from dword reads. NN, NT and TN (the
+//     forward and the two backward GEMMs autograd issues) all run the same
+//     MFMA loop.
+//   * An element-wise epilogue (ormi_hip_gemm_ex) is applied in the store of
+//     the fp32 default configurations (gemm_epi.hip), otherwise in the pass
+//     that finishes a K split.
 //   * The tile index is remapped so the 8 XCDs (round-robin block dispatch)
 //     each own a compact group of tiles, sharing operand panels in their L2.
 //   * When the output has too few tiles to occupy the 256 CUs, K is split
@@ -25,6 +31,7 @@
 //   * Shapes or strides the fast path cannot take (alignment, ragged 16-byte
 //     chunks) run a plain tiled kernel instead.
 #include <hip/hip_runtime.h>
+#include <algorithm>
 #include <cstdint>
 #include <cstdlib>
 #include <mutex>
@@ -32,308 +39,9 @@
 
 #include "ormi_hip.h"
 #include "ormi_hip_internal.h"
+#include "gemm_mfma.h"
 
 namespace ormi_hip {
-
-typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
-
-struct GemmParams {
-    const char* a;
-    const char* b;
-    float* c;          // final output, or the split-K workspace
-    int M, N, K;
-    long long a_sm, a_sk, b_sk, b_sn;  // element strides
-    int batch_ndim;
-    int batch_shape[ORMI_GEMM_MAX_BATCH_DIMS];
-    long long a_bs[ORMI_GEMM_MAX_BATCH_DIMS];
-    long long b_bs[ORMI_GEMM_MAX_BATCH_DIMS];
-    int tiles_m, tiles_n;
-    int batch;         // number of batches
-    int splits;        // K splits (1 = write C directly)
-    int k_per_split;   // multiple of BK
-};
-
-// Element-type traits: storage size, elements per 16 bytes, MFMA step.
-struct TrBF16 {
-    static constexpr int ESIZE = 2, VE = 8;
-    __device__ static void mma(const u32x4_t& a, const u32x4_t& b, f32x16_t& acc) {
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), acc, 0, 0, 0);
-    }
-};
-struct TrF16 {
-    static constexpr int ESIZE = 2, VE = 8;
-    __device__ static void mma(const u32x4_t& a, const u32x4_t& b, f32x16_t& acc) {
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), acc, 0, 0, 0);
-    }
-};
-struct TrF32 {
-    static constexpr int ESIZE = 4, VE = 4;
-    // One 16-byte fragment holds 4 consecutive k per lane: four K=2 MFMAs.
-    // Lane half h and step s cover k = 4h + s of the 8-k group, identically
-    // for A and B, so every k is paired with itself.
-    __device__ static void mma(const u32x4_t& a, const u32x4_t& b, f32x16_t& acc) {
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a[s]), __uint_as_float(b[s]), acc, 0, 0, 0);
-    }
-};
-
-// Fetch one BMN x BK operand tile (rows = m or n, columns = k) into registers
-// and store it to LDS. KC: k is the unit-stride index. NT: threads per block.
-// LDS layouts, both giving each lane a 16-byte MFMA fragment of 4 consecutive
-// k (chunk ch holds k = 4 ch .. 4 ch + 3) of one m / n row:
-//   KC, and 16-bit mn-contiguous: [BMN][KCH + 1] 16-byte chunks; 16-bit
-//       mn-contiguous tiles are transposed in registers on the way.
-//   32-bit mn-contiguous (KMN): [BK][BMN + 8] floats, stored as loaded (each
-//       k-row is one contiguous run, so the stores cannot conflict); a
-//       fragment is 4 dword reads. The lane halves of a read sit 4 k-rows =
-//       4 (BMN + 8) dwords apart, an odd multiple of 32 banks of the 64, so
-//       they do not conflict either.
-template <typename Tr, int BMN, int BK, bool KC, bool EVEN, int NT>
-struct TileLoader {
-    static constexpr int VE = Tr::VE, ES = Tr::ESIZE;
-    static constexpr int KCH = BK / VE;  // 16-byte chunks per row
-    static constexpr bool KMN = !KC && ES == 4;
-    static constexpr int PITCH = BMN + 8;  // KMN row pitch in floats
-    static_assert(!KMN || (4 * PITCH) % 64 == 32, "KMN pitch must put lane halves 32 banks apart");
-    static constexpr int LDS_BYTES = KMN ? BK * PITCH * 4 : BMN * (KCH + 1) * 16;
-    // Direct copy: 16-byte chunks per thread.
-    static constexpr int NCHUNK = (BMN * KCH) / NT;
-    // Transposed copy: each thread owns VE k-rows x MC mn-elements.
-    static constexpr int MC = (BMN * BK) / (VE * NT);
-    static constexpr int MCW = MC * ES / 4;  // dwords per k-row
-    static constexpr int MCU = BMN / (MC > 0 ? MC : 1);  // mn units per k-row (KMN)
-    static constexpr int NREG = KC ? NCHUNK * 4 : VE * MCW;
-    static_assert(KC ? (NCHUNK >= 1 && NCHUNK * NT == BMN * KCH) : (KCH == 8 && MC >= 1 && MC * VE * NT == BMN * BK && MCW >= 1),
-                  "tile / thread-count combination not supported");
-    static_assert(!KMN || (MCU % 32 == 0 && MCU * MC == BMN), "KMN needs whole half-waves per k-row");
-
-    unsigned r[NREG];
-
-    // Thread -> (mn unit of MC elements, k block of VE rows) for mn-contiguous tiles.
-    __device__ static int unit_mn() {
-        const int tid = threadIdx.x;
-        if constexpr (KMN) return tid % MCU;
-        else return (tid >> 6) * 8 + (tid & 7);
-    }
-    __device__ static int unit_kb() {
-        const int tid = threadIdx.x;
-        if constexpr (KMN) return tid / MCU;
-        else return (tid & 63) >> 3;
-    }
-
-    // The 16-byte fragment of mn-row `row`, chunk `ch`.
-    __device__ static u32x4_t frag(const char* lds, int row, int ch) {
-        if constexpr (KMN) {
-            const unsigned* f = (const unsigned*)lds + ch * 4 * PITCH + row;
-            return u32x4_t{f[0], f[PITCH], f[2 * PITCH], f[3 * PITCH]};
-        } else {
-            return ((const u32x4_t*)lds)[row * (KCH + 1) + ch];
-        }
-    }
-
-    __device__ void load(const char* base, long long s_mn, long long s_k, int mn0, int k0, int MN, int K) {
-        const int tid = threadIdx.x;
-        if constexpr (KC) {
-#pragma unroll
-            for (int i = 0; i < NCHUNK; ++i) {
-                const int idx = i * NT + tid;
-                const int row = idx / KCH, kc = idx % KCH;
-                const int mn = mn0 + row, k = k0 + kc * VE;
-                u32x4_t v = {0u, 0u, 0u, 0u};
-                if (EVEN || (mn < MN && k < K)) v = *(const u32x4_t*)(base + ((long long)mn * s_mn + k) * ES);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) r[i * 4 + e] = v[e];
-            }
-        } else {
-            const int mc = unit_mn(), kb = unit_kb();
-            const int mn = mn0 + mc * MC;
-#pragma unroll
-            for (int j = 0; j < VE; ++j) {
-                const int k = k0 + kb * VE + j;
-                const bool ok = EVEN || (mn < MN && k < K);
-                const char* p = base + ((long long)k * s_k + mn) * ES;
-                if constexpr (MCW == 4) {
-                    u32x4_t v = {0u, 0u, 0u, 0u};
-                    if (ok) v = *(const u32x4_t*)p;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) r[j * 4 + e] = v[e];
-                } else if constexpr (MCW == 2) {
-                    typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
-                    u32x2_t v = {0u, 0u};
-                    if (ok) v = *(const u32x2_t*)p;
-                    r[j * 2] = v[0];
-                    r[j * 2 + 1] = v[1];
-                } else {
-                    r[j] = ok ? *(const unsigned*)p : 0u;
-                }
-            }
-        }
-    }
-
-    __device__ void store(char* smem) const {
-        const int tid = threadIdx.x;
-        if constexpr (KC) {
-            u32x4_t (*lds)[KCH + 1] = (u32x4_t (*)[KCH + 1])smem;
-#pragma unroll
-            for (int i = 0; i < NCHUNK; ++i) {
-                const int idx = i * NT + tid;
-                lds[idx / KCH][idx % KCH] = u32x4_t{r[i * 4], r[i * 4 + 1], r[i * 4 + 2], r[i * 4 + 3]};
-            }
-        } else if constexpr (KMN) {
-            const int mc = unit_mn(), kb = unit_kb();
-            unsigned* row0 = (unsigned*)smem + (kb * VE) * PITCH + mc * MC;
-#pragma unroll
-            for (int j = 0; j < VE; ++j) {
-                unsigned* d = row0 + j * PITCH;
-                if constexpr (MCW == 4) {
-                    *(u32x4_t*)d = u32x4_t{r[j * 4], r[j * 4 + 1], r[j * 4 + 2], r[j * 4 + 3]};
-                } else if constexpr (MCW == 2) {
-                    typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
-                    *(u32x2_t*)d = u32x2_t{r[j * 2], r[j * 2 + 1]};
-                } else {
-                    *d = r[j];
-                }
-            }
-        } else {
-            // 16-bit mn-contiguous: element i of k-row j is half (i & 1) of
-            // dword i / 2 of that row.
-            static_assert(ES == 2, "32-bit mn-contiguous tiles use the KMN layout");
-            u32x4_t (*lds)[KCH + 1] = (u32x4_t (*)[KCH + 1])smem;
-            const int mc = unit_mn(), kb = unit_kb();
-#pragma unroll
-            for (int i = 0; i < MC; ++i) {
-                u32x4_t t;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const unsigned x = r[(2 * e) * MCW + (i >> 1)], y = r[(2 * e + 1) * MCW + (i >> 1)];
-                    t[e] = (i & 1) ? ((x >> 16) | (y & 0xffff0000u)) : ((x & 0xffffu) | (y << 16));
-                }
-                lds[mc * MC + i][kb] = t;
-            }
-        }
-    }
-};
-
-template <typename Tr, int BM, int BN, int BK, int WGM, int WGN, bool A_KC, bool B_KC, bool EVEN>
-__global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_kernel(GemmParams p) {
-    constexpr int NT = 64 * WGM * WGN;
-    constexpr int VE = Tr::VE, KCH = BK / VE;
-    constexpr int WTM = BM / WGM, WTN = BN / WGN, TM = WTM / 32, TN = WTN / 32;
-    static_assert(TM >= 1 && TN >= 1 && KCH % 2 == 0, "bad tile shape");
-    using LA = TileLoader<Tr, BM, BK, A_KC, EVEN, NT>;
-    using LB = TileLoader<Tr, BN, BK, B_KC, EVEN, NT>;
-
-    __shared__ __attribute__((aligned(16))) char As[2][LA::LDS_BYTES];
-    __shared__ __attribute__((aligned(16))) char Bs[2][LB::LDS_BYTES];
-
-    // ---- tile index: XCD-aware remap, then groups of 4 tile rows.
-    const int T = p.tiles_m * p.tiles_n;
-    int t = blockIdx.x;
-    if ((T & 7) == 0) t = (t & 7) * (T >> 3) + (t >> 3);
-    constexpr int GROUP = 4;
-    const int group_size = GROUP * p.tiles_n;
-    const int g = t / group_size, first_m = g * GROUP;
-    const int gm = min(p.tiles_m - first_m, GROUP);
-    const int tm_idx = first_m + (t % group_size) % gm;
-    const int tn_idx = (t % group_size) / gm;
-    const int m0 = tm_idx * BM, n0 = tn_idx * BN;
-
-    // ---- batch and K split
-    const int split = blockIdx.z % p.splits;
-    int bidx = blockIdx.z / p.splits;
-    long long a_off = 0, b_off = 0;
-    const long long c_off = ((long long)split * p.batch + bidx) * p.M * p.N;
-    for (int d = p.batch_ndim - 1; d >= 0; --d) {
-        const int coord = bidx % p.batch_shape[d];
-        bidx /= p.batch_shape[d];
-        a_off += coord * p.a_bs[d];
-        b_off += coord * p.b_bs[d];
-    }
-    const char* a = p.a + a_off * Tr::ESIZE;
-    const char* b = p.b + b_off * Tr::ESIZE;
-    float* c = p.c + c_off;
-    const int kbeg = split * p.k_per_split;
-    const int kend = min(p.K, kbeg + p.k_per_split);
-
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wm = wave / WGN, wn = wave % WGN;
-    const int KT = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
-
-    f32x16_t acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-    LA la;
-    LB lb;
-    if (KT > 0) {
-        la.load(a, p.a_sm, p.a_sk, m0, kbeg, p.M, kend);
-        lb.load(b, p.b_sn, p.b_sk, n0, kbeg, p.N, kend);
-        la.store(As[0]);
-        lb.store(Bs[0]);
-    }
-    __syncthreads();
-
-    for (int kt = 0; kt < KT; ++kt) {
-        const int cur = kt & 1;
-        const bool more = kt + 1 < KT;
-        if (more) {
-            la.load(a, p.a_sm, p.a_sk, m0, kbeg + (kt + 1) * BK, p.M, kend);
-            lb.load(b, p.b_sn, p.b_sk, n0, kbeg + (kt + 1) * BK, p.N, kend);
-        }
-        u32x4_t af[2][TM], bfr[2][TN];
-        const int half = lane >> 5, row = lane & 31;
-#pragma unroll
-        for (int i = 0; i < TM; ++i) af[0][i] = LA::frag(As[cur], wm * WTM + i * 32 + row, half);
-#pragma unroll
-        for (int j = 0; j < TN; ++j) bfr[0][j] = LB::frag(Bs[cur], wn * WTN + j * 32 + row, half);
-#pragma unroll
-        for (int ks = 0; ks < KCH / 2; ++ks) {
-            const int q = ks & 1;
-            if (ks + 1 < KCH / 2) {
-                const int chunk = (ks + 1) * 2 + half;
-#pragma unroll
-                for (int i = 0; i < TM; ++i) af[q ^ 1][i] = LA::frag(As[cur], wm * WTM + i * 32 + row, chunk);
-#pragma unroll
-                for (int j = 0; j < TN; ++j) bfr[q ^ 1][j] = LB::frag(Bs[cur], wn * WTN + j * 32 + row, chunk);
-            }
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int j = 0; j < TN; ++j) Tr::mma(af[q][i], bfr[q][j], acc[i][j]);
-            // The next tile goes to the other LDS buffer halfway through this
-            // tile's MFMAs: every wave finished reading that buffer before the
-            // previous barrier, and its write latency now overlaps matrix work.
-            if (ks == KCH / 4 - 1 && more) {
-                la.store(As[cur ^ 1]);
-                lb.store(Bs[cur ^ 1]);
-            }
-        }
-        __syncthreads();
-    }
-
-    // ---- epilogue: 32x32 MFMA result layout, lane l / register r ->
-    // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const int col = n0 + wn * WTN + j * 32 + (lane & 31);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (EVEN || (row < p.M && col < p.N)) c[(long long)row * p.N + col] = acc[i][j][r];
-            }
-        }
-    }
-}
 
 // ------------------------------------------------------------------------
 // 16-bit GEMM with direct HBM->LDS loads (gfx950 global_load_lds_dwordx4).
@@ -616,14 +324,68 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_dma_kernel(GemmParams p) 
     }
 }
 
-// C[e] = sum over splits s (in order) of ws[s][e].
-__global__ __launch_bounds__(256) void splitk_reduce_kernel(float* __restrict__ c, const float* __restrict__ ws, long long n,
-                                                            int splits) {
-    const long long stride = (long long)gridDim.x * blockDim.x;
-    for (long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += stride) {
-        float s = ws[e];
-        for (int q = 1; q < splits; ++q) s += ws[(long long)q * n + e];
-        c[e] = s;
+// Second pass after a K split, or after a kernel that has no epilogue of its
+// own: v = sum over splits q (in order) of ws[q][b][m][n], then the epilogue
+// (or a plain store). Rows of all batches run along grid y; each thread takes
+// 4 consecutive columns of a row, issuing all its loads (16-byte ones when
+// VEC: N % 4 == 0 and C, aux 16-byte aligned) before its stores.
+struct FinishParams {
+    float* c;
+    const float* ws;
+    long long n;  // elements per split: batch * M * N
+    int splits, M, N, rows;  // rows = batch * M
+    int batch_ndim;
+    int batch_shape[ORMI_GEMM_MAX_BATCH_DIMS];
+    Epi epi;
+};
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void gemm_finish_kernel(FinishParams f) {
+    const Epi& e = f.epi;
+    const float sv = e.s ? *e.s : 0.0f;
+    const bool reads_d = epi_reads_d(e);
+    for (int row = blockIdx.y; row < f.rows; row += gridDim.y) {
+        const int bi = row / f.M, m = row - bi * f.M;
+        long long d_off = 0;
+        if (reads_d) {
+            int rest = bi;
+            for (int d = f.batch_ndim - 1; d >= 0; --d) {
+                d_off += (long long)(rest % f.batch_shape[d]) * e.d_bs[d];
+                rest /= f.batch_shape[d];
+            }
+            d_off += (long long)m * e.d_sm;
+        }
+        const long long base = (long long)row * f.N;
+        for (int col0 = (blockIdx.x * blockDim.x + threadIdx.x) * 4; col0 < f.N; col0 += gridDim.x * blockDim.x * 4) {
+            const int cnt = min(4, f.N - col0);
+            float v[4] = {0.0f, 0.0f, 0.0f, 0.0f}, dv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (reads_d) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    if (k < cnt) dv[k] = e.d[d_off + (long long)(col0 + k) * e.d_sn];
+            }
+            for (int q = 0; q < f.splits; ++q) {
+                const float* w = f.ws + (long long)q * f.n + base + col0;
+                float t[4];
+                if (VEC) {
+                    const ormi_f4 x = *(const ormi_f4*)w;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) t[k] = x[k];
+                } else {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) t[k] = k < cnt ? w[k] : 0.0f;
+                }
+#pragma unroll
+                for (int k = 0; k < 4; ++k) v[k] = q == 0 ? t[k] : v[k] + t[k];
+            }
+            if (VEC && e.kind == ORMI_GEMM_EPI_NONE) {
+                *(ormi_f4*)(f.c + base + col0) = ormi_f4{v[0], v[1], v[2], v[3]};
+            } else {
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    if (k < cnt) epi_store(e, sv, f.c, e.aux, base + col0 + k, dv[k], v[k]);
+            }
+        }
     }
 }
 
@@ -646,7 +408,7 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(GemmParams p) {
     __shared__ float Bs[16][17];
     const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
     const int row = blockIdx.y * 16 + ty, col = blockIdx.x * 16 + tx;
-    long long a_off = 0, b_off = 0;
+    long long a_off = 0, b_off = 0, d_off = 0;
     int bidx = blockIdx.z;
     const long long c_off = (long long)bidx * p.M * p.N;
     for (int d = p.batch_ndim - 1; d >= 0; --d) {
@@ -654,6 +416,7 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(GemmParams p) {
         bidx /= p.batch_shape[d];
         a_off += coord * p.a_bs[d];
         b_off += coord * p.b_bs[d];
+        d_off += coord * p.epi.d_bs[d];
     }
     float acc = 0.0f;
     for (int k0 = 0; k0 < p.K; k0 += 16) {
@@ -666,7 +429,11 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(GemmParams p) {
         for (int kk = 0; kk < 16; ++kk) acc = __builtin_fmaf(As[ty][kk], Bs[kk][tx], acc);
         __syncthreads();
     }
-    if (row < p.M && col < p.N) p.c[c_off + (long long)row * p.N + col] = acc;
+    if (row < p.M && col < p.N) {
+        const Epi& e = p.epi;
+        const float dv = epi_reads_d(e) ? e.d[d_off + row * e.d_sm + col * e.d_sn] : 0.0f;
+        epi_store(e, e.s ? *e.s : 0.0f, p.c + c_off, e.aux ? e.aux + c_off : nullptr, (long long)row * p.N + col, dv, acc);
+    }
 }
 
 // ------------------------------------------------------------------ dispatch --
@@ -1233,7 +1000,74 @@ static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 using namespace ormi_hip;
 
-extern "C" int ormi_hip_gemm(const ormi_gemm_desc* d) {
+namespace ormi_hip {
+// The epilogue as the kernels take it; an error for a malformed one.
+static int make_epi(const ormi_gemm_desc* d, const ormi_gemm_epilogue* in, long long batch, Epi* out) {
+    *out = Epi{};
+    out->kind = ORMI_GEMM_EPI_NONE;
+    if (!in || in->kind == ORMI_GEMM_EPI_NONE) return ORMI_HIP_OK;
+    if (in->kind < ORMI_GEMM_EPI_ADD || in->kind > ORMI_GEMM_EPI_MUL_FN_D)
+        return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_gemm_ex: unknown epilogue kind");
+    if (in->fn < ORMI_GEMM_FN_IDENTITY || in->fn > ORMI_GEMM_FN_GELU_GRAD)
+        return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_gemm_ex: unknown epilogue function");
+    if (in->kind == ORMI_GEMM_EPI_ADD && (in->form < 0 || in->form > 2))
+        return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_gemm_ex: ADD form must be 0, 1 or 2");
+    const bool needs_d = in->kind == ORMI_GEMM_EPI_ADD || in->kind == ORMI_GEMM_EPI_MUL_FN_D;
+    if (needs_d && !in->d) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_gemm_ex: epilogue needs D");
+    auto misaligned = [](const void* q) { return ((uintptr_t)q & 3u) != 0; };
+    if ((needs_d && misaligned(in->d)) || (in->s && misaligned(in->s)) || (in->aux && misaligned(in->aux)))
+        return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_gemm_ex: epilogue operands must be 4-byte aligned");
+    const float* c0 = d->c;
+    const float* c1 = d->c + batch * d->M * d->N;
+    const bool aux_used = in->kind == ORMI_GEMM_EPI_UNARY && in->aux;
+    if (aux_used && in->aux < c1 && in->aux + batch * d->M * d->N > c0)
+        return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_gemm_ex: aux overlaps C");
+    if (needs_d && in->d >= c0 && in->d < c1) {
+        // In place only with C's own layout: each element is read before the
+        // same thread writes it.
+        bool same = in->d == c0 && in->d_stride_m == d->N && in->d_stride_n == 1;
+        long long contig = (long long)d->M * d->N;
+        for (int i = d->batch_ndim - 1; i >= 0 && same; --i) {
+            same = in->d_batch_stride[i] == contig || d->batch_shape[i] == 1;
+            contig *= d->batch_shape[i];
+        }
+        if (!same) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_gemm_ex: D overlaps C with another layout");
+    }
+    out->kind = in->kind;
+    out->fn = in->fn;
+    out->form = in->form;
+    out->s = in->kind == ORMI_GEMM_EPI_ADD ? in->s : nullptr;
+    out->d = needs_d ? in->d : nullptr;
+    out->d_sm = needs_d ? in->d_stride_m : 0;
+    out->d_sn = needs_d ? in->d_stride_n : 0;
+    for (int i = 0; i < ORMI_GEMM_MAX_BATCH_DIMS; ++i) out->d_bs[i] = needs_d && i < d->batch_ndim ? in->d_batch_stride[i] : 0;
+    out->aux = aux_used ? in->aux : nullptr;
+    return ORMI_HIP_OK;
+}
+
+static void launch_finish(const ormi_gemm_desc* d, const float* ws, int splits, long long batch, const Epi& epi) {
+    FinishParams f{};
+    f.c = d->c;
+    f.ws = ws;
+    f.n = batch * d->M * d->N;
+    f.splits = splits;
+    f.M = d->M;
+    f.N = d->N;
+    f.rows = (int)(batch * d->M);
+    f.batch_ndim = d->batch_ndim;
+    for (int i = 0; i < d->batch_ndim; ++i) f.batch_shape[i] = d->batch_shape[i];
+    f.epi = epi;
+    const int gx = std::min((d->N + 1023) / 1024, 64);
+    const int gy = std::max(1, std::min({f.rows, compute_units() * 32 / gx, 65535}));
+    const bool vec = d->N % 4 == 0 && ((uintptr_t)d->c & 15u) == 0 && ((uintptr_t)epi.aux & 15u) == 0;
+    if (vec) gemm_finish_kernel<true><<<dim3(gx, gy), 256>>>(f);
+    else gemm_finish_kernel<false><<<dim3(gx, gy), 256>>>(f);
+}
+}  // namespace ormi_hip
+
+extern "C" int ormi_hip_gemm(const ormi_gemm_desc* d) { return ormi_hip_gemm_ex(d, nullptr); }
+
+extern "C" int ormi_hip_gemm_ex(const ormi_gemm_desc* d, const ormi_gemm_epilogue* epi_in) {
     if (!d) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_gemm: null descriptor");
     if (d->M < 0 || d->N < 0 || d->K < 0) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_gemm: negative dimension");
     if (d->batch_ndim < 0 || d->batch_ndim > ORMI_GEMM_MAX_BATCH_DIMS)
@@ -1248,7 +1082,11 @@ extern "C" int ormi_hip_gemm(const ormi_gemm_desc* d) {
     if (batch > 65535) return fail(ORMI_HIP_ERR_UNSUPPORTED, "ormi_hip_gemm: more than 65535 batches");
     if ((long long)d->M * d->N == 0) return ORMI_HIP_OK;
     if (!d->a || !d->b || !d->c) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_gemm: null operand");
-    int rc = ensure_init();
+    if (batch * d->M > 0x7fffffffLL) return fail(ORMI_HIP_ERR_UNSUPPORTED, "ormi_hip_gemm: more than 2^31 output rows");
+    Epi epi;
+    int rc = make_epi(d, epi_in, batch, &epi);
+    if (rc != ORMI_HIP_OK) return rc;
+    rc = ensure_init();
     if (rc != ORMI_HIP_OK) return rc;
 
     GemmParams p{};
@@ -1267,10 +1105,21 @@ extern "C" int ormi_hip_gemm(const ormi_gemm_desc* d) {
     p.batch = (int)batch;
     p.splits = 1;
     p.k_per_split = d->K;
+    p.epi = epi;
 
     if (d->K == 0) {
+        // The product is 0; with an epilogue, 0 goes through it.
         const float zero = 0.0f;
-        return ormi_hip_fill(d->c, &zero, 4, (size_t)batch * d->M * d->N);
+        const size_t out_elems = (size_t)batch * d->M * d->N;
+        if (epi.kind == ORMI_GEMM_EPI_NONE) return ormi_hip_fill(d->c, &zero, 4, out_elems);
+        void* ws = nullptr;
+        rc = workspace(out_elems * sizeof(float), &ws);
+        if (rc == ORMI_HIP_OK) rc = ormi_hip_fill(ws, &zero, 4, out_elems);
+        if (rc != ORMI_HIP_OK) return rc;
+        launch_finish(d, (const float*)ws, 1, batch, epi);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return fail(ORMI_HIP_ERR_RUNTIME, std::string("ormi_hip_gemm launch: ") + hipGetErrorString(e));
+        return ORMI_HIP_OK;
     }
 
     const bool f32 = d->dtype == ORMI_DTYPE_F32;
@@ -1346,23 +1195,32 @@ extern "C" int ormi_hip_gemm(const ormi_gemm_desc* d) {
     p.splits = splits;
     p.k_per_split = kps;
     const size_t out_elems = (size_t)batch * d->M * d->N;
-    if (splits > 1) {
+    // The epilogue runs inside the fp32 kernels of configurations 2 and 3
+    // (the fp32 defaults) for shapes in whole tiles and the functions those
+    // kernels are instantiated for (epi_in_store). Other kernels store the
+    // plain product and the finish pass applies it: the direct-load 16-bit
+    // kernels keep their epilogue arguments few (they are pinned in scalar
+    // registers ahead of the main loop), and an epilogue in every unrolled
+    // store loop of every configuration would multiply the library's code.
+    const bool even = d->M % cf.BM == 0 && d->N % cf.BN == 0 && d->K % cf.BK == 0;
+    const bool epi_in_kernel = !dma && f32 && (id == 2 || id == 3) && even && epi_in_store(epi);
+    const bool finish = splits > 1 || (!epi_in_kernel && epi.kind != ORMI_GEMM_EPI_NONE);
+    if (finish) {
         void* ws = nullptr;
         rc = workspace(out_elems * splits * sizeof(float), &ws);
         if (rc != ORMI_HIP_OK) return rc;
         p.c = (float*)ws;
+        p.epi = Epi{};
+        p.epi.kind = ORMI_GEMM_EPI_NONE;
     }
-    const bool even = d->M % cf.BM == 0 && d->N % cf.BN == 0 && d->K % cf.BK == 0;
     dim3 grid(p.tiles_m * p.tiles_n, 1, (unsigned)(batch * splits));
     if (dma && d->dtype == ORMI_DTYPE_BF16) run_dma<TrBF16>(id, p, grid, a_kc, b_kc);
     else if (dma) run_dma<TrF16>(id, p, grid, a_kc, b_kc);
+    else if (f32 && p.epi.kind != ORMI_GEMM_EPI_NONE) run32_epi(id, p, grid, a_kc, b_kc);
     else if (f32) run32(id, p, grid, even, a_kc, b_kc);
     else if (d->dtype == ORMI_DTYPE_BF16) run16<TrBF16>(id, p, grid, even, a_kc, b_kc);
     else run16<TrF16>(id, p, grid, even, a_kc, b_kc);
-    if (splits > 1) {
-        const unsigned blocks = (unsigned)std::min<size_t>((out_elems + 255) / 256, (size_t)cus * 16);
-        splitk_reduce_kernel<<<blocks, 256>>>(d->c, p.c, (long long)out_elems, splits);
-    }
+    if (finish) launch_finish(d, p.c, splits, batch, epi);
     e = hipGetLastError();
     if (e != hipSuccess) return fail(ORMI_HIP_ERR_RUNTIME, std::string("ormi_hip_gemm launch: ") + hipGetErrorString(e));
     return ORMI_HIP_OK;

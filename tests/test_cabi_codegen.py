@@ -65,6 +65,36 @@ def test_gemm_descriptor_validation(cabi):
     assert cabi.ormi_hip_gemm(ctypes.byref(d)) == ORMI_HIP_OK
 
 
+class GemmEpilogue(ctypes.Structure):
+    _fields_ = [("kind", ctypes.c_int), ("fn", ctypes.c_int), ("form", ctypes.c_int), ("s", ctypes.c_void_p),
+                ("d", ctypes.c_void_p), ("d_stride_m", ctypes.c_int64), ("d_stride_n", ctypes.c_int64),
+                ("d_batch_stride", ctypes.c_int64 * 4), ("aux", ctypes.c_void_p)]
+
+
+def test_gemm_epilogue_validation(cabi):
+    """Malformed epilogues are rejected before any device work (the operand
+    pointers are never dereferenced)."""
+    base = 1 << 40  # fake, 16-byte aligned device addresses
+    d = GemmDesc(dtype=0, M=8, N=8, K=8, a=base, a_stride_m=8, a_stride_k=1, b=base + 4096, b_stride_k=8,
+                 b_stride_n=1, c=base + 8192)
+
+    def rc(**kw):
+        return cabi.ormi_hip_gemm_ex(ctypes.byref(d), ctypes.byref(GemmEpilogue(**kw)))
+
+    assert rc(kind=9) == ORMI_HIP_ERR_INVALID and b"kind" in cabi.ormi_hip_last_error()
+    assert rc(kind=2, fn=42) == ORMI_HIP_ERR_INVALID and b"function" in cabi.ormi_hip_last_error()
+    assert rc(kind=1, form=3, d=base + 12288, d_stride_m=8, d_stride_n=1) == ORMI_HIP_ERR_INVALID
+    assert rc(kind=1) == ORMI_HIP_ERR_INVALID and b"needs D" in cabi.ormi_hip_last_error()
+    assert rc(kind=3, d=base + 12289, d_stride_m=8, d_stride_n=1) == ORMI_HIP_ERR_INVALID
+    assert b"aligned" in cabi.ormi_hip_last_error()
+    assert rc(kind=2, fn=7, aux=base + 8192 + 64) == ORMI_HIP_ERR_INVALID and b"aux" in cabi.ormi_hip_last_error()
+    # D inside C with another layout (transposed) would race; C's own layout is fine.
+    assert rc(kind=1, form=1, d=base + 8192, d_stride_m=1, d_stride_n=8) == ORMI_HIP_ERR_INVALID
+    assert b"overlaps" in cabi.ormi_hip_last_error()
+    empty = GemmDesc(dtype=0, M=0, N=8, K=8)
+    assert cabi.ormi_hip_gemm_ex(ctypes.byref(empty), ctypes.byref(GemmEpilogue(kind=2, fn=7))) == ORMI_HIP_OK
+
+
 def _compile_only(cabi, src: str, opts):
     arr = (ctypes.c_char_p * len(opts))(*[o.encode() for o in opts])
     size = ctypes.c_size_t(0)
