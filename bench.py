@@ -17,8 +17,10 @@ from __future__ import annotations
 
 import argparse
 import collections
+import contextlib
 import csv
 import ctypes
+import gc
 import json
 import math
 import os
@@ -68,6 +70,19 @@ class Events:
         assert self.lib.ormi_hip_synchronize() == 0
 
 
+@contextlib.contextmanager
+def gc_paused():
+    """Timed GPU loops run with Python's cyclic collector off, as timeit runs its
+    loops: a collection pause otherwise lands on whichever step it hits."""
+    was = gc.isenabled()
+    gc.disable()
+    try:
+        yield
+    finally:
+        if was:
+            gc.enable()
+
+
 def timed_launches(ev: Events, make, n: int) -> float:
     """Average ms per iteration over n back-to-back realizations of pre-built
     graphs (make(i) returns a Tensor or a list of Tensors to realize). A first
@@ -86,11 +101,12 @@ def timed_launches(ev: Events, make, n: int) -> float:
     graphs = [as_list(make(i)) for i in range(n)]
     ev.sync()
     a, b = ev.new(), ev.new()
-    ev.record(a)
-    for gs in graphs:
-        for g in gs:
-            g.realize()
-    ev.record(b)
+    with gc_paused():
+        ev.record(a)
+        for gs in graphs:
+            for g in gs:
+                g.realize()
+        ev.record(b)
     return ev.elapsed_ms(a, b) / n
 
 
@@ -254,11 +270,12 @@ def bench_c2(args, ev: Events) -> dict:
         ring.append(c2_graph(*sets[i % 3]).realize())
     ev.sync()
     log("C2: timed steps")
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        ring.append(c2_graph(*sets[i % 3]).realize())
-    ev.sync()
-    step_s = (time.perf_counter() - t0) / args.steps
+    with gc_paused():
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            ring.append(c2_graph(*sets[i % 3]).realize())
+        ev.sync()
+        step_s = (time.perf_counter() - t0) / args.steps
     ring.clear()
     log("C2: kernel timing (HIP events)")
     n = max(args.steps, 20)
@@ -335,11 +352,12 @@ def bench_c1(ev: Events, n: int) -> dict:
     ms_b = timed_launches(ev, grads, n)
     ms_g = timed_launches(ev, lambda i: realize_group(grads(i)), n)
     ev.sync()
-    t0 = time.perf_counter()
-    for i in range(n):
-        realize_all(*grads(i))
-    ev.sync()
-    step_ms = (time.perf_counter() - t0) / n * 1e3
+    with gc_paused():
+        t0 = time.perf_counter()
+        for i in range(n):
+            realize_all(*grads(i))
+        ev.sync()
+        step_ms = (time.perf_counter() - t0) / n * 1e3
     fb, bb, gb = 12587008, 50331648, 25165824
     return {"fwd_us": round(ms_f * 1e3, 2), "fwd_GB/s": round(fb / ms_f / 1e6, 1),
             "bwd_separate_us": round(ms_b * 1e3, 2), "bwd_separate_GB/s": round(bb / ms_b / 1e6, 1),
@@ -432,13 +450,14 @@ def bench_c5(ev: Events, steps: int) -> dict:
     _, ws = step(ws)  # second untimed step: the pool now holds a step's blocks
     ev.sync()
     e0, e1 = ev.new(), ev.new()
-    ev.record(e0)
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        loss, ws = step(ws)
-    ev.record(e1)
-    ms = ev.elapsed_ms(e0, e1) / steps
-    wall = (time.perf_counter() - t0) / steps
+    with gc_paused():
+        ev.record(e0)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            loss, ws = step(ws)
+        ev.record(e1)
+        ms = ev.elapsed_ms(e0, e1) / steps
+        wall = (time.perf_counter() - t0) / steps
     last = float(loss.numpy())
     flops = 146028888064
     return {"step_ms": round(ms, 3), "wall_ms": round(wall * 1e3, 3), "gemm_TFLOP/s": round(flops / ms / 1e9, 1),
@@ -551,7 +570,17 @@ def main():
                     help="summarize rocprofv3 --pmc runs into a traffic table (no GPU needed)")
     ap.add_argument("--mfma-report", nargs=2, metavar=("PMC_DIR", "OUT_MD"),
                     help="summarize a rocprofv3 --pmc run of --only c4 into MFMA utilisation (no GPU needed)")
+    ap.add_argument("--ceilings", action="store_true",
+                    help="run the matrix-core ceiling probe (ormi_amd/lib/mfma_ceiling) and print its JSON lines")
     args = ap.parse_args()
+    if args.ceilings:
+        # A child process, started before this process touches the GPU.
+        import subprocess
+
+        probe = ROOT / "ormi_amd" / "lib" / "mfma_ceiling"
+        if not probe.exists():
+            raise SystemExit(f"bench.py: {probe} is not built (run __graft_entry__.build())")
+        sys.exit(subprocess.run([str(probe)]).returncode)
     if args.mfma_report:
         mfma_report(Path(args.mfma_report[0]), Path(args.mfma_report[1]),
                     "rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_MFMA SQ_LDS_BANK_CONFLICT GRBM_GUI_ACTIVE "

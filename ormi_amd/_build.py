@@ -53,6 +53,9 @@ ORACLE_SOURCES = sorted((ORACLE / "cpu_backend").glob("*.cpp"))
 EXT_SUFFIX = sysconfig.get_config_var("EXT_SUFFIX") or ".so"
 MODULE_PATH = PKG / f"ormi_backend{EXT_SUFFIX}"
 HIP_LIB = LIBDIR / "libormi_hip.so"
+# Matrix-core ceiling probe for the roofline (python3 bench.py --ceilings).
+CEILING_SRC = CSRC / "bench" / "mfma_ceiling.hip"
+CEILING_BIN = LIBDIR / "mfma_ceiling"
 CORE_LIB = LIBDIR / "libormi_core.so"
 ORACLE_LIB = ORACLE_OUT / "libormi_cpu_oracle.so"
 
@@ -109,10 +112,12 @@ def build(verbose: bool = False) -> None:
         # One object per HIP translation unit, compiled in parallel (the GEMM
         # units take the longest), then linked into the shared library.
         hip_objs = [ex.submit(_compile_hip, s) for s in HIP_SOURCES]
+        ceiling = ex.submit(_run, [HIPCC, *HIP_FLAGS, str(CEILING_SRC), "-o", str(CEILING_BIN)])
         core_objs = [ex.submit(_compile_cxx, s, core_inc) for s in CORE_SOURCES]
         bind_objs = [ex.submit(_compile_cxx, s, core_inc + py_inc) for s in BINDING_SOURCES]
         oracle_objs = [ex.submit(_compile_cxx, s, core_inc) for s in ORACLE_SOURCES]
         hip = [f.result() for f in hip_objs]
+        ceiling.result()
         core = [f.result() for f in core_objs]
         binds = [f.result() for f in bind_objs]
         oracle = [f.result() for f in oracle_objs]
