@@ -65,6 +65,7 @@ namespace ormi::hip {
             x.map_nt_loads = env_int("ORMI_MAP_NT_LOADS", x.map_nt_loads) != 0;
             x.reduce_nt_loads = env_int("ORMI_REDUCE_NT_LOADS", x.reduce_nt_loads) != 0;
             x.map_nt_stores = env_int("ORMI_MAP_NT_STORES", x.map_nt_stores) != 0;
+            x.map_off32 = env_int("ORMI_MAP_OFF32", x.map_off32) != 0;
             return x;
         }();
         return t;
@@ -215,6 +216,13 @@ namespace ormi::hip {
             Canon c;
             std::vector<bool> scalar;
             bool idx32 = true;
+            // off32 (map kernels that ask for it, idx32 only): every operand and
+            // output byte offset fits in 32 bits. Indices are unsigned and each
+            // access is base pointer + 32-bit byte offset, which the compiler
+            // emits as a load or store with a uniform (SGPR) base and a 32-bit
+            // VGPR offset, with no 64-bit address arithmetic per element.
+            bool want_off32 = false;
+            bool off32 = false;
             int vec = 1;
             int vec_dim = -1;  // dim whose coordinate advances by VEC
             bool nt_loads = false;
@@ -230,7 +238,16 @@ namespace ormi::hip {
                 for (const auto& L : e.leaves) scalar.push_back(L.scalar);
             }
 
-            std::string idx() const { return idx32 ? "int" : "long long"; }
+            std::string idx() const { return off32 ? "unsigned" : idx32 ? "int" : "long long"; }
+
+            // Pointer expression for element `off` of pointer `base` of type T
+            // (sizeof `bytes`), cast to `ptr_type`.
+            std::string elem_ptr(const std::string& ptr_type, const std::string& base, const std::string& off, int bytes,
+                                 bool is_const) const {
+                if (!off32) return "(" + ptr_type + ")(" + base + " + (" + off + "))";
+                return "(" + ptr_type + ")((" + (is_const ? "const char*" : "char*") + ")" + base + " + (unsigned)(" + off +
+                       ") * " + std::to_string(bytes) + "u)";
+            }
 
             // Leaf L has a unit stride on the vector dim and can be read 4-wide.
             bool leaf_vec_ok(size_t L, int d) const {
@@ -254,17 +271,26 @@ namespace ormi::hip {
 
             // 32-bit index arithmetic when every index the kernel forms (element
             // counts, operand offsets, the cursor bound extra_extent) fits.
-            void choose_idx(long long extra_extent) {
+            // out_bytes: largest output element size (for off32).
+            void choose_idx(long long extra_extent, int out_bytes = 4) {
                 const long long lim = (1ll << 31) - 1;
+                const long long blim = (1ll << 32) - 1;
                 long long numel = 1;
                 for (auto& d : c.dims) numel *= d.size;
                 idx32 = numel < lim && extra_extent < lim;
+                off32 = want_off32 && idx32 && (numel + 4) * out_bytes < blim;
                 for (size_t L = 0; L < e.leaves.size() && idx32; ++L) {
                     if (scalar[L]) continue;
                     long long span = 0;
-                    for (size_t d = 0; d < c.dims.size(); ++d) span += (c.dims[d].size - 1) * std::llabs(c.st[L][d]);
+                    bool nonneg = true;
+                    for (size_t d = 0; d < c.dims.size(); ++d) {
+                        span += (c.dims[d].size - 1) * std::llabs(c.st[L][d]);
+                        nonneg = nonneg && c.st[L][d] >= 0;
+                    }
                     if (span >= lim) idx32 = false;
+                    if (!nonneg || (span + 4) * dtype_size(e.leaves[L].dtype) >= blim) off32 = false;
                 }
+                off32 = off32 && idx32;
             }
 
             void declare_leaves() {
@@ -312,8 +338,8 @@ namespace ormi::hip {
                 for (size_t k = dims.size() - 1; k >= 1; --k) {
                     const std::string d = std::to_string(dims[k]);
                     if (idx32)
-                        o << ind << "  { const int q_ = (int)ormi_fdiv((unsigned)rem_, (unsigned)M" << d << ", (unsigned)(M" << d
-                          << " >> 32));";
+                        o << ind << "  { const " << t << " q_ = (" << t << ")ormi_fdiv((unsigned)rem_, (unsigned)M" << d
+                          << ", (unsigned)(M" << d << " >> 32));";
                     else
                         o << ind << "  { const long long q_ = rem_ / D" << d << ";";
                     o << " c" << d << " = rem_ - q_ * (" << t << ")D" << d << "; rem_ = q_; }\n";
@@ -347,7 +373,7 @@ namespace ormi::hip {
                 const bool nt = nt_loads;
                 if (unit) {
                     const char* vt = dt == DType::Float32 ? "ormi_f4" : "ormi_u16x4";
-                    const std::string addr = std::string("(const ") + vt + "*)(" + p + " + (" + off + "))";
+                    const std::string addr = elem_ptr(std::string("const ") + vt + "*", p, off, dtype_size(dt), true);
                     o << ind << "{ const " << vt << " v_ = " << (nt ? "__builtin_nontemporal_load(" + addr + ")" : "*" + addr) << ";";
                     for (int k = 0; k < vec; ++k) {
                         const std::string ek = "v_[" + std::to_string(k) + "]";
@@ -355,7 +381,10 @@ namespace ormi::hip {
                     }
                     o << " }\n";
                 } else {
-                    o << ind << "{ const float v_ = " << to_f32(dt, p + "[" + off + "]") << ";";
+                    const std::string elem = off32 ? "*" + elem_ptr(std::string("const ") + storage_type(dt) + "*", p, off,
+                                                                    dtype_size(dt), true)
+                                                   : p + "[" + off + "]";
+                    o << ind << "{ const float v_ = " << to_f32(dt, elem) << ";";
                     for (int k = 0; k < vec; ++k) o << " " << dst << "[" << k << "] = v_;";
                     o << " }\n";
                 }
@@ -470,7 +499,7 @@ namespace ormi::hip {
             append_int(s, g.vec);
             s += ',';
             append_int(s, g.vec_dim);
-            s += g.idx32 ? ",32|" : ",64|";
+            s += g.off32 ? ",32u|" : g.idx32 ? ",32|" : ",64|";
             for (size_t L = 0; L < g.e.leaves.size(); ++L) {
                 if (g.scalar[L]) {
                     s += 'S';
@@ -575,6 +604,7 @@ namespace ormi::hip {
         const int block = 256, unroll = tn.map_unroll;
         Gen g(expr);
         g.nt_loads = tn.map_nt_loads;
+        g.want_off32 = tn.map_off32;
         for (int s : shape) g.c.dims.push_back({(long long)s, G_M});
         for (const auto& L : expr.leaves) g.c.st.push_back(L.st);
         canonicalize(g.c, g.scalar);
@@ -593,7 +623,9 @@ namespace ormi::hip {
         const long long tiles = (G + tile - 1) / tile;
         const long long grid = std::max(1LL, std::min(tiles, (long long)std::max(cu, 1) * tn.map_blocks_per_cu));
         // The grid-stride cursor reaches G + grid * tile before the loop exits.
-        g.choose_idx(G + grid * tile);
+        int out_bytes = 1;
+        for (DType dt : out_dtypes) out_bytes = std::max(out_bytes, (int)dtype_size(dt));
+        g.choose_idx(G + grid * tile, out_bytes);
 
         // A single output keeps the name "out"; several are out0, out1, ...
         auto out_name = [&](size_t r) { return nout == 1 ? std::string("out") : "out" + std::to_string(r); };
@@ -609,6 +641,7 @@ namespace ormi::hip {
         k.plan.add("ndim", n);
         k.plan.add("vec", g.vec);
         k.plan.add("idx", g.idx32 ? 32 : 64);
+        k.plan.add("off32", g.off32 ? 1 : 0);
         k.plan.add("groups", G);
         k.plan.add("unroll", unroll);
         if (nout > 1) k.plan.add("outputs", (long long)nout);
@@ -651,11 +684,12 @@ namespace ormi::hip {
                     std::string val = std::string(vt) + "{";
                     for (int q = 0; q < 4; ++q) val += (q ? ", " : "") + from_f32(odt, res(r) + "[" + std::to_string(q) + "]");
                     val += "}";
-                    const std::string addr = std::string("(") + vt + "*)(" + out_name(r) + " + gi[u] * 4)";
+                    const std::string addr = g.elem_ptr(std::string(vt) + "*", out_name(r), "gi[u] * 4", dtype_size(odt), false);
                     if (nt) b << "        __builtin_nontemporal_store(" << val << ", " << addr << ");\n";
                     else b << "        *" << addr << " = " << val << ";\n";
                 } else {
-                    b << "        " << out_name(r) << "[gi[u]] = " << from_f32(odt, res(r) + "[0]") << ";\n";
+                    b << "        *" << g.elem_ptr(std::string(storage_type(odt)) + "*", out_name(r), "gi[u]", dtype_size(odt), false)
+                      << " = " << from_f32(odt, res(r) + "[0]") << ";\n";
                 }
             }
             b << "      }\n    }\n  }\n";

@@ -122,6 +122,7 @@ namespace ormi::hip {
         bool map_nt_loads = false;    // non-temporal hint on a map's operand loads
         bool map_nt_stores = false;   // non-temporal hint on a map's output stores
         bool reduce_nt_loads = true;  // non-temporal hint on a reduction's loads
+        bool map_off32 = true;        // 32-bit byte offsets from uniform bases when they fit (map)
     };
     const Tuning& tuning();
 
