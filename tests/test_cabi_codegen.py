@@ -257,3 +257,17 @@ def test_generated_kernels_compile_for_nd_index_spaces(ob, cpu, cabi, kind):
     if d["two_pass"]:
         rc, _ = _compile_only(cabi, d["second_source"], ob._rtc_options())
         assert rc == ORMI_HIP_OK, cabi.ormi_hip_last_error()
+
+
+def test_map_and_reduce_plans_past_2_31_use_64_bit_indices(ob, cpu):
+    """A broadcast map over 65537 x 32768 elements (> 2^31; the operands are a
+    row and a column, so nothing large is allocated) plans 64-bit indices and
+    no 32-bit byte offsets; a small one plans 32-bit offsets."""
+    from ormi_amd import Tensor
+
+    a = Tensor(np.zeros(32768, np.float32), "cpu")
+    b = Tensor(np.zeros((65537, 1), np.float32), "cpu")
+    plan = ob._plan_kernel((b + a)._node)["plan"]
+    assert "idx=64" in plan and "off32=0" in plan
+    small = ob._plan_kernel((Tensor(np.zeros((4, 1), np.float32), "cpu") + a)._node)["plan"]
+    assert "idx=32" in small and "off32=1" in small
