@@ -92,11 +92,20 @@ def timed_launches(ev: Events, make, n: int) -> float:
     def as_list(g):
         return g if isinstance(g, (list, tuple)) else [g]
 
+    def release(sets):
+        # Autograd graphs hold reference cycles until zero_grad_graph (the
+        # reference's contract); objects that own one release it here.
+        for gs in sets:
+            for g in gs:
+                if hasattr(g, "release"):
+                    g.release()
+
     warm = [as_list(make(i)) for i in range(n)]
     for gs in warm:
         for g in gs:
             g.realize()
     ev.sync()
+    release(warm)
     del warm
     graphs = [as_list(make(i)) for i in range(n)]
     ev.sync()
@@ -107,7 +116,9 @@ def timed_launches(ev: Events, make, n: int) -> float:
             for g in gs:
                 g.realize()
         ev.record(b)
-    return ev.elapsed_ms(a, b) / n
+    ms = ev.elapsed_ms(a, b) / n
+    release(graphs)
+    return ms
 
 
 # ------------------------------------------------------------------ workloads
@@ -345,17 +356,20 @@ def bench_c1(ev: Events, n: int) -> dict:
     def grads(i):
         for t in (A, B, C):
             t.zero_grad()
-        fwd(i).sum().backward()
-        return [A.grad, B.grad, C.grad]
+        loss = fwd(i).sum()
+        loss.backward()
+        return loss, [A.grad, B.grad, C.grad]
 
     ms_f = timed_launches(ev, fwd, n)
-    ms_b = timed_launches(ev, grads, n)
-    ms_g = timed_launches(ev, lambda i: realize_group(grads(i)), n)
+    ms_b = timed_launches(ev, lambda i: _Grads(*grads(i), grouped=False), n)
+    ms_g = timed_launches(ev, lambda i: _Grads(*grads(i), grouped=True), n)
     ev.sync()
     with gc_paused():
         t0 = time.perf_counter()
         for i in range(n):
-            realize_all(*grads(i))
+            loss, gs = grads(i)
+            realize_all(*gs)
+            loss.zero_grad_graph()  # a training step releases its graph (reference contract)
         ev.sync()
         step_ms = (time.perf_counter() - t0) / n * 1e3
     fb, bb, gb = 12587008, 50331648, 25165824
@@ -365,23 +379,30 @@ def bench_c1(ev: Events, n: int) -> dict:
             "bwd_step_wall_us": round(step_ms * 1e3, 1),
             "note": "fwd: one fused reduce kernel (12,587,008 B); bwd_separate: one fused kernel per gradient root "
                     "(3 x 16,777,216 B); bwd_grouped: realize_all, one multi-output kernel (25,165,824 B); "
-                    "bwd_step_wall_us: host-inclusive loop (graph build + backward + realize_all)"}
+                    "bwd_step_wall_us: host-inclusive loop (graph build + backward + realize_all + zero_grad_graph)"}
 
 
-class _Group:
-    """Adapter so timed_launches can realize a list of tensors with realize_all."""
+class _Grads:
+    """One backward graph for timed_launches: realize() realizes its gradients
+    (one multi-output kernel with realize_all when grouped, else one kernel per
+    gradient); release() clears the graph's stored gradients
+    (zero_grad_graph), which autograd's reference cycles otherwise keep alive
+    with every buffer they hold."""
 
-    def __init__(self, tensors):
-        self.tensors = tensors
+    def __init__(self, loss, tensors, grouped):
+        self.loss, self.tensors, self.grouped = loss, tensors, grouped
 
     def realize(self):
         from ormi_amd import realize_all
 
-        realize_all(*self.tensors)
+        if self.grouped:
+            realize_all(*self.tensors)
+        else:
+            for t in self.tensors:
+                t.realize()
 
-
-def realize_group(tensors):
-    return _Group(tensors)
+    def release(self):
+        self.loss.zero_grad_graph()
 
 
 def bench_c4(ev: Events, n: int) -> dict:

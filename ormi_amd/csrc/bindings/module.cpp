@@ -280,6 +280,10 @@ PYBIND11_MODULE(ormi_backend, m) {
         .def_readwrite("data", &Node::data)
         .def_readwrite("grad", &Node::grad);
 
+    // Internal fast paths for ormi_amd.Tensor's operators: two node arguments
+    // instead of a list, the device taken from the first operand.
+    m.def("_binary", &ops::binary);
+    m.def("_unary", &ops::unary);
     m.def("add", &ops::add);
     m.def("sub", &ops::sub);
     m.def("mul", &ops::mul);

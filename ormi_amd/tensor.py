@@ -8,6 +8,8 @@ max, argmax, astype).
 """
 from __future__ import annotations
 
+import math
+
 import numpy as np
 from numpy.lib.stride_tricks import as_strided
 
@@ -22,18 +24,36 @@ Node = ormi_backend.Node
 _DEVICE_STRINGS = {"cpu": DeviceEnum.CPU, "cuda": DeviceEnum.CUDA, "hip": DeviceEnum.HIP}
 
 
+# One canonical Device object per (type, id), kept for the process: tensors on
+# the same device share it, so device checks and the scalar-leaf cache can
+# compare identities. _CANONICAL_IDS holds only these never-freed objects.
+_CANONICAL: dict = {}
+_CANONICAL_IDS: dict = {}
+
+
+def _canonical(device: Device) -> Device:
+    if id(device) in _CANONICAL_IDS:
+        return device
+    key = (int(device.type), device.id)
+    canon = _CANONICAL.get(key)
+    if canon is None:
+        canon = _CANONICAL[key] = device
+        _CANONICAL_IDS[id(device)] = device
+    return canon
+
+
 def _parse_device(device) -> Device:
     if device is None:
-        return Device(DeviceEnum.CPU, 0)
+        return _canonical(Device(DeviceEnum.CPU, 0))
     if isinstance(device, str):
         name, _, idx = device.lower().partition(":")
         if name not in _DEVICE_STRINGS:
             raise_device_mismatch(msg="Unsupported string backend", got=device)
-        return Device(_DEVICE_STRINGS[name], int(idx) if idx else 0)
+        return _canonical(Device(_DEVICE_STRINGS[name], int(idx) if idx else 0))
     if isinstance(device, DeviceEnum):
-        return Device(device, 0)
+        return _canonical(Device(device, 0))
     if isinstance(device, Device):
-        return device
+        return _canonical(device)
     raise_device_mismatch(msg="Device argument is of invalid type.", got=type(device))
 
 
@@ -45,7 +65,9 @@ def _scalar_leaf(value: float, device: Device) -> Node:
     (reference tensor.py:80-85), but created once per (device, value): leaves are
     never written after creation, so sharing them is invisible to results and
     saves a host-to-device copy on every operation with a literal."""
-    key = (int(device.type), device.id, np.float32(value).tobytes())
+    # device is canonical (one object per device, hashed by identity);
+    # -0.0 == 0.0 as a float, so a zero's key carries its sign.
+    key = (device, value) if value != 0.0 else (device, value, math.copysign(1.0, value))
     node = _SCALAR_LEAVES.get(key)
     if node is None:
         if len(_SCALAR_LEAVES) >= 4096:
@@ -70,6 +92,15 @@ class Tensor:
         else:
             self._node = None
 
+    @classmethod
+    def _wrap(cls, node: Node, device: Device) -> "Tensor":
+        """A Tensor over an existing node with an already-parsed device (the
+        constructor's work minus argument parsing; every op result uses it)."""
+        t = cls.__new__(cls)
+        t.device = device
+        t._node = node
+        return t
+
     # ------------------------------------------------------------ properties
     @property
     def op(self):
@@ -90,24 +121,24 @@ class Tensor:
     @property
     def grad(self):
         if self._node and self._node.grad:
-            return Tensor(_node=self._node.grad, device=self.device)
+            return Tensor._wrap(self._node.grad, self.device)
         return None
 
     # ------------------------------------------------------------- operators
     def _ensure_tensor(self, other) -> "Tensor":
         if isinstance(other, Tensor):
-            if self.device.type != other.device.type:
+            if other.device is not self.device and self.device.type != other.device.type:
                 raise_device_mismatch(msg="Cannot mix devices in operation.", got=other.device.type)
             return other
         if isinstance(other, (int, float)) and not isinstance(other, bool):
-            return Tensor(_node=_scalar_leaf(float(other), self.device), device=self.device)
+            return Tensor._wrap(_scalar_leaf(float(other), self.device), self.device)
         return Tensor(data=other, device=self.device)
 
     def _binary(self, op, a: "Tensor", b: "Tensor") -> "Tensor":
-        return Tensor(_node=Node(op, [a._node, b._node], self.device), device=self.device)
+        return Tensor._wrap(ormi_backend._binary(op, a._node, b._node), self.device)
 
     def _unary(self, op) -> "Tensor":
-        return Tensor(_node=Node(op, [self._node], self.device), device=self.device)
+        return Tensor._wrap(ormi_backend._unary(op, self._node), self.device)
 
     def __add__(self, other):
         return self._binary(OpEnum.ADD, self, self._ensure_tensor(other))
@@ -127,7 +158,7 @@ class Tensor:
     def __matmul__(self, other):
         if not isinstance(other, Tensor):
             raise TypeError("Matmul requires both operands to be Tensors.")
-        if self.device.type != other.device.type:
+        if other.device is not self.device and self.device.type != other.device.type:
             raise_device_mismatch(msg="Cannot perform MATMUL across different devices", got=other.device.type)
         return self._binary(OpEnum.MATMUL, self, other)
 
@@ -172,7 +203,7 @@ class Tensor:
         return self._unary(OpEnum.GELU)
 
     def astype(self, dtype: str) -> "Tensor":
-        return Tensor(_node=ormi_backend.cast(self._node, dtype), device=self.device)
+        return Tensor._wrap(ormi_backend.cast(self._node, dtype), self.device)
 
     # ---------------------------------------------------- reductions (additive)
     @staticmethod
@@ -184,13 +215,13 @@ class Tensor:
         return list(axis)
 
     def sum(self, axis=None, keepdims: bool = False) -> "Tensor":
-        return Tensor(_node=ormi_backend.sum(self._node, self._axes(axis), keepdims), device=self.device)
+        return Tensor._wrap(ormi_backend.sum(self._node, self._axes(axis), keepdims), self.device)
 
     def max(self, axis=None, keepdims: bool = False) -> "Tensor":
-        return Tensor(_node=ormi_backend.max(self._node, self._axes(axis), keepdims), device=self.device)
+        return Tensor._wrap(ormi_backend.max(self._node, self._axes(axis), keepdims), self.device)
 
     def argmax(self, axis: int | None = None, keepdims: bool = False) -> "Tensor":
-        return Tensor(_node=ormi_backend.argmax(self._node, self._axes(axis), keepdims), device=self.device)
+        return Tensor._wrap(ormi_backend.argmax(self._node, self._axes(axis), keepdims), self.device)
 
     def mean(self, axis=None, keepdims: bool = False) -> "Tensor":
         """sum * (1/N), N = number of reduced elements (exact scaling for powers of two)."""
@@ -204,15 +235,15 @@ class Tensor:
 
     # ------------------------------------------------------------------ views
     def reshape(self, shape) -> "Tensor":
-        return Tensor(_node=ormi_backend.reshape(self._node, list(shape)), device=self.device)
+        return Tensor._wrap(ormi_backend.reshape(self._node, list(shape)), self.device)
 
     def transpose(self, axes=None) -> "Tensor":
         if axes is None:
             axes = tuple(reversed(range(len(self.shape))))
-        return Tensor(_node=ormi_backend.transpose(self._node, list(axes)), device=self.device)
+        return Tensor._wrap(ormi_backend.transpose(self._node, list(axes)), self.device)
 
     def expand(self, shape) -> "Tensor":
-        return Tensor(_node=ormi_backend.expand(self._node, list(shape)), device=self.device)
+        return Tensor._wrap(ormi_backend.expand(self._node, list(shape)), self.device)
 
     @property
     def T(self) -> "Tensor":

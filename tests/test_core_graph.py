@@ -186,3 +186,4 @@ def test_deep_graph_no_recursion_limit(ob, cpu):
 def test_unknown_device_errors(ob):
     with pytest.raises(RuntimeError, match="no CUDA backend"):
         ob.numpy_to_buffer(np.zeros(2, np.float32), ob.DeviceEnum.CUDA)
+

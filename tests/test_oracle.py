@@ -274,3 +274,17 @@ def test_golden_kats_on_oracle(ob, cpu, name):
 
     case = next(c for c in cases() if c["name"] == name)
     run_case(ob, case, ob.DeviceEnum.CPU)
+
+
+def test_python_scalar_operands_share_leaves_but_keep_signed_zero(cpu):
+    """Python scalars become cached 0-d leaves per (device, value) (a host-to-device
+    copy saved per literal); -0.0 and 0.0 compare equal as floats but must stay
+    distinct leaves."""
+    from ormi_amd import Tensor
+
+    x = Tensor(np.array([1.0, -2.0], np.float32), "cpu")
+    assert (x * 0.5)._node.parents[1] is (x * 0.5)._node.parents[1]
+    assert list(np.signbit((x * 0.0).numpy())) == [False, True]
+    assert list(np.signbit((x * -0.0).numpy())) == [True, False]
+    a, b = Tensor(np.ones(2, np.float32), "cpu"), Tensor(np.ones(2, np.float32), "cpu")
+    assert (a + b).numpy().tolist() == [2.0, 2.0]  # tensors with separate Device objects
