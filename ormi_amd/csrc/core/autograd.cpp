@@ -1,6 +1,8 @@
+#include <map>
+#include <mutex>
+#include <stdexcept>
 #include <unordered_set>
 #include <vector>
-#include <stdexcept>
 #include "core/autograd.h"
 #include "core/registry.h"
 #include "core/memory.h"
@@ -32,12 +34,27 @@ namespace ormi {
         return topo;
     }
 
+    // The seed of a one-element root (a loss): one read-only buffer of 1.0 per
+    // (device, shape), shared by every backward instead of a fresh allocation
+    // and fill launch each time, as Python-scalar leaves are shared. Never
+    // freed (device memory outlives static destructors otherwise).
+    static std::shared_ptr<Buffer> scalar_seed(const std::vector<int>& shape, DeviceEnum dev) {
+        static std::mutex mu;
+        static auto* cache = new std::map<std::pair<int, std::vector<int>>, std::shared_ptr<Buffer>>();
+        std::lock_guard<std::mutex> lock(mu);
+        auto& b = (*cache)[{(int)dev, shape}];
+        if (!b) b = ones(shape, dev);
+        return b;
+    }
+
     // Reverse-mode pass that only builds lazy gradient nodes
     // (reference: csrc/core/autograd.cpp:24-47).
     void compute_gradients(std::shared_ptr<Node> root) {
         auto topo = topo_order(root);
         if (!root->grad) {
-            auto seed = ones(root->view.shape, root->device.type);
+            long long n = 1;
+            for (int d : root->view.shape) n *= d;
+            auto seed = n == 1 ? scalar_seed(root->view.shape, root->device.type) : ones(root->view.shape, root->device.type);
             root->grad = std::make_shared<Node>(seed, false, root->device);
         }
         for (auto it = topo.rbegin(); it != topo.rend(); ++it) {
