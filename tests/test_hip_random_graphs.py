@@ -140,3 +140,74 @@ def test_random_matmul_matches_oracle(cpu, hip, seed):
         bb = np.swapaxes(bb, -1, -2)
     bound = (k + 2) * np.finfo(np.float32).eps * (aa @ bb)
     assert np.all(np.abs(got.astype(np.float64) - want) <= bound + 1e-6), (m, k, n, batch, ta, tb, dtype)
+
+
+ACTS = ["none", "relu", "tanh", "sigmoid", "gelu"]
+
+
+def _net(dev, spec):
+    """Random small network: forward, backward, SGD updates realized in a random
+    order, then the weight gradients read afterwards (a gradient GEMM fused
+    into an update is computed again here)."""
+    from ormi_amd import Tensor
+
+    X, Y = Tensor(spec["X"], dev), Tensor(spec["Y"], dev)
+    Ws = [Tensor(w, dev, requires_grad=True) for w in spec["W"]]
+    bs = [None if b is None else Tensor(b, dev, requires_grad=True) for b in spec["b"]]
+    h = X
+    for W, b, act in zip(Ws, bs, spec["act"]):
+        h = h @ W
+        if b is not None:
+            h = h + b
+        if act != "none":
+            h = getattr(h, act)()
+    if spec["loss"] == "mse":
+        d = h - Y
+        loss = (d * d).sum() * (1.0 / spec["X"].shape[0])
+    else:
+        loss = (h * Y).sum() * 0.5
+    loss.backward()
+    params = Ws + [b for b in bs if b is not None]
+    updates = [p - p.grad * spec["lr"] for p in params]
+    got = {}
+    for i in spec["order"][: len(updates)]:
+        got[i] = updates[i].numpy()
+    out = [loss.numpy()] + [got[i] for i in range(len(updates))] + [W.grad.numpy() for W in Ws]
+    loss.zero_grad_graph()
+    return out
+
+
+def _net_spec(seed):
+    rng = np.random.default_rng(5000 + seed)
+    L = int(rng.integers(1, 4))
+    dims = [int(rng.choice([16, 32, 64, 96, 128, 256])) for _ in range(L + 1)]
+    n = int(rng.choice([8, 33, 64, 128, 256]))
+    spec = {"X": rng.standard_normal((n, dims[0])).astype(np.float32),
+            "Y": rng.standard_normal((n, dims[-1])).astype(np.float32),
+            "W": [(rng.standard_normal((i, o)) / np.sqrt(i)).astype(np.float32) for i, o in zip(dims, dims[1:])],
+            "b": [rng.standard_normal(o).astype(np.float32) * 0.1 if rng.random() < 0.4 else None for o in dims[1:]],
+            "act": [str(rng.choice(ACTS)) for _ in range(L)],
+            "loss": "mse" if rng.random() < 0.6 else "dot",
+            "lr": float(rng.choice([1e-3, 0.01, 0.1]))}
+    nparams = L + sum(b is not None for b in spec["b"])
+    spec["order"] = [int(v) for v in rng.permutation(nparams)]
+    return spec
+
+
+@pytest.mark.parametrize("seed", range(30))
+def test_random_network_step_fused_unfused_and_oracle(ob, cpu, hip, seed):
+    spec = _net_spec(seed)
+    ob.set_gemm_epilogue(True)
+    fused = _net(hip, spec)
+    ob.set_gemm_epilogue(False)
+    try:
+        plain = _net(hip, spec)
+    finally:
+        ob.set_gemm_epilogue(True)
+    for f, p in zip(fused, plain):
+        assert np.array_equal(np.atleast_1d(f).view(np.uint8), np.atleast_1d(p).view(np.uint8)), (spec["act"], spec["loss"])
+    want = _net(cpu, spec)
+    for f, w in zip(fused, want):
+        f, w = np.asarray(f, np.float64), np.asarray(w, np.float64)
+        scale = max(1.0, float(np.max(np.abs(w))))
+        np.testing.assert_allclose(f, w, rtol=2e-4, atol=2e-5 * scale, err_msg=str((spec["act"], spec["loss"])))
