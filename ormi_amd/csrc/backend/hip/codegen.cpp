@@ -66,6 +66,7 @@ namespace ormi::hip {
             x.reduce_nt_loads = env_int("ORMI_REDUCE_NT_LOADS", x.reduce_nt_loads) != 0;
             x.map_nt_stores = env_int("ORMI_MAP_NT_STORES", x.map_nt_stores) != 0;
             x.map_off32 = env_int("ORMI_MAP_OFF32", x.map_off32) != 0;
+            x.map_rows = env_int("ORMI_MAP_ROWS", x.map_rows) != 0;
             return x;
         }();
         return t;
@@ -225,6 +226,7 @@ namespace ormi::hip {
             bool off32 = false;
             int vec = 1;
             int vec_dim = -1;  // dim whose coordinate advances by VEC
+            int rows = 0;      // map tile alignment to the last dim (plan_map_multi)
             bool nt_loads = false;
             ArgList args;
             std::unique_ptr<std::ostringstream> body_;  // created when a source is generated
@@ -426,9 +428,13 @@ namespace ormi::hip {
                 return name[e.root];
             }
 
-            void declare_leaf_regs(std::ostringstream& o, const std::string& ind, int unroll) {
+            // Registers x<L>[unroll][vec] of every non-scalar leaf whose `pick` entry
+            // is true (all of them when pick is empty).
+            void declare_leaf_regs(std::ostringstream& o, const std::string& ind, int unroll,
+                                   const std::vector<bool>& pick = {}) {
                 for (size_t L = 0; L < e.leaves.size(); ++L)
-                    if (!scalar[L]) o << ind << "float x" << L << "[" << unroll << "][" << vec << "];\n";
+                    if (!scalar[L] && (pick.empty() || pick[L]))
+                        o << ind << "float x" << L << "[" << unroll << "][" << vec << "];\n";
             }
 
             std::string finish(const std::string& kind, int block, KernelLaunch& k) {
@@ -499,7 +505,9 @@ namespace ormi::hip {
             append_int(s, g.vec);
             s += ',';
             append_int(s, g.vec_dim);
-            s += g.off32 ? ",32u|" : g.idx32 ? ",32|" : ",64|";
+            s += g.off32 ? ",32u," : g.idx32 ? ",32," : ",64,";
+            append_int(s, g.rows);
+            s += '|';
             for (size_t L = 0; L < g.e.leaves.size(); ++L) {
                 if (g.scalar[L]) {
                     s += 'S';
@@ -627,6 +635,37 @@ namespace ormi::hip {
         for (DType dt : out_dtypes) out_bytes = std::max(out_bytes, (int)dtype_size(dt));
         g.choose_idx(G + grid * tile, out_bytes);
 
+        // Tiles aligned to the last dim, which holds Dl groups (32-bit indices,
+        // two or more dims):
+        //  rows 1: a tile covers P = tile / Dl > 1 whole rows. Each lane keeps its
+        //          last-dim coordinate and its row within the tile for the whole
+        //          loop: operands that vary only along the last dim are loaded once
+        //          before the loop, and an access's row is the tile's first row
+        //          plus that lane constant (no division per element);
+        //  rows 2: a tile lies inside one row (Dl a multiple of tile). The outer
+        //          coordinates are uniform per tile, so they and the loads of
+        //          operands that vary only across rows are scalar work, and every
+        //          tile is full, so stores need no bounds guard;
+        //  rows 3: a tile is exactly one row (tile == Dl): both of the above.
+        const int n_last = n - 1;
+        const long long Dl = g.c.dims[n_last].size / g.vec;
+        if (tn.map_rows && g.idx32 && n >= 2 && Dl > 0) {
+            if (tile == Dl) g.rows = 3;
+            else if (tile % Dl == 0) g.rows = 1;
+            else if (Dl % tile == 0) g.rows = 2;
+        }
+        const int rows = g.rows;
+        // Leaves loaded once before the loop (rows 1 and 3): zero stride on every outer dim.
+        std::vector<bool> hoist(expr.leaves.size(), false), in_loop(expr.leaves.size(), true);
+        if (rows == 1 || rows == 3)
+            for (size_t L = 0; L < expr.leaves.size(); ++L) {
+                if (g.scalar[L]) continue;
+                bool only_last = true;
+                for (int d = 0; d < n_last; ++d) only_last = only_last && g.c.st[L][d] == 0;
+                hoist[L] = only_last;
+                in_loop[L] = !only_last;
+            }
+
         // A single output keeps the name "out"; several are out0, out1, ...
         auto out_name = [&](size_t r) { return nout == 1 ? std::string("out") : "out" + std::to_string(r); };
         KernelLaunch k;
@@ -636,38 +675,106 @@ namespace ormi::hip {
         g.args.i64("G", G);
         g.declare_dims();
         g.declare_strides();
+        if (rows == 1) {
+            g.args.i64("R", G / Dl);
+            g.args.i64("P", tile / Dl);
+        }
         k.grid[0] = (uint32_t)grid;
         k.plan.kind = "map";
         k.plan.add("ndim", n);
         k.plan.add("vec", g.vec);
         k.plan.add("idx", g.idx32 ? 32 : 64);
         k.plan.add("off32", g.off32 ? 1 : 0);
+        k.plan.add("rows", rows);
         k.plan.add("groups", G);
         k.plan.add("unroll", unroll);
         if (nout > 1) k.plan.add("outputs", (long long)nout);
         resolve(g, "map", block, k, [&] {
-            std::vector<int> all;
+            std::vector<int> all, outer;
             for (int d = 0; d < n; ++d) all.push_back(d);
+            for (int d = 0; d < n_last; ++d) outer.push_back(d);
             const std::string t = g.idx();
+            const std::string tid = "(" + t + ")threadIdx.x";
+            const std::string lane = "u * " + std::to_string(block) + " + " + tid;  // group offset within the tile
+            const std::string cl = "c" + std::to_string(n_last);
+            const std::string Dn = "D" + std::to_string(n_last), Mn = "M" + std::to_string(n_last);
             const int V = g.vec;
             std::ostringstream& b = g.body();
+            auto load_all = [&](const std::string& ind, const std::vector<bool>& pick) {
+                for (size_t L = 0; L < expr.leaves.size(); ++L) {
+                    if (g.scalar[L] || !pick[L]) continue;
+                    std::string off = g.offset(L, all);
+                    g.load_leaf(b, ind, L, off.empty() ? "0" : off, "x" + std::to_string(L) + "[u]");
+                }
+            };
             g.hoist_scalars(b, "  ");
             b << "  const " << t << " tile = " << tile << ";\n";
-            b << "  for (" << t << " base = (" << t << ")blockIdx.x * tile; base < (" << t << ")G; base += (" << t << ")gridDim.x * tile) {\n";
-            g.declare_leaf_regs(b, "    ", unroll);
-            b << "    " << t << " gi[" << unroll << "];\n";
-            b << "#pragma unroll\n    for (int u = 0; u < " << unroll << "; ++u) {\n";
-            b << "      const " << t << " gg = base + u * " << block << " + (" << t << ")threadIdx.x;\n";
-            b << "      gi[u] = gg;\n";
-            b << "      const " << t << " gc = gg < (" << t << ")G ? gg : (" << t << ")G - 1;\n";
-            g.declare_coords(b, "      ", all);
-            g.decompose(b, "      ", "gc", all);
-            for (size_t L = 0; L < expr.leaves.size(); ++L) {
-                if (g.scalar[L]) continue;
-                std::string off = g.offset(L, all);
-                g.load_leaf(b, "      ", L, off.empty() ? "0" : off, "x" + std::to_string(L) + "[u]");
+            if (rows == 1 || rows == 3) {
+                // Per-lane constants: last-dim coordinate (times VEC) and, for
+                // rows 1, the row within the tile.
+                b << "  " << t << " cl_[" << unroll << "];\n";
+                if (rows == 1) b << "  " << t << " q_[" << unroll << "];\n";
+                b << "#pragma unroll\n  for (int u = 0; u < " << unroll << "; ++u) {\n";
+                b << "    const " << t << " l_ = " << lane << ";\n";
+                if (rows == 1) {
+                    b << "    const " << t << " q = (" << t << ")ormi_fdiv((unsigned)l_, (unsigned)" << Mn << ", (unsigned)(" << Mn
+                      << " >> 32));\n";
+                    b << "    q_[u] = q;\n    cl_[u] = (l_ - q * (" << t << ")" << Dn << ") * " << V << ";\n";
+                } else {
+                    b << "    cl_[u] = l_ * " << V << ";\n";
+                }
+                b << "  }\n";
+                g.declare_leaf_regs(b, "  ", unroll, hoist);
+                b << "#pragma unroll\n  for (int u = 0; u < " << unroll << "; ++u) {\n";
+                b << "    const " << t << " " << cl << " = cl_[u];\n";
+                load_all("    ", hoist);
+                b << "  }\n";
+                const std::string step = rows == 1 ? "(" + t + ")P" : "1";
+                b << "  for (" << t << " base = (" << t << ")blockIdx.x * tile, row = (" << t << ")blockIdx.x * " << step
+                  << "; base < (" << t << ")G; base += (" << t << ")gridDim.x * tile, row += (" << t << ")gridDim.x * " << step
+                  << ") {\n";
+                g.declare_leaf_regs(b, "    ", unroll, in_loop);
+                if (rows == 3) {
+                    g.declare_coords(b, "    ", outer);
+                    g.decompose(b, "    ", "row", outer);
+                }
+                b << "#pragma unroll\n    for (int u = 0; u < " << unroll << "; ++u) {\n";
+                if (rows == 1) {
+                    // The last tile may hold fewer than P rows: clamp the row for the loads.
+                    b << "      const " << t << " o_ = row + q_[u] < (" << t << ")R ? row + q_[u] : (" << t << ")R - 1;\n";
+                    g.declare_coords(b, "      ", outer);
+                    g.decompose(b, "      ", "o_", outer);
+                }
+                b << "      const " << t << " " << cl << " = cl_[u];\n";
+                load_all("      ", in_loop);
+                b << "    }\n";
+            } else if (rows == 2) {
+                b << "  for (" << t << " base = (" << t << ")blockIdx.x * tile; base < (" << t << ")G; base += (" << t
+                  << ")gridDim.x * tile) {\n";
+                b << "    const " << t << " row = (" << t << ")ormi_fdiv((unsigned)base, (unsigned)" << Mn << ", (unsigned)(" << Mn
+                  << " >> 32));\n";
+                b << "    const " << t << " col0 = base - row * (" << t << ")" << Dn << ";\n";
+                g.declare_coords(b, "    ", outer);
+                g.decompose(b, "    ", "row", outer);
+                g.declare_leaf_regs(b, "    ", unroll);
+                b << "#pragma unroll\n    for (int u = 0; u < " << unroll << "; ++u) {\n";
+                b << "      const " << t << " " << cl << " = (col0 + " << lane << ") * " << V << ";\n";
+                load_all("      ", in_loop);
+                b << "    }\n";
+            } else {
+                b << "  for (" << t << " base = (" << t << ")blockIdx.x * tile; base < (" << t << ")G; base += (" << t
+                  << ")gridDim.x * tile) {\n";
+                g.declare_leaf_regs(b, "    ", unroll);
+                b << "#pragma unroll\n    for (int u = 0; u < " << unroll << "; ++u) {\n";
+                b << "      const " << t << " gg = base + " << lane << ";\n";
+                b << "      const " << t << " gc = gg < (" << t << ")G ? gg : (" << t << ")G - 1;\n";
+                g.declare_coords(b, "      ", all);
+                g.decompose(b, "      ", "gc", all);
+                load_all("      ", in_loop);
+                b << "    }\n";
             }
-            b << "    }\n";
+            // rows 2 and 3 tiles are always full; rows 0 and 1 guard the last one.
+            const bool guard = rows == 0 || rows == 1;
             b << "#pragma unroll\n    for (int u = 0; u < " << unroll << "; ++u) {\n";
             auto res = [&](size_t r) { return nout == 1 ? std::string("res") : "res" + std::to_string(r); };
             for (size_t r = 0; r < nout; ++r) b << "      float " << res(r) << "[" << V << "];\n";
@@ -675,7 +782,9 @@ namespace ormi::hip {
             g.eval(b, "        ", "u", "k");
             for (size_t r = 0; r < nout; ++r) b << "        " << res(r) << "[k] = " << g.root_names[r] << ";\n";
             b << "      }\n";
-            b << "      if (gi[u] < (" << t << ")G) {\n";
+            b << "      const " << t << " go = base + " << lane << ";\n";
+            if (guard) b << "      if (go < (" << t << ")G) {\n";
+            const std::string ind = guard ? "        " : "      ";
             const bool nt = tn.map_nt_stores;
             for (size_t r = 0; r < nout; ++r) {
                 const DType odt = out_dtypes[r];
@@ -684,15 +793,16 @@ namespace ormi::hip {
                     std::string val = std::string(vt) + "{";
                     for (int q = 0; q < 4; ++q) val += (q ? ", " : "") + from_f32(odt, res(r) + "[" + std::to_string(q) + "]");
                     val += "}";
-                    const std::string addr = g.elem_ptr(std::string(vt) + "*", out_name(r), "gi[u] * 4", dtype_size(odt), false);
-                    if (nt) b << "        __builtin_nontemporal_store(" << val << ", " << addr << ");\n";
-                    else b << "        *" << addr << " = " << val << ";\n";
+                    const std::string addr = g.elem_ptr(std::string(vt) + "*", out_name(r), "go * 4", dtype_size(odt), false);
+                    if (nt) b << ind << "__builtin_nontemporal_store(" << val << ", " << addr << ");\n";
+                    else b << ind << "*" << addr << " = " << val << ";\n";
                 } else {
-                    b << "        *" << g.elem_ptr(std::string(storage_type(odt)) + "*", out_name(r), "gi[u]", dtype_size(odt), false)
+                    b << ind << "*" << g.elem_ptr(std::string(storage_type(odt)) + "*", out_name(r), "go", dtype_size(odt), false)
                       << " = " << from_f32(odt, res(r) + "[0]") << ";\n";
                 }
             }
-            b << "      }\n    }\n  }\n";
+            if (guard) b << "      }\n";
+            b << "    }\n  }\n";
         });
         return k;
     }

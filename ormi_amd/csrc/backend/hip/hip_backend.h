@@ -123,6 +123,7 @@ namespace ormi::hip {
         bool map_nt_stores = false;   // non-temporal hint on a map's output stores
         bool reduce_nt_loads = true;  // non-temporal hint on a reduction's loads
         bool map_off32 = true;        // 32-bit byte offsets from uniform bases when they fit (map)
+        bool map_rows = true;         // row-aligned tiles when a tile covers whole rows or lies in one (map)
     };
     const Tuning& tuning();
 

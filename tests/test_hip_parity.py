@@ -196,6 +196,78 @@ def test_views_and_strides_as_leaves(cpu, hip):
     assert_bits_equal(e_h.numpy(), e_c.numpy())
 
 
+# Row-aligned map tiles. A tile is 1024 groups (256 threads x 4 groups; a group
+# is 4 floats when every operand allows 128-bit accesses, else 1). rows=1: a
+# tile spans P whole rows (lane constants, last-dim-only operands loaded once,
+# a partial last tile when P does not divide the row count); rows=2: a tile
+# lies in one row; rows=3: a tile is one row; rows=0: neither.
+def row_graph(dev, x, bias, scale, xt=None):
+    X, B, S = T(x, dev), T(bias, dev), T(scale, dev)
+    z = (X + B) * S - X * 0.5
+    if xt is not None:  # a transposed operand: 1-float groups
+        z = z + T(xt, dev).transpose().realize() * S  # the realized view aliases xt's buffer
+    return z
+
+
+def row_inputs(rows, cols, vec1, seed=31):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((rows, cols)).astype(np.float32)
+    bias = rng.normal(0, 0.1, cols).astype(np.float32)
+    scale = rng.uniform(0.5, 1.5, (rows, 1)).astype(np.float32)
+    xt = rng.standard_normal((cols, rows)).astype(np.float32) if vec1 else None
+    return x, bias, scale, xt
+
+
+@pytest.mark.parametrize("shape,mode,vec1", [
+    ((6, 4096), 3, False), ((33, 256), 1, False), ((32, 256), 1, False), ((33, 256), 1, True),
+    ((5, 1024), 3, True), ((3, 8192), 2, False), ((2, 3072), 2, True), ((7, 300), 0, False)])
+def test_row_aligned_map_tiles(ob, cpu, hip, shape, mode, vec1):
+    x, bias, scale, xt = row_inputs(*shape, vec1)
+    z = row_graph(hip, x, bias, scale, xt)
+    plan = ob._plan_kernel(z._node)["plan"]
+    assert f"rows={mode}" in plan and ("vec=1" in plan) == vec1, plan
+    assert_bits_equal(z.numpy(), row_graph(cpu, x, bias, scale, xt).numpy())
+
+
+@pytest.mark.parametrize("a_shape,b_shape,c_shape,mode", [
+    ((4, 1, 256), (1, 3, 256), (4, 3, 1), 1), ((2, 1, 8192), (1, 3, 8192), (2, 3, 1), 2),
+    ((3, 1, 4096), (1, 5, 4096), (3, 5, 1), 3)])
+def test_row_aligned_map_tiles_3d(ob, cpu, hip, a_shape, b_shape, c_shape, mode):
+    """Three dims that do not merge: the outer coordinates come from the row
+    index by division (per lane for rows=1, per tile for rows=2 and 3)."""
+    rng = np.random.default_rng(32)
+    a, b, c = (rng.standard_normal(s).astype(np.float32) for s in (a_shape, b_shape, c_shape))
+
+    def graph(dev):
+        A, B, C = T(a, dev), T(b, dev), T(c, dev)
+        return A * B + C - A / (C * C + 1.0)
+
+    z = graph(hip)
+    plan = ob._plan_kernel(z._node)["plan"]
+    assert f"rows={mode}" in plan and "ndim=3" in plan, plan
+    assert_bits_equal(z.numpy(), graph(cpu).numpy())
+
+
+@pytest.mark.parametrize("shape,mode,vec1", [
+    ((262161, 256), 1, False), ((70001, 256), 1, True), ((16400, 4096), 3, False), ((8200, 8192), 2, False)])
+def test_row_aligned_map_tiles_grid_stride(ob, hip, shape, mode, vec1):
+    """More tiles than the grid holds (64 blocks per CU), so every block walks
+    several tiles and the row cursor advances with the grid stride. The chain is
+    + - x only, so numpy's float32 arithmetic in the same order is the exact
+    answer (the oracle's tape computes the same bits; numpy keeps the 67M-element
+    cases to seconds)."""
+    x, bias, scale, xt = row_inputs(*shape, vec1, seed=33)
+    z = row_graph(hip, x, bias, scale, xt)
+    plan = ob._plan_kernel(z._node)["plan"]
+    assert f"rows={mode}" in plan, plan
+    tiles = int(plan.split("groups=")[1].split()[0]) // 1024
+    assert tiles > 256 * 64
+    want = (x + bias) * scale - x * np.float32(0.5)
+    if xt is not None:
+        want = want + xt.T * scale
+    assert_bits_equal(z.numpy(), want)
+
+
 def test_bf16_leaves_and_casts(cpu, hip):
     rng = np.random.default_rng(23)
     x = rng.standard_normal((40, 64)).astype(np.float32)
