@@ -115,12 +115,12 @@ namespace ormi::hip {
     // Launch-shape knobs of the generated kernels. Defaults are the values
     // measured best on MI355X; ORMI_* environment variables override them.
     struct Tuning {
-        int map_unroll = 4;        // VEC groups per thread per iteration (map)
+        int map_unroll = 2;        // VEC groups per thread per iteration (map)
         int map_blocks_per_cu = 64;
         int row_unroll = 4;        // VEC groups per lane per iteration (row reduce)
         int col_waves = 8;         // waves per block along R (column reduce)
         bool map_nt_loads = false;    // non-temporal hint on a map's operand loads
-        bool map_nt_stores = false;   // non-temporal hint on a map's output stores
+        bool map_nt_stores = true;    // non-temporal hint on a map's output stores
         bool reduce_nt_loads = true;  // non-temporal hint on a reduction's loads
         bool map_off32 = true;        // 32-bit byte offsets from uniform bases when they fit (map)
         bool map_rows = true;         // row-aligned tiles when a tile covers whole rows or lies in one (map)

@@ -58,6 +58,14 @@ def cabi():
     return lib
 
 
+def map_tile_groups(ob) -> int:
+    """Groups per map tile (256 threads x the planned unroll), from a plan."""
+    from ormi_amd import Tensor
+
+    plan = ob._plan_kernel((Tensor(np.zeros(4, np.float32), "cpu") * 2.0)._node)["plan"]
+    return 256 * int(plan.split("unroll=")[1].split()[0])
+
+
 def header_functions():
     text = (ROOT / "include" / "ormi_hip.h").read_text()
     return sorted(set(re.findall(r"\b(ormi_hip_\w+)\s*\(", text)))

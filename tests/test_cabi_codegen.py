@@ -9,7 +9,7 @@ import ctypes
 import numpy as np
 import pytest
 
-from conftest import header_functions
+from conftest import map_tile_groups, header_functions
 
 ORMI_HIP_OK, ORMI_HIP_ERR_NO_DEVICE, ORMI_HIP_ERR_INVALID, ORMI_HIP_ERR_COMPILE, ORMI_HIP_ERR_UNSUPPORTED = 0, 2, 3, 4, 5
 
@@ -148,20 +148,23 @@ def test_generated_map_kernel_structure(ob, cpu, cabi):
     assert size > 0
 
 
+def row_mode_shapes(tile):
+    """(rows, cols) of fp32 maps whose tile of `tile` groups of 4 floats spans
+    whole rows (1), lies inside one row (2), is one row (3) or neither (0)."""
+    return {1: [(64, 128), (512, 256)], 3: [(8, 4 * tile), (512, 4 * tile)], 2: [(4, 8 * tile), (2, 12 * tile)],
+            0: [(10, 100), (7, 300)]}
+
+
 def test_kernel_source_is_shape_independent(ob, cpu):
     """Sizes and strides are arguments: the same chain over another shape of the
     same structure and the same tile alignment to the rows generates the same
-    kernel (one cache entry). With 1024 groups of 4 per tile, a row of 128 or
-    256 floats (32 or 64 groups) makes a tile span whole rows (rows=1), 4096
-    floats make a tile one row (rows=3), 8192 or 16384 make it part of one
-    (rows=2), and 100 or 300 align with neither (rows=0)."""
+    kernel (one cache entry)."""
     def plan(r, c):
         X, B = _cpu(np.zeros((r, c))), _cpu(np.zeros(c))
         return ob._plan_kernel(((X + B) * 2.0).exp()._node)
 
     names = {}
-    for mode, shapes in {1: [(64, 128), (512, 256)], 3: [(8, 4096), (512, 4096)], 2: [(4, 8192), (2, 16384)],
-                         0: [(10, 100), (7, 300)]}.items():
+    for mode, shapes in row_mode_shapes(map_tile_groups(ob)).items():
         a, b = plan(*shapes[0]), plan(*shapes[1])
         assert f"rows={mode}" in a["plan"] and f"rows={mode}" in b["plan"], (a["plan"], b["plan"])
         assert a["name"] == b["name"] and a["source"] == b["source"]
@@ -170,13 +173,17 @@ def test_kernel_source_is_shape_independent(ob, cpu):
     assert plan(64, 128)["name"] != ob._plan_kernel((_cpu(np.zeros((64, 128))) * 2.0).exp()._node)["name"]
 
 
-@pytest.mark.parametrize("shape,mode", [((33, 256), 1), ((3, 8192), 2), ((6, 4096), 3), ((7, 300), 0)])
+@pytest.mark.parametrize("mode", [1, 2, 3, 0])
 @pytest.mark.parametrize("variant", ["plain", "3d", "vec1", "multi"])
-def test_row_aligned_map_kernels_compile(ob, cpu, cabi, shape, mode, variant):
+def test_row_aligned_map_kernels_compile(ob, cpu, cabi, mode, variant):
     """Every tile alignment compiles for gfx950: two dims and three (outer
-    coordinates by division), 1-float groups (a transposed operand) and several
-    outputs from one kernel."""
-    r, c = shape
+    coordinates by division), 1-float groups (a transposed operand, with the
+    row length in floats set so the alignment holds) and several outputs from
+    one kernel."""
+    tile = map_tile_groups(ob)
+    r, c = row_mode_shapes(tile)[mode][0]
+    if variant == "vec1" and mode in (2, 3):
+        c //= 4
     x, bias, scale = _cpu(np.ones((r, c))), _cpu(np.ones(c)), _cpu(np.ones((r, 1)))
     if variant == "3d":
         x = _cpu(np.ones((2, 1, c))) * _cpu(np.ones((1, r, c)))
@@ -188,8 +195,8 @@ def test_row_aligned_map_kernels_compile(ob, cpu, cabi, shape, mode, variant):
         d = ob._plan_group([z, (x * scale)._node])
     else:
         d = ob._plan_kernel(z)
-    if variant == "vec1" and mode == 3:
-        mode = 2  # 4096 one-float groups a row: four tiles
+    if variant == "3d":
+        assert "ndim=3" in d["plan"], d["plan"]
     assert f"rows={mode}" in d["plan"] and ("vec=1" in d["plan"]) == (variant == "vec1"), d["plan"]
     rc, _ = _compile_only(cabi, d["source"], ob._rtc_options())
     assert rc == ORMI_HIP_OK, (d["plan"], cabi.ormi_hip_last_error())

@@ -11,7 +11,7 @@ import math
 import numpy as np
 import pytest
 
-from conftest import fp32_sum_tolerance
+from conftest import fp32_sum_tolerance, map_tile_groups
 
 pytestmark = pytest.mark.gpu
 
@@ -196,11 +196,11 @@ def test_views_and_strides_as_leaves(cpu, hip):
     assert_bits_equal(e_h.numpy(), e_c.numpy())
 
 
-# Row-aligned map tiles. A tile is 1024 groups (256 threads x 4 groups; a group
-# is 4 floats when every operand allows 128-bit accesses, else 1). rows=1: a
-# tile spans P whole rows (lane constants, last-dim-only operands loaded once,
-# a partial last tile when P does not divide the row count); rows=2: a tile
-# lies in one row; rows=3: a tile is one row; rows=0: neither.
+# Row-aligned map tiles. A tile is 256 threads x the planned unroll groups (a
+# group is 4 floats when every operand allows 128-bit accesses, else 1).
+# rows=1: a tile spans P whole rows (lane constants, last-dim-only operands
+# loaded once, a partial last tile when P does not divide the row count);
+# rows=2: a tile lies in one row; rows=3: a tile is one row; rows=0: neither.
 def row_graph(dev, x, bias, scale, xt=None):
     X, B, S = T(x, dev), T(bias, dev), T(scale, dev)
     z = (X + B) * S - X * 0.5
@@ -218,10 +218,16 @@ def row_inputs(rows, cols, vec1, seed=31):
     return x, bias, scale, xt
 
 
-@pytest.mark.parametrize("shape,mode,vec1", [
-    ((6, 4096), 3, False), ((33, 256), 1, False), ((32, 256), 1, False), ((33, 256), 1, True),
-    ((5, 1024), 3, True), ((3, 8192), 2, False), ((2, 3072), 2, True), ((7, 300), 0, False)])
-def test_row_aligned_map_tiles(ob, cpu, hip, shape, mode, vec1):
+def row_case(tile, case):
+    """(shape, rows mode, 1-float groups) for a tile of `tile` groups."""
+    return {"span": ((33, 256), 1, False), "span_full": ((32, 256), 1, False), "span_vec1": ((33, 256), 1, True),
+            "one": ((6, 4 * tile), 3, False), "one_vec1": ((5, tile), 3, True), "inside": ((3, 8 * tile), 2, False),
+            "inside_vec1": ((2, 3 * tile), 2, True), "none": ((7, 300), 0, False)}[case]
+
+
+@pytest.mark.parametrize("case", ["span", "span_full", "span_vec1", "one", "one_vec1", "inside", "inside_vec1", "none"])
+def test_row_aligned_map_tiles(ob, cpu, hip, case):
+    shape, mode, vec1 = row_case(map_tile_groups(ob), case)
     x, bias, scale, xt = row_inputs(*shape, vec1)
     z = row_graph(hip, x, bias, scale, xt)
     plan = ob._plan_kernel(z._node)["plan"]
@@ -229,17 +235,17 @@ def test_row_aligned_map_tiles(ob, cpu, hip, shape, mode, vec1):
     assert_bits_equal(z.numpy(), row_graph(cpu, x, bias, scale, xt).numpy())
 
 
-@pytest.mark.parametrize("a_shape,b_shape,c_shape,mode", [
-    ((4, 1, 256), (1, 3, 256), (4, 3, 1), 1), ((2, 1, 8192), (1, 3, 8192), (2, 3, 1), 2),
-    ((3, 1, 4096), (1, 5, 4096), (3, 5, 1), 3)])
-def test_row_aligned_map_tiles_3d(ob, cpu, hip, a_shape, b_shape, c_shape, mode):
+@pytest.mark.parametrize("mode", [1, 2, 3])
+def test_row_aligned_map_tiles_3d(ob, cpu, hip, mode):
     """Three dims that do not merge: the outer coordinates come from the row
     index by division (per lane for rows=1, per tile for rows=2 and 3)."""
+    tile = map_tile_groups(ob)
+    c = {1: 256, 2: 8 * tile, 3: 4 * tile}[mode]
     rng = np.random.default_rng(32)
-    a, b, c = (rng.standard_normal(s).astype(np.float32) for s in (a_shape, b_shape, c_shape))
+    a, b, s = (rng.standard_normal(sh).astype(np.float32) for sh in ((4, 1, c), (1, 3, c), (4, 3, 1)))
 
     def graph(dev):
-        A, B, C = T(a, dev), T(b, dev), T(c, dev)
+        A, B, C = T(a, dev), T(b, dev), T(s, dev)
         return A * B + C - A / (C * C + 1.0)
 
     z = graph(hip)
@@ -248,20 +254,24 @@ def test_row_aligned_map_tiles_3d(ob, cpu, hip, a_shape, b_shape, c_shape, mode)
     assert_bits_equal(z.numpy(), graph(cpu).numpy())
 
 
-@pytest.mark.parametrize("shape,mode,vec1", [
-    ((262161, 256), 1, False), ((70001, 256), 1, True), ((16400, 4096), 3, False), ((8200, 8192), 2, False)])
-def test_row_aligned_map_tiles_grid_stride(ob, hip, shape, mode, vec1):
+@pytest.mark.parametrize("case", ["span", "span_vec1", "one", "inside"])
+def test_row_aligned_map_tiles_grid_stride(ob, hip, case):
     """More tiles than the grid holds (64 blocks per CU), so every block walks
     several tiles and the row cursor advances with the grid stride. The chain is
     + - x only, so numpy's float32 arithmetic in the same order is the exact
-    answer (the oracle's tape computes the same bits; numpy keeps the 67M-element
-    cases to seconds)."""
+    answer (the oracle's tape computes the same bits; numpy keeps the 30-70M
+    element cases to seconds)."""
+    tile = map_tile_groups(ob)
+    grid = 256 * 64
+    shape, mode, vec1 = {"span": ((grid * tile // 64 + 17, 256), 1, False),  # 64 groups a row
+                         "span_vec1": ((grid * tile // 256 + 5, 256), 1, True),  # 256 groups a row
+                         "one": ((grid + 16, 4 * tile), 3, False),
+                         "inside": ((grid // 2 + 8, 8 * tile), 2, False)}[case]
     x, bias, scale, xt = row_inputs(*shape, vec1, seed=33)
     z = row_graph(hip, x, bias, scale, xt)
     plan = ob._plan_kernel(z._node)["plan"]
     assert f"rows={mode}" in plan, plan
-    tiles = int(plan.split("groups=")[1].split()[0]) // 1024
-    assert tiles > 256 * 64
+    assert -(-int(plan.split("groups=")[1].split()[0]) // tile) > grid  # tiles, the last one possibly partial
     want = (x + bias) * scale - x * np.float32(0.5)
     if xt is not None:
         want = want + xt.T * scale
