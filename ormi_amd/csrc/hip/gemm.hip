@@ -462,9 +462,9 @@ struct Launcher {
 //   1: 256x256x64, 2x4 waves (128x64 per wave, 2 waves/SIMD)
 //   2: 256x256x64, 4x2 waves (64x128 per wave, 2 waves/SIMD)
 //   3: 128x128x64, 2x2 waves (64x64 per wave, 2 blocks/CU)
-// fp32 configurations (ORMI_GEMM_CFG32 forces one; by default 2, measured fastest
-// on MI355X for the forward and both backward layouts of the benchmark shapes,
-// and 3 for short-K shapes that 128x256 tiles cannot spread over the CUs):
+// fp32 configurations (ORMI_GEMM_CFG32 forces one; by default 2 for shapes in
+// whole 128x256 tiles, and 3 for short-K shapes that 128x256 tiles cannot
+// spread over the CUs and for shapes with partial tiles):
 //   0: 128x128x32, 2x2 waves (64x64 per wave)
 //   1: 256x128x32, 4x2 waves (64x64 per wave)
 //   2: 128x256x32, 2x4 waves (64x64 per wave)
@@ -1164,15 +1164,20 @@ extern "C" int ormi_hip_gemm_ex(const ormi_gemm_desc* d, const ormi_gemm_epilogu
                      (b_kc || d->N % 8 == 0) && a_span < (1LL << 32) && b_span < (1LL << 32);
     int id = dma ? dma_id : f32 ? env_cfg("ORMI_GEMM_CFG32", -1) : env_cfg("ORMI_GEMM_CFG16", 0);
     if (f32 && id < 0) {
-        // 128x256 tiles (config 2) unless they cannot fill the compute units
-        // and K is short: then 128x128 tiles (config 3) fill them without a
-        // K split, whose partial round trip and second kernel cost more than
-        // the smaller tiles lose at K <= 1024 (measured: 1024x4096x1024 86 us
-        // against 94 us split; at K = 2048 the split is 4% faster).
+        // 128x256 tiles (config 2) for M and N in whole 128x256 tiles, unless
+        // they cannot fill the compute units and K is short: then 128x128
+        // tiles (config 3) fill them without a K split, whose partial round
+        // trip and second kernel cost more than the smaller tiles lose at
+        // K <= 1024 (measured: 1024x4096x1024 86 us against 94 us split; at
+        // K = 2048 the split is 4% faster). Shapes with a partial tile take
+        // config 3: config 2 measured 16-29% slower on 3000x3000x1000,
+        // 2500x4000x1500, 4100x4100x512 and 5000^3, and config 3 18% faster
+        // than either other on 3000x4096x1024, within 8% of the best on all.
         const long long cus_ll = compute_units();
         const long long t2 = (long long)((d->M + 127) / 128) * ((d->N + 255) / 256) * batch;
         const long long t3 = (long long)((d->M + 127) / 128) * ((d->N + 127) / 128) * batch;
-        id = (t2 < cus_ll && t3 >= cus_ll && d->K <= 1024) ? 3 : 2;
+        const bool whole2 = d->M % 128 == 0 && d->N % 256 == 0;
+        id = (!whole2 || (t2 < cus_ll && t3 >= cus_ll && d->K <= 1024)) ? 3 : 2;
     }
     const Cfg cf = dma ? (d->dtype == ORMI_DTYPE_BF16 ? cfg_dma<TrBF16>(id) : cfg_dma<TrF16>(id))
                        : f32 ? cfg32(id) : (d->dtype == ORMI_DTYPE_BF16 ? cfg16<TrBF16>(id) : cfg16<TrF16>(id));
