@@ -122,7 +122,9 @@ int ormi_hip_rtc_cache_size(uint64_t* entries);
  * dtype: ORMI_DTYPE_F32 (fp32 MFMA), ORMI_DTYPE_BF16 or ORMI_DTYPE_F16
  * (MFMA with fp32 accumulation). Batch index b decomposes row-major over
  * batch_shape[0..batch_ndim); each operand's batch offset is
- * sum(coord[i] * {a,b}_batch_stride[i]) — a stride of 0 broadcasts. */
+ * sum(coord[i] * {a,b}_batch_stride[i]) — a stride of 0 broadcasts.
+ * M == 0 or N == 0 is a no-op; K == 0 writes zeros to C and reads neither
+ * operand (a and b may then be null). */
 #define ORMI_GEMM_MAX_BATCH_DIMS 4
 typedef struct ormi_gemm_desc {
     int         dtype;

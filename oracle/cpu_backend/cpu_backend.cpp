@@ -337,7 +337,10 @@ namespace ormi::oracle {
         const auto& a = std::get<ReduceAttrs>(root->attrs);
         const auto& x = root->parents[0];
         const long long nout = shape_numel(root->view.shape);
-        if (shape_numel(x->view.shape) == 0) throw std::runtime_error("zero-size array to reduction operation maximum which has no identity");
+        // numpy's rule: an empty result is fine; a non-empty one over a
+        // zero-length reduced range has no identity to return.
+        if (nout > 0 && shape_numel(x->view.shape) == 0)
+            throw std::runtime_error("zero-size array to reduction operation maximum which has no identity");
         std::vector<float> best(nout, 0.0f);
         std::vector<long long> idx(nout, -1);
         const void* in = x->data->ptr;
@@ -351,11 +354,11 @@ namespace ormi::oracle {
         });
         if (want_index) {
             auto out = empty(root->view.shape, DeviceEnum::CPU, DType::Int64);
-            std::memcpy(out->ptr, idx.data(), nout * sizeof(long long));
+            if (nout) std::memcpy(out->ptr, idx.data(), nout * sizeof(long long));
             root->data = out;
         } else {
             auto out = empty(root->view.shape, DeviceEnum::CPU, DType::Float32);
-            std::memcpy(out->ptr, best.data(), nout * sizeof(float));
+            if (nout) std::memcpy(out->ptr, best.data(), nout * sizeof(float));
             root->data = out;
         }
     }

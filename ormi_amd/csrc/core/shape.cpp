@@ -20,6 +20,9 @@ namespace ormi {
     }
 
     // Right-aligned numpy broadcasting (reference: csrc/core/shape.cpp:27-44).
+    // A size-1 dim takes the other operand's size, so a 0-length dim against
+    // 1 stays 0 as in numpy; the reference takes max(da, db) = 1 there, and its
+    // kernels then read an element of the empty operand.
     std::vector<int> broadcast_shapes(const std::vector<int>& a, const std::vector<int>& b) {
         const int na = (int)a.size(), nb = (int)b.size();
         const int n = std::max(na, nb);
@@ -28,7 +31,7 @@ namespace ormi {
             const int da = i < n - na ? 1 : a[i - (n - na)];
             const int db = i < n - nb ? 1 : b[i - (n - nb)];
             if (da != db && da != 1 && db != 1) throw std::runtime_error("Operands could not be broadcast together.");
-            out[i] = std::max(da, db);
+            out[i] = da == 1 ? db : da;
         }
         return out;
     }

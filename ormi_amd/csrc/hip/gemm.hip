@@ -1081,7 +1081,9 @@ extern "C" int ormi_hip_gemm_ex(const ormi_gemm_desc* d, const ormi_gemm_epilogu
     }
     if (batch > 65535) return fail(ORMI_HIP_ERR_UNSUPPORTED, "ormi_hip_gemm: more than 65535 batches");
     if ((long long)d->M * d->N == 0) return ORMI_HIP_OK;
-    if (!d->a || !d->b || !d->c) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_gemm: null operand");
+    // With K == 0 the operands hold no elements (an empty buffer may have no
+    // address) and are never read.
+    if (!d->c || (d->K > 0 && (!d->a || !d->b))) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_gemm: null operand");
     if (batch * d->M > 0x7fffffffLL) return fail(ORMI_HIP_ERR_UNSUPPORTED, "ormi_hip_gemm: more than 2^31 output rows");
     Epi epi;
     int rc = make_epi(d, epi_in, batch, &epi);

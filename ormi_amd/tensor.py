@@ -224,14 +224,15 @@ class Tensor:
         return Tensor._wrap(ormi_backend.argmax(self._node, self._axes(axis), keepdims), self.device)
 
     def mean(self, axis=None, keepdims: bool = False) -> "Tensor":
-        """sum * (1/N), N = number of reduced elements (exact scaling for powers of two)."""
+        """sum * (1/N), N = number of reduced elements (exact scaling for powers of two).
+        An empty reduced range gives NaN (0 * inf), as numpy's mean does."""
         axes = self._axes(axis)
         shape = self.shape
         reduced = range(len(shape)) if not axes else [a % len(shape) for a in axes]
         n = 1
         for a in set(reduced):
             n *= shape[a]
-        return self.sum(axis, keepdims) * (1.0 / n)
+        return self.sum(axis, keepdims) * (1.0 / n if n else math.inf)
 
     # ------------------------------------------------------------------ views
     def reshape(self, shape) -> "Tensor":

@@ -66,6 +66,49 @@ def map_tile_groups(ob) -> int:
     return 256 * int(plan.split("unroll=")[1].split()[0])
 
 
+def empty_tensor_cases(dev: str) -> dict:
+    """Graphs over 0-length dims on `dev`: name -> numpy result, or the
+    ("error", message) a reduction with no identity raises. numpy's rules: a
+    0-length dim broadcasts against 1 to 0; sum over nothing is 0, mean NaN;
+    max/argmax over nothing raise unless the result itself is empty; a K = 0
+    product is zeros. Gradients flow through empty operands."""
+    from ormi_amd import Tensor
+
+    def T(shape, fill=0.0, **kw):
+        return Tensor(np.full(shape, fill, np.float32), dev, **kw)
+
+    cases = {
+        "bcast_rows": lambda: T((0, 5)) + T((5,), 1.0),
+        "bcast_cols": lambda: T((3, 0)) * T((3, 1), 2.0),
+        "bcast_both": lambda: T((0, 1)) - T((1, 7), 1.0),
+        "unary": lambda: T((4, 0)).tanh(),
+        "sum_rows": lambda: T((0, 5)).sum(0),
+        "sum_cols": lambda: T((0, 5)).sum(1),
+        "sum_all": lambda: T((0, 5)).sum(),
+        "sum_keep": lambda: T((2, 0, 3)).sum(1, keepdims=True),
+        "mean_empty": lambda: T((0, 5)).mean(0),
+        "max_kept_empty": lambda: T((0, 5)).max(1),
+        "max_over_empty": lambda: T((0, 5)).max(0),
+        "argmax_over_empty": lambda: T((3, 0)).argmax(1),
+        "matmul_k0": lambda: T((3, 0)) @ T((0, 4)),
+        "matmul_m0": lambda: T((0, 3), 1.0) @ T((3, 4), 1.0),
+        "matmul_n0": lambda: T((3, 4), 1.0) @ T((4, 0)),
+        "matmul_batched_k0": lambda: T((2, 3, 0)) @ T((2, 0, 5)),
+    }
+    out = {}
+    for name, f in cases.items():
+        try:
+            out[name] = f().numpy()
+        except RuntimeError as e:
+            out[name] = ("error", str(e))
+    a = T((0, 5), requires_grad=True)
+    b = T((5,), 1.0, requires_grad=True)
+    w = T((5, 3), 1.0, requires_grad=True)
+    ((a * b) @ w).sum().backward()
+    out["grad_a"], out["grad_b"], out["grad_w"] = a.grad.numpy(), b.grad.numpy(), w.grad.numpy()
+    return out
+
+
 def header_functions():
     text = (ROOT / "include" / "ormi_hip.h").read_text()
     return sorted(set(re.findall(r"\b(ormi_hip_\w+)\s*\(", text)))

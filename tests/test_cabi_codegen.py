@@ -63,6 +63,10 @@ def test_gemm_descriptor_validation(cabi):
     assert cabi.ormi_hip_gemm(ctypes.byref(d)) == ORMI_HIP_ERR_INVALID
     d = GemmDesc(dtype=0, M=0, N=4, K=4)  # empty output: nothing to do
     assert cabi.ormi_hip_gemm(ctypes.byref(d)) == ORMI_HIP_OK
+    d = GemmDesc(dtype=0, M=4, N=4, K=4)  # operands are read: null is an error
+    assert cabi.ormi_hip_gemm(ctypes.byref(d)) == ORMI_HIP_ERR_INVALID and b"null" in cabi.ormi_hip_last_error()
+    d = GemmDesc(dtype=0, M=4, N=4, K=0)  # K == 0 reads no operand, but C is written
+    assert cabi.ormi_hip_gemm(ctypes.byref(d)) == ORMI_HIP_ERR_INVALID and b"null" in cabi.ormi_hip_last_error()
 
 
 class GemmEpilogue(ctypes.Structure):

@@ -11,7 +11,7 @@ import math
 import numpy as np
 import pytest
 
-from conftest import fp32_sum_tolerance, map_tile_groups
+from conftest import empty_tensor_cases, fp32_sum_tolerance, map_tile_groups
 
 pytestmark = pytest.mark.gpu
 
@@ -276,6 +276,22 @@ def test_row_aligned_map_tiles_grid_stride(ob, hip, case):
     if xt is not None:
         want = want + xt.T * scale
     assert_bits_equal(z.numpy(), want)
+
+
+def test_empty_tensors_match_oracle(cpu, hip):
+    """0-length dims on the HIP device: the same shapes, values and errors as
+    the oracle (maps and products with nothing to compute launch nothing; sums
+    over nothing fill zeros; max/argmax over nothing raise)."""
+    want, got = empty_tensor_cases(cpu), empty_tensor_cases(hip)
+    assert want.keys() == got.keys()
+    for name in want:
+        w, g = want[name], got[name]
+        if isinstance(w, tuple):
+            assert isinstance(g, tuple) and g[0] == "error" and "zero-size" in g[1], (name, g)
+        else:
+            assert not isinstance(g, tuple), (name, g)
+            assert g.shape == w.shape and g.dtype == w.dtype, (name, g.shape, w.shape)
+            np.testing.assert_array_equal(g, w, err_msg=name)
 
 
 def test_bf16_leaves_and_casts(cpu, hip):

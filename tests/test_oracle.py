@@ -10,7 +10,7 @@ import math
 import numpy as np
 import pytest
 
-from conftest import fp32_sum_tolerance
+from conftest import empty_tensor_cases, fp32_sum_tolerance
 
 
 def T(data, dev="cpu", **kw):
@@ -274,6 +274,31 @@ def test_golden_kats_on_oracle(ob, cpu, name):
 
     case = next(c for c in cases() if c["name"] == name)
     run_case(ob, case, ob.DeviceEnum.CPU)
+
+
+def test_empty_tensors_follow_numpy(cpu):
+    """0-length dims through maps, reductions, products and backward on the
+    oracle, against numpy's results for the same operations."""
+    import warnings
+
+    got = empty_tensor_cases("cpu")
+    z = lambda *s: np.zeros(s, np.float32)  # noqa: E731
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore", RuntimeWarning)  # numpy's mean of nothing
+        want = {
+            "bcast_rows": z(0, 5) + np.ones(5, np.float32), "bcast_cols": z(3, 0) * 2, "bcast_both": z(0, 1) - np.ones((1, 7)),
+            "unary": z(4, 0), "sum_rows": z(0, 5).sum(0), "sum_cols": z(0, 5).sum(1), "sum_all": z(0, 5).sum(),
+            "sum_keep": z(2, 0, 3).sum(1, keepdims=True), "mean_empty": z(0, 5).mean(0), "max_kept_empty": z(0, 5).max(1),
+            "matmul_k0": z(3, 0) @ z(0, 4), "matmul_m0": z(0, 3) @ np.ones((3, 4)), "matmul_n0": np.ones((3, 4)) @ z(4, 0),
+            "matmul_batched_k0": z(2, 3, 0) @ z(2, 0, 5), "grad_a": z(0, 5), "grad_b": z(5), "grad_w": z(5, 3),
+        }
+    for name in ("max_over_empty", "argmax_over_empty"):
+        assert got[name][0] == "error" and "zero-size" in got[name][1], (name, got[name])
+    for name, w in want.items():
+        g = got[name]
+        assert not isinstance(g, tuple), (name, g)
+        assert g.shape == np.shape(w), (name, g.shape, np.shape(w))
+        np.testing.assert_array_equal(g, np.asarray(w, np.float32), err_msg=name)
 
 
 def test_python_scalar_operands_share_leaves_but_keep_signed_zero(cpu):
