@@ -65,7 +65,6 @@ namespace ormi_hip {
 // transposes. K must be a multiple of BK; rows and columns past M / N are
 // clamped on load (they only feed outputs that are not stored).
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) char lds_char;
 
 // The direct loads set M0 (the LDS destination) in inline assembly and list
 // it as clobbered; clang warns that M0 is a reserved register. No code the
@@ -527,13 +526,6 @@ static void run32(int id, const GemmParams& p, dim3 grid, bool even, bool a_kc, 
 //               step KS-1.
 // One barrier per tile; the loads are counted per wave (PER instructions per
 // operand per tile), so the vmcnt bound is exact.
-template <int V>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(V >= 0 && V < 64, "vmcnt is a 6-bit counter");
-    // s_waitcnt encoding: vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt[5:4] at [15:14];
-    // expcnt and lgkmcnt at their maxima (no wait).
-    __builtin_amdgcn_s_waitcnt((V & 15) | ((V >> 4) << 14) | (7 << 4) | (15 << 8));
-}
 // Wait until at most n tiles' loads (PER_TILE instructions each) are pending.
 template <int PER_TILE, int MAXN>
 __device__ __forceinline__ void wait_tiles(int n) {
@@ -542,10 +534,6 @@ __device__ __forceinline__ void wait_tiles(int n) {
     if constexpr (MAXN >= 1) { if (n >= 1) { wait_vmcnt<PER_TILE>(); return; } }
     wait_vmcnt<0>();
 }
-// Workgroup barrier that orders LDS accesses in program order for the
-// compiler without waiting for outstanding vector-memory loads (a C++
-// __syncthreads() would also drain the direct loads of later stages).
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 template <typename Tr, int BM, int BN, int BK, int WGM, int WGN, int STAGES, bool A_KC, bool B_KC>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_pipe_kernel(GemmParams p) {
@@ -1164,8 +1152,20 @@ extern "C" int ormi_hip_gemm_ex(const ormi_gemm_desc* d, const ormi_gemm_epilogu
     const int dma_bk = f32 ? 64 : cfg_dma<TrBF16>(dma_id).BK;
     const bool dma = !f32 && env_cfg("ORMI_GEMM_DMA", 1) != 0 && d->K % dma_bk == 0 && (a_kc || d->M % 8 == 0) &&
                      (b_kc || d->N % 8 == 0) && a_span < (1LL << 32) && b_span < (1LL << 32);
-    int id = dma ? dma_id : f32 ? env_cfg("ORMI_GEMM_CFG32", -1) : env_cfg("ORMI_GEMM_CFG16", 0);
-    if (f32 && id < 0) {
+    // fp32 with direct loads: K in whole 32-deep tiles, mn-contiguous extents
+    // in whole 16-byte chunks, per-lane tile offsets in 32 bits.
+    const long long a_span32 = a_kc ? 256LL * d->a_stride_m * 4 : 64LL * d->a_stride_k * 4 + 1024;
+    const long long b_span32 = b_kc ? 256LL * d->b_stride_n * 4 : 64LL * d->b_stride_k * 4 + 1024;
+    const int dma32_id = env_cfg("ORMI_GEMM_F32_DMA_CFG", 1);
+    int dma32_bm = 0, dma32_bn = 0, dma32_bk = 0;
+    cfg32_dma(dma32_id, &dma32_bm, &dma32_bn, &dma32_bk);
+    const bool dma32 = f32 && env_cfg("ORMI_GEMM_F32_DMA", 1) != 0 && d->K % dma32_bk == 0 && (a_kc || d->M % 4 == 0) &&
+                       (b_kc || d->N % 4 == 0) && a_span32 < (1LL << 32) && b_span32 < (1LL << 32);
+    int id = dma ? dma_id
+             : dma32 ? dma32_id
+             : f32 ? env_cfg("ORMI_GEMM_CFG32", -1)
+                   : env_cfg("ORMI_GEMM_CFG16", 0);
+    if (f32 && !dma32 && id < 0) {
         // 128x256 tiles (config 2) for M and N in whole 128x256 tiles, unless
         // they cannot fill the compute units and K is short: then 128x128
         // tiles (config 3) fill them without a K split, whose partial round
@@ -1181,8 +1181,11 @@ extern "C" int ormi_hip_gemm_ex(const ormi_gemm_desc* d, const ormi_gemm_epilogu
         const bool whole2 = d->M % 128 == 0 && d->N % 256 == 0;
         id = (!whole2 || (t2 < cus_ll && t3 >= cus_ll && d->K <= 1024)) ? 3 : 2;
     }
-    const Cfg cf = dma ? (d->dtype == ORMI_DTYPE_BF16 ? cfg_dma<TrBF16>(id) : cfg_dma<TrF16>(id))
-                       : f32 ? cfg32(id) : (d->dtype == ORMI_DTYPE_BF16 ? cfg16<TrBF16>(id) : cfg16<TrF16>(id));
+    const Cfg cf = [&] {
+        if (dma) return d->dtype == ORMI_DTYPE_BF16 ? cfg_dma<TrBF16>(id) : cfg_dma<TrF16>(id);
+        if (dma32) return Cfg{dma32_bm, dma32_bn, dma32_bk};
+        return f32 ? cfg32(id) : (d->dtype == ORMI_DTYPE_BF16 ? cfg16<TrBF16>(id) : cfg16<TrF16>(id));
+    }();
     p.tiles_m = (d->M + cf.BM - 1) / cf.BM;
     p.tiles_n = (d->N + cf.BN - 1) / cf.BN;
     // Split K when the tiles cannot occupy the compute units, keeping at least
@@ -1210,7 +1213,7 @@ extern "C" int ormi_hip_gemm_ex(const ormi_gemm_desc* d, const ormi_gemm_epilogu
     // registers ahead of the main loop), and an epilogue in every unrolled
     // store loop of every configuration would multiply the library's code.
     const bool even = d->M % cf.BM == 0 && d->N % cf.BN == 0 && d->K % cf.BK == 0;
-    const bool epi_in_kernel = !dma && f32 && (id == 2 || id == 3) && even && epi_in_store(epi);
+    const bool epi_in_kernel = !dma && f32 && (dma32 || id == 2 || id == 3) && even && epi_in_store(epi);
     const bool finish = splits > 1 || (!epi_in_kernel && epi.kind != ORMI_GEMM_EPI_NONE);
     if (finish) {
         void* ws = nullptr;
@@ -1223,6 +1226,7 @@ extern "C" int ormi_hip_gemm_ex(const ormi_gemm_desc* d, const ormi_gemm_epilogu
     dim3 grid(p.tiles_m * p.tiles_n, 1, (unsigned)(batch * splits));
     if (dma && d->dtype == ORMI_DTYPE_BF16) run_dma<TrBF16>(id, p, grid, a_kc, b_kc);
     else if (dma) run_dma<TrF16>(id, p, grid, a_kc, b_kc);
+    else if (dma32) run32_dma(id, p, grid, a_kc, b_kc, p.epi.kind != ORMI_GEMM_EPI_NONE);
     else if (f32 && p.epi.kind != ORMI_GEMM_EPI_NONE) run32_epi(id, p, grid, a_kc, b_kc);
     else if (f32) run32(id, p, grid, even, a_kc, b_kc);
     else if (d->dtype == ORMI_DTYPE_BF16) run16<TrBF16>(id, p, grid, even, a_kc, b_kc);

@@ -14,6 +14,26 @@ typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) char lds_char;
+
+// Wait until at most V vector-memory instructions of this wave are pending.
+template <int V>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(V >= 0 && V < 64, "vmcnt is a 6-bit counter");
+    // s_waitcnt encoding: vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt[5:4] at [15:14];
+    // expcnt and lgkmcnt at their maxima (no wait).
+    __builtin_amdgcn_s_waitcnt((V & 15) | ((V >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+// The same with lgkmcnt(0): this wave's LDS reads have also completed.
+template <int V>
+__device__ __forceinline__ void wait_vmcnt_lds() {
+    static_assert(V >= 0 && V < 64, "vmcnt is a 6-bit counter");
+    __builtin_amdgcn_s_waitcnt((V & 15) | ((V >> 4) << 14) | (7 << 4));
+}
+// Workgroup barrier that orders LDS accesses in program order for the
+// compiler without waiting for outstanding vector-memory loads (a C++
+// __syncthreads() would also drain the direct loads of later stages).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 // Element-wise epilogue (ormi_hip_gemm_ex). kind is ORMI_GEMM_EPI_NONE in the
 // GEMM kernels whenever the epilogue runs in gemm_finish_kernel instead.
@@ -190,6 +210,8 @@ struct TileLoader {
     static_assert(KC ? (NCHUNK >= 1 && NCHUNK * NT == BMN * KCH) : (KCH == 8 && MC >= 1 && MC * VE * NT == BMN * BK && MCW >= 1),
                   "tile / thread-count combination not supported");
     static_assert(!KMN || (MCU % 32 == 0 && MCU * MC == BMN), "KMN needs whole half-waves per k-row");
+    // load() moves 4, 2 or 1 dwords per k-row of an mn-contiguous tile.
+    static_assert(KC || MCW == 4 || MCW == 2 || MCW == 1, "mn-contiguous tiles need 1, 2 or 4 dwords per thread and k-row");
 
     unsigned r[NREG];
 
@@ -300,6 +322,76 @@ struct TileLoader {
 
 // EPI: the store applies p.epi (only instantiated for the configurations the
 // fp32 dispatch picks by default; the others leave epilogues to the finish pass).
+// Epilogue of one wave's TM x TN 32x32 accumulator blocks, all in bounds:
+// block (i, j) covers rows row0 + 32 i .. and columns col0 + 32 j .. of C
+// (row stride ldc); lane l / register r holds row 8*(r/4) + 4*(l/32) + r%4,
+// column l%32. dd points at D's element (0, 0) for this batch (strides e.d_sm,
+// e.d_sn); aux, when set, shares C's layout. D values are loaded ahead of the
+// stores that need them: loads and stores retire through one in-order
+// counter, so a load issued after a store would wait out a memory latency per
+// element. EARLY_D: dv already holds them (loaded during the last k-tile);
+// otherwise 32x32 block t + 1's are loaded before block t is stored (a lane's
+// blocks are distinct elements, so this holds when D is C itself).
+template <int TM, int TN, bool EARLY_D>
+__device__ __forceinline__ void epi_tile(const Epi& e, float* c, float* aux, const float* dd, int ldc, int row0, int col0,
+                                         const f32x16_t (&acc)[TM][TN], float (&dv)[TM][TN][16], bool reads_d) {
+    const int lane = threadIdx.x & 63;
+    const float sv = e.s ? *e.s : 0.0f;
+    if (!reads_d) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) dv[i][j][r] = 0.0f;
+    }
+    auto load_sub = [&](float (&dst)[16], int i, int j) {
+        const int col = col0 + j * 32 + (lane & 31);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = row0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            dst[r] = dd[row * e.d_sm + col * e.d_sn];
+        }
+    };
+    // One unrolled store loop per (kind, function, aux), chosen once:
+    // a run-time dispatch inside the loop costs more than the arithmetic.
+    auto each = [&](auto&& op) {
+        float dn[16];
+        if (!EARLY_D && reads_d) load_sub(dn, 0, 0);
+#pragma unroll
+        for (int t = 0; t < TM * TN; ++t) {
+            const int i = t / TN, j = t % TN;
+            float dc[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) dc[r] = (EARLY_D || !reads_d) ? dv[i][j][r] : dn[r];
+            if (!EARLY_D && reads_d && t + 1 < TM * TN) load_sub(dn, (t + 1) / TN, (t + 1) % TN);
+            const int col = col0 + j * 32 + (lane & 31);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = row0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                op((long long)row * ldc + col, dc[r], acc[i][j][r]);
+            }
+        }
+    };
+    if (e.kind == ORMI_GEMM_EPI_ADD) {
+        const bool scaled = e.s != nullptr;
+        const int form = e.form;
+        each([&](long long ci, float d, float v) {
+            const float t = scaled ? v * sv : v;
+            c[ci] = form == 0 ? d + t : form == 1 ? d - t : t - d;
+        });
+    } else if (e.kind == ORMI_GEMM_EPI_UNARY) {
+        epi_dispatch_unary(e.fn, [&](auto fn) {
+            if (aux) each([&](long long ci, float, float v) { aux[ci] = v; c[ci] = epi_fn_t<decltype(fn)::value>(v); });
+            else each([&](long long ci, float, float v) { c[ci] = epi_fn_t<decltype(fn)::value>(v); });
+        });
+    } else {
+        epi_dispatch_grad(e.fn, [&](auto fn) {
+            each([&](long long ci, float d, float v) { c[ci] = v * epi_fn_t<decltype(fn)::value>(d); });
+        });
+    }
+}
+
 template <typename Tr, int BM, int BN, int BK, int WGM, int WGN, bool A_KC, bool B_KC, bool EVEN, bool EPI = false>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_kernel(GemmParams p) {
     constexpr int NT = 64 * WGM * WGN;
@@ -431,7 +523,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_kernel(GemmParams p)
 
     // ---- epilogue: 32x32 MFMA result layout, lane l / register r ->
     // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
-    if (!EPI) {
+    if constexpr (!EPI) {
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -447,74 +539,19 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_kernel(GemmParams p)
     } else {
         // Only without a K split (the host runs the finish pass otherwise),
         // so c_off is the batch offset and aux shares it.
-        const Epi& e = p.epi;
-        const float sv = e.s ? *e.s : 0.0f;
-        float* aux = e.aux ? e.aux + c_off : nullptr;
-        // D values are loaded ahead of the stores that need them: loads and
-        // stores retire through one in-order counter, so a load issued after
-        // a store would wait out a memory latency per element. EARLY_D: all
-        // of them during the last k-tile; otherwise 32x32 sub-tile t + 1's
-        // are loaded before sub-tile t is stored (a lane's sub-tiles are
-        // distinct elements, so this holds when D is C itself).
-        if (!reads_d) {
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int j = 0; j < TN; ++j)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) dv[i][j][r] = 0.0f;
-        }
-        auto load_sub = [&](float (&dst)[16], int i, int j) {
-            const float* dd = e.d + d_off;
-            const int col = n0 + wn * WTN + j * 32 + (lane & 31);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                dst[r] = dd[row * e.d_sm + col * e.d_sn];
-            }
-        };
-        // One unrolled store loop per (kind, function, aux), chosen once:
-        // a run-time dispatch inside the loop costs more than the arithmetic.
-        auto each = [&](auto&& op) {
-            float dn[16];
-            if (!EARLY_D && reads_d) load_sub(dn, 0, 0);
-#pragma unroll
-            for (int t = 0; t < TM * TN; ++t) {
-                const int i = t / TN, j = t % TN;
-                float dc[16];
-#pragma unroll
-                for (int r = 0; r < 16; ++r) dc[r] = (EARLY_D || !reads_d) ? dv[i][j][r] : dn[r];
-                if (!EARLY_D && reads_d && t + 1 < TM * TN) load_sub(dn, (t + 1) / TN, (t + 1) % TN);
-                const int col = n0 + wn * WTN + j * 32 + (lane & 31);
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int row = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                    op((long long)row * p.N + col, dc[r], acc[i][j][r]);
-                }
-            }
-        };
-        if (e.kind == ORMI_GEMM_EPI_ADD) {
-            const bool scaled = e.s != nullptr;
-            const int form = e.form;
-            each([&](long long ci, float d, float v) {
-                const float t = scaled ? v * sv : v;
-                c[ci] = form == 0 ? d + t : form == 1 ? d - t : t - d;
-            });
-        } else if (e.kind == ORMI_GEMM_EPI_UNARY) {
-            epi_dispatch_unary(e.fn, [&](auto fn) {
-                if (aux) each([&](long long ci, float, float v) { aux[ci] = v; c[ci] = epi_fn_t<decltype(fn)::value>(v); });
-                else each([&](long long ci, float, float v) { c[ci] = epi_fn_t<decltype(fn)::value>(v); });
-            });
-        } else {
-            epi_dispatch_grad(e.fn, [&](auto fn) {
-                each([&](long long ci, float d, float v) { c[ci] = v * epi_fn_t<decltype(fn)::value>(d); });
-            });
-        }
+        epi_tile<TM, TN, EARLY_D>(p.epi, c, p.epi.aux ? p.epi.aux + c_off : nullptr, p.epi.d + d_off, p.N,
+                                  m0 + wm * WTM, n0 + wn * WTN, acc, dv, reads_d);
     }
 }
 
 // Launch gemm_mfma_kernel with the epilogue in its store: fp32 configuration
 // 2 or 3, M, N and K in whole tiles (gemm_epi.hip).
 void run32_epi(int id, const GemmParams& p, dim3 grid, bool a_kc, bool b_kc);
+// fp32 GEMM with direct HBM->LDS loads (gemm_f32dma.hip): tile extents and
+// depth of configuration id, and its launch. K must be a multiple of the
+// depth, and an mn-contiguous operand's extent a multiple of 4.
+void cfg32_dma(int id, int* bm, int* bn, int* bk);
+// epi: apply p.epi in the store (M, N and K in whole tiles, no K split).
+void run32_dma(int id, const GemmParams& p, dim3 grid, bool a_kc, bool b_kc, bool epi);
 
 }  // namespace ormi_hip

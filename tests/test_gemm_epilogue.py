@@ -11,11 +11,25 @@ Lipschitz constant.
 """
 import ctypes
 import math
+import os
 
 import numpy as np
 import pytest
 
 pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True, params=["direct", "staged"])
+def f32_kernels(request):
+    """Every test runs on both fp32 GEMM families: the direct-load kernels (the
+    default) and the register-staged ones (ORMI_GEMM_F32_DMA=0, read per call)."""
+    old = os.environ.get("ORMI_GEMM_F32_DMA")
+    os.environ["ORMI_GEMM_F32_DMA"] = "1" if request.param == "direct" else "0"
+    yield request.param
+    if old is None:
+        os.environ.pop("ORMI_GEMM_F32_DMA", None)
+    else:
+        os.environ["ORMI_GEMM_F32_DMA"] = old
 
 
 def T(data, dev, **kw):
@@ -57,9 +71,10 @@ def fused_and_plain(ob, build):
     return fused, plain, used
 
 
-# (M, K, N) -> dispatch: fp32 config 3 in the kernel's store; config 2 in the
-# store; K split (finish pass); ragged tiles (finish pass); unaligned K (the
-# generic kernel's store).
+# (M, K, N) -> dispatch (direct-load kernels / register-staged ones): the
+# epilogue in the kernel's store (128x128 tiles / config 3); in the store (one
+# tile / config 2); K split (finish pass); ragged tiles (finish pass);
+# unaligned K (the generic kernel's store).
 SHAPES = [(1024, 1024, 4096), (128, 64, 256), (256, 512, 512), (120, 64, 200), (100, 70, 130)]
 
 
