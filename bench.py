@@ -433,6 +433,95 @@ def bench_c4(ev: Events, n: int) -> dict:
     return out
 
 
+class _GemmDesc(ctypes.Structure):
+    _fields_ = [("dtype", ctypes.c_int), ("M", ctypes.c_int), ("N", ctypes.c_int), ("K", ctypes.c_int),
+                ("a", ctypes.c_void_p), ("a_stride_m", ctypes.c_int64), ("a_stride_k", ctypes.c_int64),
+                ("b", ctypes.c_void_p), ("b_stride_k", ctypes.c_int64), ("b_stride_n", ctypes.c_int64),
+                ("c", ctypes.c_void_p), ("batch_ndim", ctypes.c_int), ("batch_shape", ctypes.c_int * 4),
+                ("a_batch_stride", ctypes.c_int64 * 4), ("b_batch_stride", ctypes.c_int64 * 4)]
+
+
+def vendor_gemm(out_md: Path, cmd: str, rounds: int = 3, n: int = 20) -> None:
+    """The C4 and C5 GEMM shapes through ormi_hip_gemm and through torch.matmul
+    (hipBLASLt) on the same device buffers, in one process, alternating per
+    shape; each side timed with HIP events over n back-to-back launches, best
+    of `rounds`. Writes a markdown summary to out_md."""
+    import torch
+
+    ev = Events()
+    lib = ev.lib
+    lib.ormi_hip_gemm.argtypes = [ctypes.POINTER(_GemmDesc)]
+    lib.ormi_hip_last_error.restype = ctypes.c_char_p
+    assert lib.ormi_hip_init(0) == 0
+
+    def t_torch(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(n):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / n * 1e3
+
+    def t_ours(g):
+        for _ in range(3):
+            assert lib.ormi_hip_gemm(ctypes.byref(g)) == 0, lib.ormi_hip_last_error()
+        ev.sync()
+        e0, e1 = ev.new(), ev.new()
+        ev.record(e0)
+        for _ in range(n):
+            lib.ormi_hip_gemm(ctypes.byref(g))
+        ev.record(e1)
+        ev.sync()
+        return ev.elapsed_ms(e0, e1) / n * 1e3
+
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(3)
+    cases = []
+    for name, M, N, K, ta, tb, bf16 in [("C4 fp32 forward NN", 2048, 4096, 1024, False, False, False),
+                                        ("C4 fp32 dA = dC B^T (NT)", 2048, 1024, 4096, False, True, False),
+                                        ("C4 fp32 dB = A^T dC (TN)", 1024, 4096, 2048, True, False, False),
+                                        ("C5 fp32 H1 W2 (NN)", 1024, 4096, 4096, False, False, False),
+                                        ("C5 fp32 dW2 = H1^T dH2 (TN)", 4096, 4096, 1024, True, False, False),
+                                        ("C5 fp32 dH1 = dH2 W2^T (NT)", 1024, 4096, 4096, False, True, False),
+                                        ("C4 bf16 4096^3 (NN), fp32 out", 4096, 4096, 4096, False, False, True)]:
+        dt = torch.bfloat16 if bf16 else torch.float32
+        a_st = (torch.randn(K, M, device="cuda", generator=gen) / 64).to(dt) if ta else \
+            (torch.randn(M, K, device="cuda", generator=gen) / 64).to(dt)
+        b_st = (torch.randn(N, K, device="cuda", generator=gen) / 64).to(dt) if tb else \
+            (torch.randn(K, N, device="cuda", generator=gen) / 64).to(dt)
+        A = a_st.t() if ta else a_st
+        B = b_st.t() if tb else b_st
+        C = torch.empty(M, N, device="cuda")
+        g = _GemmDesc(dtype=3 if bf16 else 0, M=M, N=N, K=K, a=a_st.data_ptr(), b=b_st.data_ptr(), c=C.data_ptr())
+        g.a_stride_m, g.a_stride_k = (1, M) if ta else (K, 1)
+        g.b_stride_k, g.b_stride_n = (1, K) if tb else (N, 1)
+        fn = (lambda A=A, B=B: torch.mm(A, B, out_dtype=torch.float32)) if bf16 else (lambda A=A, B=B: A @ B)
+        cases.append((name, fn, g, 2 * M * N * K, bf16, (a_st, b_st, C)))
+    best = {}
+    for _ in range(rounds):
+        for name, fn, g, fl, bf16, keep in cases:
+            tt, to = t_torch(fn), t_ours(g)
+            b0 = best.get(name, (math.inf, math.inf))
+            best[name] = (min(b0[0], tt), min(b0[1], to))
+    lines = ["# GEMM: ormi_hip_gemm against torch.matmul (hipBLASLt) on the same box", "",
+             f"Command (from the repo root): `{cmd}`", "",
+             f"torch {torch.__version__}; one process, the same device buffers, the two alternating per shape; "
+             f"HIP events over {n} back-to-back launches, best of {rounds} rounds. Operands N(0, 1/64) "
+             "(the C4 distribution); T = stored transposed (a view, as autograd passes it).", "",
+             "| GEMM | M x N x K | hipBLASLt us | TFLOP/s | ours us | TFLOP/s | ours / hipBLASLt time |",
+             "|---|---|---|---|---|---|---|"]
+    for name, fn, g, fl, bf16, keep in cases:
+        tt, to = best[name]
+        lines.append(f"| {name} | {g.M}x{g.N}x{g.K} | {tt:.1f} | {fl / tt / 1e6:.1f} | {to:.1f} | {fl / to / 1e6:.1f} | "
+                     f"{to / tt:.3f} |")
+    out_md.write_text("\n".join(lines) + "\n")
+    print(out_md.read_text())
+
+
 def bench_c5(ev: Events, steps: int) -> dict:
     from ormi_amd import Tensor
     from ormi_amd.ormi_backend import Node
@@ -593,7 +682,12 @@ def main():
                     help="summarize a rocprofv3 --pmc run of --only c4 into MFMA utilisation (no GPU needed)")
     ap.add_argument("--ceilings", action="store_true",
                     help="run the matrix-core ceiling probe (ormi_amd/lib/mfma_ceiling) and print its JSON lines")
+    ap.add_argument("--vendor-gemm", metavar="OUT_MD",
+                    help="time the C4/C5 GEMM shapes against torch.matmul (hipBLASLt) and write a markdown summary")
     args = ap.parse_args()
+    if args.vendor_gemm:
+        vendor_gemm(Path(args.vendor_gemm), "python3 bench.py --vendor-gemm profiles/gemm_vs_hipblaslt.md")
+        return
     if args.ceilings:
         # A child process, started before this process touches the GPU.
         import subprocess

@@ -353,7 +353,7 @@ void cfg32_dma(int id, int* bm, int* bn, int* bk) {
     if (id < 0 || id > 5) id = 1;
     *bm = 128;
     *bn = id == 2 ? 256 : 128;
-    *bk = id >= 4 ? 64 : 32;
+    *bk = id == 4 || id == 5 ? 64 : 32;
 }
 void run32_dma(int id, const GemmParams& p, dim3 grid, bool a_kc, bool b_kc, bool epi) {
     if (id < 0 || id > 5) id = 1;
