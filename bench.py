@@ -667,6 +667,70 @@ def mfma_report(pmc_dir: Path, out: Path, cmd: str) -> None:
     print(out.read_text())
 
 
+WAVE_COUNTERS = (
+    "SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_WAIT_ANY SQ_WAIT_INST_ANY SQ_WAIT_INST_LDS SQ_ACTIVE_INST_LDS "
+    "SQ_ACTIVE_INST_ANY GRBM_GUI_ACTIVE",
+    "SQ_LDS_IDX_ACTIVE SQ_LDS_DATA_FIFO_FULL SQ_LDS_CMD_FIFO_FULL SQ_LDS_ADDR_CONFLICT SQ_LDS_UNALIGNED_STALL "
+    "SQ_INSTS_LDS SQ_ACTIVE_INST_VALU GRBM_GUI_ACTIVE",
+)
+
+
+def wave_report(pmc_dirs, out: Path, cmd: str) -> None:
+    """Wave states, shader clock and LDS activity per GEMM kernel from the two
+    rocprofv3 --pmc passes of WAVE_COUNTERS over `--only c4` (one run each).
+    clock = GRBM_GUI_ACTIVE per XCC / kernel duration. SQ wave-cycle counters
+    count 4-cycle units (SQ_WAVE_CYCLES x 4 matches waves x active cycles), so
+    shares of SQ_WAVE_CYCLES are fractions of wave time and the LDS busy
+    fraction is SQ_LDS_IDX_ACTIVE x 4 / (CUs x active cycles per XCC)."""
+    agent = {}
+    per = collections.defaultdict(lambda: collections.defaultdict(list))
+    dur = collections.defaultdict(dict)
+    for d in pmc_dirs:
+        for f in sorted(Path(d).rglob("*agent_info.csv")):
+            for r in csv.DictReader(open(f, newline="")):
+                if r.get("Name", "").startswith("gfx"):
+                    agent = r
+        for f in sorted(Path(d).rglob("*counter_collection.csv")):
+            for r in csv.DictReader(open(f, newline="")):
+                name = r.get("Kernel_Name", "").strip()
+                if "gemm" not in name:
+                    continue
+                per[name][r["Counter_Name"].strip()].append(float(r["Counter_Value"]))
+                dur[name][(d, r["Dispatch_Id"])] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3
+    cus, xcc = int(agent.get("Cu_Count", 256)), int(agent.get("Num_Xcc", 8))
+
+    def mean(cs, c):
+        v = cs.get(c, [])
+        return sum(v) / len(v) if v else float("nan")
+
+    lines = [
+        "# GEMM wave states, shader clock and LDS activity (rocprofv3 counters)", "",
+        f"Command (from the repo root): `{cmd}`", "",
+        f"Device: {agent.get('Name', '?')}, {cus} CUs, {xcc} XCCs, datasheet engine clock "
+        f"{agent.get('Max_Engine_Clk_Fcompute', '?')} MHz. clock = GRBM_GUI_ACTIVE / XCCs / kernel duration. "
+        "Shares are of SQ_WAVE_CYCLES (wave time): s_waitcnt = SQ_WAIT_ANY, waiting to issue = SQ_WAIT_INST_ANY. "
+        "LDS busy = SQ_LDS_IDX_ACTIVE x 4 / (CUs x active cycles per XCC), taking the SQ counters' 4-cycle unit. "
+        "Counters serialize kernels; the duration is that of the counted dispatches. Kernels under 20 us "
+        "(the split-K finish pass) are left out: their GRBM count is mostly dispatch overhead.", "",
+        "| kernel | dispatches (both passes) | avg us | clock GHz | s_waitcnt share | waiting-to-issue share | LDS instructions / dispatch "
+        "| LDS busy | LDS FIFO-full (data / cmd) |",
+        "|---|---|---|---|---|---|---|---|---|",
+    ]
+    for name, cs in sorted(per.items()):
+        us = sum(dur[name].values()) / len(dur[name])
+        if us < 20.0:
+            continue  # a few-us kernel's GRBM count is mostly dispatch overhead
+        cyc = mean(cs, "GRBM_GUI_ACTIVE") / xcc
+        wc = mean(cs, "SQ_WAVE_CYCLES")
+        lines.append(
+            f"| `{name[:100]}` | {len(dur[name])} | {us:.1f} | {cyc / (us * 1e3):.2f} | {mean(cs, 'SQ_WAIT_ANY') / wc:.1%} "
+            f"| {mean(cs, 'SQ_WAIT_INST_ANY') / wc:.1%} | {mean(cs, 'SQ_INSTS_LDS'):.4g} "
+            f"| {mean(cs, 'SQ_LDS_IDX_ACTIVE') * 4 / (cus * cyc):.1%} "
+            f"| {mean(cs, 'SQ_LDS_DATA_FIFO_FULL'):.4g} / {mean(cs, 'SQ_LDS_CMD_FIFO_FULL'):.4g} |")
+    out.write_text("\n".join(lines) + "\n")
+    print(out.read_text())
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -680,6 +744,8 @@ def main():
                     help="summarize rocprofv3 --pmc runs into a traffic table (no GPU needed)")
     ap.add_argument("--mfma-report", nargs=2, metavar=("PMC_DIR", "OUT_MD"),
                     help="summarize a rocprofv3 --pmc run of --only c4 into MFMA utilisation (no GPU needed)")
+    ap.add_argument("--wave-report", nargs=3, metavar=("PMC_A", "PMC_B", "OUT_MD"),
+                    help="summarize the two rocprofv3 --pmc passes of WAVE_COUNTERS over --only c4 (no GPU needed)")
     ap.add_argument("--ceilings", action="store_true",
                     help="run the matrix-core ceiling probe (ormi_amd/lib/mfma_ceiling) and print its JSON lines")
     ap.add_argument("--vendor-gemm", metavar="OUT_MD",
@@ -701,6 +767,12 @@ def main():
                     "rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_MFMA SQ_LDS_BANK_CONFLICT GRBM_GUI_ACTIVE "
                     "-d gpurun_out/pmc_mfma -o run --output-format csv -- python3 bench.py --only c4 --steps 5 --warmup 1; "
                     "python3 bench.py --mfma-report gpurun_out/pmc_mfma profiles/gemm_mfma_util.md")
+        return
+    if args.wave_report:
+        wave_report(args.wave_report[:2], Path(args.wave_report[2]),
+                    " ; ".join(f"rocprofv3 --pmc {c} --kernel-trace -d gpurun_out/pmc_{k} -o run --output-format csv "
+                               "-- python3 bench.py --only c4 --steps 5 --warmup 1" for k, c in zip("ab", WAVE_COUNTERS))
+                    + " ; python3 bench.py --wave-report gpurun_out/pmc_a gpurun_out/pmc_b profiles/gemm_wave_states.md")
         return
     if args.pmc_report:
         pmc_report(Path(args.pmc_report[0]), Path(args.pmc_report[1]),
