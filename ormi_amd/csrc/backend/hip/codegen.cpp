@@ -62,6 +62,7 @@ namespace ormi::hip {
             x.map_blocks_per_cu = std::clamp(env_int("ORMI_MAP_BLOCKS_PER_CU", x.map_blocks_per_cu), 1, 1024);
             x.row_unroll = std::clamp(env_int("ORMI_ROW_UNROLL", x.row_unroll), 1, 8);
             x.col_waves = std::clamp(env_int("ORMI_COL_WAVES", x.col_waves), 1, 16);
+            x.col_cwaves = std::clamp(env_int("ORMI_COL_CWAVES", x.col_cwaves), 1, 16);
             x.map_nt_loads = env_int("ORMI_MAP_NT_LOADS", x.map_nt_loads) != 0;
             x.reduce_nt_loads = env_int("ORMI_REDUCE_NT_LOADS", x.reduce_nt_loads) != 0;
             x.map_nt_stores = env_int("ORMI_MAP_NT_STORES", x.map_nt_stores) != 0;
@@ -572,11 +573,19 @@ namespace ormi::hip {
         }
 
         // Emit the source of a kernel unless the cache already has it.
+        // layout: whatever else the emitted body depends on that the signature
+        // does not see (a column kernel's waves across columns, which follow
+        // the kept extent). The block size is part of the key too.
         template <typename EmitBody>
-        void resolve(Gen& g, const std::string& kind, int block, KernelLaunch& k, EmitBody emit) {
+        void resolve(Gen& g, const std::string& kind, int block, KernelLaunch& k, EmitBody emit,
+                     const std::string& layout = std::string()) {
             k.args = g.args.vals;
             k.block[0] = (uint32_t)block;
-            if (cache_lookup(signature(g, kind), k)) return;
+            std::string sig = signature(g, kind);
+            sig += "|b";
+            append_int(sig, block);
+            sig += layout;
+            if (cache_lookup(sig, k)) return;
             emit();
             k.source = g.finish(kind, block, k);
             cache_store(k);
@@ -977,16 +986,23 @@ namespace ormi::hip {
         }
 
         // ------------------------------------------------------------ column --
-        const int W = tn.col_waves;
-        const int block = 64 * W;
+        // A block is WC x WR waves: WC side by side across the kept columns
+        // (each lane V consecutive columns, so a row segment is WC KB at V = 4)
+        // and WR interleaved along the reduced rows. Fewer column waves when
+        // the kept extent is narrow.
         const long long IG = I / V;
-        const long long BI = (IG + 63) / 64;
+        int WC = 1;
+        while (WC * 2 <= tn.col_cwaves && WC * 64LL < IG) WC *= 2;
+        const int WR = std::max(1, tn.col_waves / WC);
+        const int W = WC * WR;
+        const int block = 64 * W;
+        const long long BI = (IG + 64LL * WC - 1) / (64LL * WC);
         long long P = 1;
         // Enough waves to keep HBM busy (about 16 per CU), each covering at
         // least 32 rows of its part.
         const long long target_waves = (long long)std::max(cu, 1) * 16;
         const long long waves1 = BI * O * W;
-        if (waves1 < target_waves) P = std::max(1LL, std::min((target_waves + waves1 - 1) / waves1, R / (32LL * W)));
+        if (waves1 < target_waves) P = std::max(1LL, std::min((target_waves + waves1 - 1) / waves1, R / (32LL * WR)));
         const long long CH = (R + P - 1) / P;
         P = R == 0 ? 1 : (R + CH - 1) / CH;
         g.choose_idx(O * I * P + R + 4LL * W * 4);
@@ -1005,7 +1021,8 @@ namespace ormi::hip {
         k.grid[0] = (uint32_t)std::max(1LL, BI * O * P);
         k.plan.kind = "column";
         k.plan.op = name;
-        for (auto [key, v] : {std::pair<const char*, long long>{"O", O}, {"R", R}, {"I", I}, {"vec", V}, {"waves", W}, {"parts", P},
+        for (auto [key, v] : {std::pair<const char*, long long>{"O", O}, {"R", R}, {"I", I}, {"vec", V}, {"waves", W},
+                              {"cwaves", WC}, {"parts", P},
                               {"idx", g.idx32 ? 32 : 64}})
             k.plan.add(key, v);
         resolve(g, std::string("col") + name, block, k, [&] {
@@ -1013,13 +1030,14 @@ namespace ormi::hip {
             std::ostringstream& b = g.body();
             const int CU = 4;  // rows in flight per wave
             g.hoist_scalars(b, "  ");
-            b << "  __shared__ float sv[" << W << "][64][" << V << "];\n";
-            if (!is_sum) b << "  __shared__ int si[" << W << "][64][" << V << "];\n";
-            b << "  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;\n";
+            b << "  __shared__ float sv[" << WR << "][" << 64 * WC << "][" << V << "];\n";
+            if (!is_sum) b << "  __shared__ int si[" << WR << "][" << 64 * WC << "][" << V << "];\n";
+            b << "  const int lane = threadIdx.x & 63, wc = (threadIdx.x >> 6) % " << WC << ", w = (threadIdx.x >> 6) / " << WC
+              << ", cl = wc * 64 + lane;\n";
             b << "  const " << t << " bid = (" << t << ")blockIdx.x;\n";
             b << "  const " << t << " bi_ = bid % (" << t << ")NBI; const " << t << " rest = bid / (" << t << ")NBI;\n";
             b << "  const " << t << " o = rest % (" << t << ")NO, p = rest / (" << t << ")NO;\n";
-            b << "  const " << t << " ig = bi_ * 64 + lane;\n";
+            b << "  const " << t << " ig = bi_ * " << 64 * WC << " + cl;\n";
             b << "  const bool active = ig < (" << t << ")NIG;\n";
             b << "  const " << t << " igc = active ? ig : (" << t << ")NIG - 1;\n";
             std::vector<int> oi = od;
@@ -1040,7 +1058,7 @@ namespace ormi::hip {
             auto emit_cstep = [&](int UNR, const std::string& ind) {
                 g.declare_leaf_regs(b, ind, UNR);
                 b << ind << "#pragma unroll\n" << ind << "for (int u = 0; u < " << UNR << "; ++u) {\n";
-                b << ind << "  const " << t << " ru = r + u * " << W << ";\n";
+                b << ind << "  const " << t << " ru = r + u * " << WR << ";\n";
                 g.declare_coords(b, ind + "  ", rd);
                 g.decompose(b, ind + "  ", "ru", rd);
                 for (size_t L = 0; L < expr.leaves.size(); ++L) {
@@ -1053,38 +1071,38 @@ namespace ormi::hip {
                 b << ind << "#pragma unroll\n" << ind << "  for (int k = 0; k < " << V << "; ++k) {\n";
                 const std::string v = g.eval(b, ind + "    ", "u", "k");
                 if (is_sum) b << ind << "    acc[k] += " << v << ";\n";
-                else b << ind << "    ormi_am_step(bv[k], bx[k], " << v << ", (int)(r + u * " << W << "));\n";
+                else b << ind << "    ormi_am_step(bv[k], bx[k], " << v << ", (int)(r + u * " << WR << "));\n";
                 b << ind << "  }\n" << ind << "}\n";
             };
             b << "  " << t << " r = r0 + w;\n";
             b << "  if (active) {\n";
-            b << "    for (; r + " << W * (CU - 1) << " < r1; r += " << W * CU << ") {\n";
+            b << "    for (; r + " << WR * (CU - 1) << " < r1; r += " << WR * CU << ") {\n";
             emit_cstep(CU, "      ");
             b << "    }\n";
-            b << "    for (; r < r1; r += " << W << ") {\n";
+            b << "    for (; r < r1; r += " << WR << ") {\n";
             emit_cstep(1, "      ");
             b << "    }\n  }\n";
             if (!is_sum)  // a non-empty all -inf chain: its first element r0 + w (see the row kernel)
                 b << "#pragma unroll\n  for (int k = 0; k < " << V << "; ++k) if (bx[k] == 0x7fffffff && r0 + w < r1) bx[k] = (int)(r0 + w);\n";
             b << "#pragma unroll\n  for (int k = 0; k < " << V << "; ++k) {";
-            if (is_sum) b << " sv[w][lane][k] = acc[k]; }\n";
-            else b << " sv[w][lane][k] = bv[k]; si[w][lane][k] = bx[k]; }\n";
+            if (is_sum) b << " sv[w][cl][k] = acc[k]; }\n";
+            else b << " sv[w][cl][k] = bv[k]; si[w][cl][k] = bx[k]; }\n";
             b << "  __syncthreads();\n";
             b << "  if (w == 0 && active) {\n";
             b << "    const " << t << " e0 = (p * (" << t << ")NO + o) * (" << t << ")NI + ig * " << V << ";\n";
             b << "#pragma unroll\n    for (int k = 0; k < " << V << "; ++k) {\n";
             if (is_sum) {
-                b << "      float s = sv[0][lane][k];\n";
-                b << "#pragma unroll\n      for (int q = 1; q < " << W << "; ++q) s += sv[q][lane][k];\n";
+                b << "      float s = sv[0][cl][k];\n";
+                b << "#pragma unroll\n      for (int q = 1; q < " << WR << "; ++q) s += sv[q][cl][k];\n";
                 b << "      ((float*)outp)[e0 + k] = s;\n";
             } else {
-                b << "      float v = sv[0][lane][k]; int x = si[0][lane][k];\n";
-                b << "#pragma unroll\n      for (int q = 1; q < " << W << "; ++q) ormi_am_take(v, x, sv[q][lane][k], si[q][lane][k]);\n";
+                b << "      float v = sv[0][cl][k]; int x = si[0][cl][k];\n";
+                b << "#pragma unroll\n      for (int q = 1; q < " << WR << "; ++q) ormi_am_take(v, x, sv[q][cl][k], si[q][cl][k]);\n";
                 if (is_arg) b << "      if (outi == nullptr) ((long long*)outp)[e0 + k] = (long long)x; else { ((float*)outp)[e0 + k] = v; outi[e0 + k] = x; }\n";
                 else b << "      ((float*)outp)[e0 + k] = v; if (outi != nullptr) outi[e0 + k] = x;\n";
             }
             b << "    }\n  }\n";
-        });
+        }, "|cw" + std::to_string(WC));
         if (plan.two_pass) {
             // Partials are laid out [P][O*I]; the second pass walks them in part order.
             plan.workspace_bytes = (size_t)(P * O * I) * (sizeof(float) + sizeof(int));
@@ -1102,12 +1120,22 @@ namespace ormi::hip {
                 std::ostringstream& sb = g2.body();
                 sb << "  const long long e = (long long)blockIdx.x * 256 + threadIdx.x;\n";
                 sb << "  if (e >= NE) return;\n";
+                // Parts are combined in part order; their loads are issued FIN at a
+                // time (one round trip per FIN parts, not one per part). 16 measured
+                // best: 64 loads in flight with 64-thread blocks was slower.
+                constexpr int FIN = 16;
                 if (is_sum) {
-                    sb << "  float s = 0.0f;\n  for (long long q = 0; q < NP; ++q) s += pvals[q * NE + e];\n";
+                    sb << "  float s = 0.0f;\n  for (long long q0 = 0; q0 < NP; q0 += " << FIN << ") {\n";
+                    sb << "    float v[" << FIN << "];\n";
+                    sb << "#pragma unroll\n    for (int j = 0; j < " << FIN << "; ++j) v[j] = q0 + j < NP ? pvals[(q0 + j) * NE + e] : 0.0f;\n";
+                    sb << "#pragma unroll\n    for (int j = 0; j < " << FIN << "; ++j) if (q0 + j < NP) s += v[j];\n  }\n";
                     sb << "  ((float*)outp)[e] = s;\n";
                 } else {
                     sb << "  float bv = -__builtin_inff(); int bi = 0x7fffffff;\n";
-                    sb << "  for (long long q = 0; q < NP; ++q) ormi_am_take(bv, bi, pvals[q * NE + e], pidx[q * NE + e]);\n";
+                    sb << "  for (long long q0 = 0; q0 < NP; q0 += " << FIN << ") {\n";
+                    sb << "    float v[" << FIN << "]; int x[" << FIN << "];\n";
+                    sb << "#pragma unroll\n    for (int j = 0; j < " << FIN << "; ++j) if (q0 + j < NP) { v[j] = pvals[(q0 + j) * NE + e]; x[j] = pidx[(q0 + j) * NE + e]; }\n";
+                    sb << "#pragma unroll\n    for (int j = 0; j < " << FIN << "; ++j) if (q0 + j < NP) ormi_am_take(bv, bi, v[j], x[j]);\n  }\n";
                     if (is_arg) sb << "  ((long long*)outp)[e] = (long long)bi;\n";
                     else sb << "  ((float*)outp)[e] = bv;\n";
                 }

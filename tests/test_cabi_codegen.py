@@ -317,3 +317,20 @@ def test_map_and_reduce_plans_past_2_31_use_64_bit_indices(ob, cpu):
     assert "idx=64" in plan and "off32=0" in plan
     small = ob._plan_kernel((Tensor(np.zeros((4, 1), np.float32), "cpu") + a)._node)["plan"]
     assert "idx=32" in small and "off32=1" in small
+
+
+def test_column_kernels_keyed_by_column_waves(ob, cpu, cabi):
+    """A column reduction's waves across columns follow the kept extent (1 for 6
+    columns, 2 for 70, 4 for 2048), and the emitted body depends on it, so the
+    kernel cache keys it: a narrow plan compiled first must not serve a wider one
+    whose grid assumes more columns per block."""
+    seen = {}
+    for shape in [(1 << 16, 6), (1003, 70), (1024, 2048)]:
+        for red in ("sum", "argmax"):
+            d = ob._plan_kernel(getattr(ob, red)(_cpu(np.zeros(shape))._node, [0], False))
+            cw = int(d["plan"].split("cwaves=")[1].split()[0])
+            assert f"bi_ * {64 * cw} + cl" in d["source"], (shape, red, d["plan"])
+            seen.setdefault(red, set()).add(d["name"])
+            rc, _ = _compile_only(cabi, d["source"], ob._rtc_options())
+            assert rc == ORMI_HIP_OK, (shape, red, cabi.ormi_hip_last_error())
+    assert all(len(names) == 3 for names in seen.values()), seen
