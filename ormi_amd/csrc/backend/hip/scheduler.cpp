@@ -360,6 +360,59 @@ namespace ormi::hip {
         return true;
     }
 
+    // Forward activations of GEMM products, indexed once per top-level
+    // realize. Autograd can reach a product p first through f'(p), as the D of
+    // a backward epilogue, when a weight update is realized before the loss;
+    // p would then run as a plain GEMM and f(p) as a map over it. A product the
+    // scheduler must compute runs instead as the UNARY epilogue of an
+    // activation f(p) the same graph holds, which stores p and f(p) from one
+    // GEMM (identical values either way).
+    struct RealizeScope {
+        std::vector<NodePtr> roots;
+        bool indexed = false;
+        std::unordered_map<Node*, NodePtr> act;  // product -> f(product)
+    };
+    static thread_local RealizeScope* t_scope = nullptr;
+    // The outermost realize owns the scope; nested realizes share it.
+    struct ScopeGuard {
+        RealizeScope scope;
+        bool owner;
+        explicit ScopeGuard(const std::vector<NodePtr>& roots) : owner(t_scope == nullptr) {
+            if (!owner) return;
+            scope.roots = roots;
+            t_scope = &scope;
+        }
+        ~ScopeGuard() {
+            if (owner) t_scope = nullptr;
+        }
+        ScopeGuard(const ScopeGuard&) = delete;
+        ScopeGuard& operator=(const ScopeGuard&) = delete;
+    };
+
+    static NodePtr activation_consumer(const NodePtr& p) {
+        if (!t_scope || !epilogue_enabled()) return nullptr;
+        RealizeScope& sc = *t_scope;
+        if (!sc.indexed) {
+            // Walk the unrealized part of the graph below the roots once.
+            sc.indexed = true;
+            std::vector<NodePtr> stack;
+            std::unordered_set<Node*> seen;
+            for (const auto& r : sc.roots)
+                if (r && !r->is_realized() && seen.insert(r.get()).second) stack.push_back(r);
+            while (!stack.empty()) {
+                const NodePtr n = stack.back();
+                stack.pop_back();
+                if (ops::op_arity(n->op) == 1 && unary_fn(n->op) >= 0 && fusible_root(*n) && n->dtype == DType::Float32 &&
+                    is_open_product(n->parents[0], n->view.shape))
+                    sc.act.emplace(n->parents[0].get(), n);
+                for (const auto& q : n->parents)
+                    if (!q->is_realized() && seen.insert(q.get()).second) stack.push_back(q);
+            }
+        }
+        const auto it = sc.act.find(p.get());
+        return it == sc.act.end() || it->second->is_realized() ? nullptr : it->second;
+    }
+
     // An element-wise region: a matched GEMM epilogue, else one fused kernel.
     static void run_map(const NodePtr& root) {
         {
@@ -409,6 +462,13 @@ namespace ormi::hip {
             run_map(n);
             return;
         }
+        if (n->op == OpEnum::MATMUL) {
+            // Its operands are realized, and so are the activation's (the same).
+            if (const NodePtr a = activation_consumer(n)) {
+                EpilogueMatch m;
+                if (match_epilogue(a, m) && m.g == n && run_gemm_epilogue(a, m) && n->is_realized()) return;
+            }
+        }
         if (try_execute_graph_break(n)) return;
         if (n->op == OpEnum::LEAF || n->op == OpEnum::CONST) throw std::runtime_error("HIP scheduler: leaf without a buffer.");
         throw std::runtime_error(std::string("HIP scheduler: no lowering for op ") + ops::op_name(n->op));
@@ -420,6 +480,7 @@ namespace ormi::hip {
     // dependencies pushed for a node still cover it when it runs.
     void realize(const NodePtr& root) {
         if (!root || root->is_realized()) return;
+        ScopeGuard guard({root});
         std::vector<NodePtr> stack{root};
         std::unordered_set<Node*> expanded;
         while (!stack.empty()) {
@@ -443,6 +504,7 @@ namespace ormi::hip {
     }
 
     void realize_group(const std::vector<NodePtr>& roots) {
+        ScopeGuard guard(roots);
         // Element-wise roots with float results that can share one kernel,
         // grouped by shape in first-seen order; everything else realizes alone.
         std::vector<std::pair<std::vector<int>, std::vector<NodePtr>>> groups;

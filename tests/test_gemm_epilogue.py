@@ -213,6 +213,28 @@ def test_mlp_step_fused_equals_unfused(ob, hip, cpu):
         np.testing.assert_allclose(f, r, rtol=1e-4, atol=1e-5)
 
 
+def test_mlp_step_updates_first_fuses_forward_gelu(ob, hip):
+    """Realizing the weight updates before the loss (as a training loop that
+    only reads the new weights does) reaches each hidden product first through
+    the backward's gelu'(p). The product still runs as its forward GELU's GEMM
+    epilogue, storing p and gelu(p) together: 2 GELU + 2 dGELU + 3 SGD epilogues,
+    bit-exact with the unfused step."""
+    rng = np.random.default_rng(5)
+    dims = [256, 512, 512, 256]
+    X = rng.normal(0, 1, (128, dims[0])).astype(np.float32)
+    Yt = rng.normal(0, 1, (128, dims[-1])).astype(np.float32)
+    Ws = [rng.uniform(-math.sqrt(6 / i), math.sqrt(6 / i), (i, o)).astype(np.float32) for i, o in zip(dims, dims[1:])]
+
+    def updates_first():
+        out = mlp_step(hip, X, Yt, Ws)
+        return out[1:] + out[:1]
+
+    fused, plain, used = fused_and_plain(ob, updates_first)
+    assert used >= 7, used
+    for f, p in zip(fused, plain):
+        assert bits_equal(f, p)
+
+
 # ------------------------------------------------------------- the C ABI --
 class Desc(ctypes.Structure):
     _fields_ = [("dtype", ctypes.c_int), ("M", ctypes.c_int), ("N", ctypes.c_int), ("K", ctypes.c_int),
