@@ -377,9 +377,10 @@ namespace ormi::hip {
     struct ScopeGuard {
         RealizeScope scope;
         bool owner;
-        explicit ScopeGuard(const std::vector<NodePtr>& roots) : owner(t_scope == nullptr) {
+        // Roots are copied only by the owner: nested realizes allocate nothing.
+        ScopeGuard(const NodePtr* roots, size_t n) : owner(t_scope == nullptr) {
             if (!owner) return;
-            scope.roots = roots;
+            scope.roots.assign(roots, roots + n);
             t_scope = &scope;
         }
         ~ScopeGuard() {
@@ -480,7 +481,7 @@ namespace ormi::hip {
     // dependencies pushed for a node still cover it when it runs.
     void realize(const NodePtr& root) {
         if (!root || root->is_realized()) return;
-        ScopeGuard guard({root});
+        ScopeGuard guard(&root, 1);
         std::vector<NodePtr> stack{root};
         std::unordered_set<Node*> expanded;
         while (!stack.empty()) {
@@ -504,7 +505,7 @@ namespace ormi::hip {
     }
 
     void realize_group(const std::vector<NodePtr>& roots) {
-        ScopeGuard guard(roots);
+        ScopeGuard guard(roots.data(), roots.size());
         // Element-wise roots with float results that can share one kernel,
         // grouped by shape in first-seen order; everything else realizes alone.
         std::vector<std::pair<std::vector<int>, std::vector<NodePtr>>> groups;
