@@ -118,8 +118,8 @@ namespace ormi::hip {
         int map_unroll = 2;        // VEC groups per thread per iteration (map)
         int map_blocks_per_cu = 64;
         int row_unroll = 4;        // VEC groups per lane per iteration (row reduce)
-        int col_waves = 8;         // waves per block (column reduce)
-        int col_cwaves = 4;        // of those, waves side by side across the kept columns
+        int col_waves = 16;        // waves per block (column reduce)
+        int col_cwaves = 8;        // of those, waves side by side across the kept columns
         bool map_nt_loads = false;    // non-temporal hint on a map's operand loads
         bool map_nt_stores = true;    // non-temporal hint on a map's output stores
         bool reduce_nt_loads = true;  // non-temporal hint on a reduction's loads
