@@ -548,6 +548,7 @@ def bench_c5(ev: Events, steps: int) -> dict:
         for w in ws:
             u = (w - w.grad * 1e-3).realize()
             out.append(Tensor(_node=Node(u._node.data, True, u._node.device), device="hip"))
+        loss.realize()  # the step reports its loss: the MSE reduction is part of the timed work
         # backward stored a gradient on every node and gradient graphs point at
         # forward nodes (reference csrc/core/autograd.cpp:24-47): clearing them
         # (zero_grad_graph, :49-58) lets the step's buffers return to the pool.
@@ -746,22 +747,12 @@ def main():
                     help="summarize a rocprofv3 --pmc run of --only c4 into MFMA utilisation (no GPU needed)")
     ap.add_argument("--wave-report", nargs=3, metavar=("PMC_A", "PMC_B", "OUT_MD"),
                     help="summarize the two rocprofv3 --pmc passes of WAVE_COUNTERS over --only c4 (no GPU needed)")
-    ap.add_argument("--ceilings", action="store_true",
-                    help="run the matrix-core ceiling probe (ormi_amd/lib/mfma_ceiling) and print its JSON lines")
     ap.add_argument("--vendor-gemm", metavar="OUT_MD",
                     help="time the C4/C5 GEMM shapes against torch.matmul (hipBLASLt) and write a markdown summary")
     args = ap.parse_args()
     if args.vendor_gemm:
         vendor_gemm(Path(args.vendor_gemm), "python3 bench.py --vendor-gemm profiles/gemm_vs_hipblaslt.md")
         return
-    if args.ceilings:
-        # A child process, started before this process touches the GPU.
-        import subprocess
-
-        probe = ROOT / "ormi_amd" / "lib" / "mfma_ceiling"
-        if not probe.exists():
-            raise SystemExit(f"bench.py: {probe} is not built (run __graft_entry__.build())")
-        sys.exit(subprocess.run([str(probe)]).returncode)
     if args.mfma_report:
         mfma_report(Path(args.mfma_report[0]), Path(args.mfma_report[1]),
                     "rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_MFMA SQ_LDS_BANK_CONFLICT GRBM_GUI_ACTIVE "

@@ -53,9 +53,6 @@ ORACLE_SOURCES = sorted((ORACLE / "cpu_backend").glob("*.cpp"))
 EXT_SUFFIX = sysconfig.get_config_var("EXT_SUFFIX") or ".so"
 MODULE_PATH = PKG / f"ormi_backend{EXT_SUFFIX}"
 HIP_LIB = LIBDIR / "libormi_hip.so"
-# Matrix-core ceiling probe for the roofline (python3 bench.py --ceilings).
-CEILING_SRC = CSRC / "bench" / "mfma_ceiling.hip"
-CEILING_BIN = LIBDIR / "mfma_ceiling"
 CORE_LIB = LIBDIR / "libormi_core.so"
 ORACLE_LIB = ORACLE_OUT / "libormi_cpu_oracle.so"
 
@@ -78,10 +75,28 @@ def _gen_device_text() -> None:
     (GENDIR / "ormi_device_text.inc").write_text(f'R"{delim}({text}){delim}"\n')
 
 
+_INCREMENTAL = False
+
+
+def _newest_header() -> float:
+    heads = [p for d in (CSRC, INCLUDE) for p in d.rglob("*.h")]
+    return max((p.stat().st_mtime for p in heads), default=0.0)
+
+
+def _fresh(src: Path, obj: Path) -> bool:
+    """Incremental builds only: obj is newer than its source and every header."""
+    if not _INCREMENTAL or not obj.exists():
+        return False
+    t = obj.stat().st_mtime
+    return t > src.stat().st_mtime and t > _newest_header()
+
+
 def _compile_cxx(src: Path, includes: list[Path], extra: list[str] | None = None) -> Path:
     rel = src.relative_to(ROOT)
     obj = OBJDIR / "obj" / (str(rel).replace(os.sep, "__") + ".o")
     obj.parent.mkdir(parents=True, exist_ok=True)
+    if _fresh(src, obj):
+        return obj
     cmd = ["g++", *CXX_FLAGS, *(extra or []), *[f"-I{p}" for p in includes], "-c", str(src), "-o", str(obj)]
     _run(cmd)
     return obj
@@ -90,11 +105,17 @@ def _compile_cxx(src: Path, includes: list[Path], extra: list[str] | None = None
 def _compile_hip(src: Path) -> Path:
     obj = OBJDIR / "obj" / (str(src.relative_to(ROOT)).replace(os.sep, "__") + ".o")
     obj.parent.mkdir(parents=True, exist_ok=True)
+    if _fresh(src, obj):
+        return obj
     _run([HIPCC, *HIP_FLAGS, f"-I{INCLUDE}", f"-I{CSRC / 'hip'}", "-c", str(src), "-o", str(obj)])
     return obj
 
 
-def build(verbose: bool = False) -> None:
+def build(verbose: bool = False, incremental: bool = False) -> None:
+    """Compile every part. incremental=True (python -m ormi_amd._build -i) skips
+    objects newer than their source and every header; the default recompiles all."""
+    global _INCREMENTAL
+    _INCREMENTAL = incremental
     if verbose:
         os.environ["ORMI_BUILD_VERBOSE"] = "1"
     LIBDIR.mkdir(parents=True, exist_ok=True)
@@ -112,12 +133,10 @@ def build(verbose: bool = False) -> None:
         # One object per HIP translation unit, compiled in parallel (the GEMM
         # units take the longest), then linked into the shared library.
         hip_objs = [ex.submit(_compile_hip, s) for s in HIP_SOURCES]
-        ceiling = ex.submit(_run, [HIPCC, *HIP_FLAGS, str(CEILING_SRC), "-o", str(CEILING_BIN)])
         core_objs = [ex.submit(_compile_cxx, s, core_inc) for s in CORE_SOURCES]
         bind_objs = [ex.submit(_compile_cxx, s, core_inc + py_inc) for s in BINDING_SOURCES]
         oracle_objs = [ex.submit(_compile_cxx, s, core_inc) for s in ORACLE_SOURCES]
         hip = [f.result() for f in hip_objs]
-        ceiling.result()
         core = [f.result() for f in core_objs]
         binds = [f.result() for f in bind_objs]
         oracle = [f.result() for f in oracle_objs]
@@ -137,5 +156,5 @@ def built() -> bool:
 
 
 if __name__ == "__main__":
-    build(verbose="-v" in sys.argv)
+    build(verbose="-v" in sys.argv, incremental="-i" in sys.argv)
     print("built:", HIP_LIB, CORE_LIB, MODULE_PATH, ORACLE_LIB)

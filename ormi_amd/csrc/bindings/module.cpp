@@ -74,7 +74,7 @@ namespace {
     std::shared_ptr<Buffer> numpy_to_buffer(py::array array, DeviceEnum dev, std::optional<std::string> dtype_name) {
         const DType dt = dtype_name ? dtype_from_name(*dtype_name) : DType::Float32;
         std::vector<int> shape;
-        for (py::ssize_t i = 0; i < array.ndim(); ++i) shape.push_back((int)array.shape(i));
+        for (py::ssize_t i = 0; i < array.ndim(); ++i) shape.push_back(checked_extent(array.shape(i), "Array dimension"));
         const size_t n = (size_t)array.size();
         std::vector<unsigned char> host;
         const void* src = nullptr;

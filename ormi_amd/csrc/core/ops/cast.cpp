@@ -13,6 +13,11 @@ namespace ormi {
     namespace ops {
         NodePtr cast(NodePtr x, DType dtype) {
             if (dtype == DType::Bool || dtype == DType::Int32) throw std::runtime_error("CAST supports float32, bfloat16, float16 and int64 targets.");
+            // A cast to the operand's own type is the operand: nodes are never
+            // written after they are realized, so aliasing is invisible, and an
+            // int64 value above 2^24 must not round through the fp32 registers
+            // the element-wise kernels compute in.
+            if (x->dtype == dtype) return x;
             return std::make_shared<Node>(OpEnum::CAST, NodeVec{x}, x->device, CastAttrs{dtype});
         }
     }

@@ -85,7 +85,7 @@ namespace ormi {
             }
             long long s = old_strides[o_end - 1];
             for (size_t i = n_end; i-- > n;) {
-                strides[i] = (int)s;
+                strides[i] = checked_extent(s, "RESHAPE stride");
                 s *= out[i];
             }
             o = o_end;

@@ -1,5 +1,7 @@
 #include <stdexcept>
 #include <algorithm>
+#include <climits>
+#include <string>
 #include "core/shape.h"
 #include "core/node.h"
 
@@ -13,9 +15,22 @@ namespace ormi {
         return true;
     }
 
+    int checked_extent(long long v, const char* what) {
+        if (v > INT_MAX || v < INT_MIN)
+            throw std::runtime_error(std::string(what) + " " + std::to_string(v) +
+                                     " exceeds the 32-bit range of TensorView (shapes and strides are int).");
+        return (int)v;
+    }
+
+    // Strides are computed in 64 bits: a trailing extent product of 2^31 or more
+    // (2 x 32768 x 65536, say) is an error, never a wrapped stride.
     std::vector<int> calc_contiguous_strides(const std::vector<int>& shape) {
         std::vector<int> strides(shape.size(), 1);
-        for (int i = (int)shape.size() - 2; i >= 0; --i) strides[i] = strides[i + 1] * shape[i + 1];
+        long long s = 1;
+        for (int i = (int)shape.size() - 2; i >= 0; --i) {
+            s *= shape[i + 1];
+            strides[i] = checked_extent(s, "Contiguous stride");
+        }
         return strides;
     }
 

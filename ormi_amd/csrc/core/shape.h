@@ -15,6 +15,8 @@ namespace ormi {
         bool is_contiguous() const;
     };
 
+    // v as an int, or a std::runtime_error naming `what` when it does not fit.
+    int checked_extent(long long v, const char* what);
     std::vector<int> calc_contiguous_strides(const std::vector<int>& shape);
     std::vector<int> broadcast_shapes(const std::vector<int>& a, const std::vector<int>& b);
     std::vector<int> infer_shape(ops::OpEnum op, const std::vector<std::shared_ptr<Node>>& parents, const OpAttributes& attrs);

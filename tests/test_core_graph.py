@@ -187,3 +187,20 @@ def test_unknown_device_errors(ob):
     with pytest.raises(RuntimeError, match="no CUDA backend"):
         ob.numpy_to_buffer(np.zeros(2, np.float32), ob.DeviceEnum.CUDA)
 
+
+
+def test_strides_past_int32_raise(ob, cpu):
+    """Shapes and strides are int (reference csrc/core/shape.h:11-16). A node whose
+    contiguous stride would reach 2^31 (a 2 x 32768 x 65536 map) raises instead of
+    wrapping; views and shapes below the limit are unaffected."""
+    from ormi_amd import Tensor
+
+    one = Tensor(np.ones((1, 1, 1), np.float32), "cpu")
+    big = one.expand((2, 32768, 65536))          # view: strides (0, 0, 0), fine
+    assert big.shape == (2, 32768, 65536)
+    with pytest.raises(RuntimeError, match="exceeds the 32-bit range"):
+        big * 2.0                                # its output would need stride 2^31
+    with pytest.raises(RuntimeError, match="exceeds the 32-bit range"):
+        (one.expand((2, 32768, 65536)) * Tensor(np.ones((65536,), np.float32), "cpu")).sum(0)
+    ok = one.reshape((1, 1)).expand((65535, 32768)) * 1.0  # 2-D, stride 32768: below the limit
+    assert list(ok._node.view.strides) == [32768, 1]
