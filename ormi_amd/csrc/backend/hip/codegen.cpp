@@ -592,6 +592,13 @@ namespace ormi::hip {
         }
     }  // namespace
 
+    std::string kernel_source(const KernelLaunch& k) {
+        if (!k.source.empty() || k.key.empty()) return k.source;
+        std::lock_guard<std::mutex> lock(cache_mu());
+        auto it = kernel_cache().find(k.key);
+        return it == kernel_cache().end() ? std::string() : it->second.source;
+    }
+
     std::string PlanInfo::text() const {
         std::string s = kind;
         if (op) {

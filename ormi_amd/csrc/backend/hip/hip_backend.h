@@ -149,6 +149,10 @@ namespace ormi::hip {
                            void* out, int compute_units);
     void bind_workspace(ReducePlan& plan, void* workspace);
 
+    // Source text of a planned kernel: a plan that hit the kernel cache after
+    // its kernel was compiled carries only the handle, and this returns the
+    // text the cache kept (diagnostics and compile-only checks).
+    std::string kernel_source(const KernelLaunch& k);
     // hipRTC options every generated kernel is compiled with.
     const std::vector<std::string>& rtc_options();
     // Compile (cached) and launch.

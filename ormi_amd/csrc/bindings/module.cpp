@@ -159,7 +159,7 @@ namespace {
             rp = hip::plan_reduce(e, x->view.shape, a.axes, op, (void*)(uintptr_t)0x100000, cu);
             k = rp.first;
             d["two_pass"] = rp.two_pass;
-            d["second_source"] = rp.second.source;
+            d["second_source"] = hip::kernel_source(rp.second);
             d["second_name"] = rp.second.name;
             d["workspace_bytes"] = rp.workspace_bytes;
         } else {
@@ -167,7 +167,7 @@ namespace {
             k = hip::plan_map(e, root->view.shape, (void*)(uintptr_t)0x100000, root->dtype, cu);
             d["two_pass"] = false;
         }
-        d["source"] = k.source;
+        d["source"] = hip::kernel_source(k);
         d["name"] = k.name;
         d["plan"] = k.plan.text();
         d["grid"] = std::vector<uint32_t>{k.grid[0], k.grid[1], k.grid[2]};
@@ -186,7 +186,7 @@ namespace {
         for (const auto& r : roots) dts.push_back(r->dtype);
         const hip::KernelLaunch k = hip::plan_map_multi(e, shape, outs, dts, 256);
         py::dict d;
-        d["source"] = k.source;
+        d["source"] = hip::kernel_source(k);
         d["name"] = k.name;
         d["plan"] = k.plan.text();
         d["num_leaves"] = e.leaves.size();
