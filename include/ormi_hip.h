@@ -189,6 +189,21 @@ typedef struct ormi_gemm_epilogue {
 } ormi_gemm_epilogue;
 int ormi_hip_gemm_ex(const ormi_gemm_desc* desc, const ormi_gemm_epilogue* epi);
 
+/* ormi_hip_gemm_ex without any device allocation. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same kernels, same results bit for bit; the split-K partials and the finish
+ * pass's input live in a static device array of ORMI_GEMM_NOALLOC_SCRATCH_BYTES
+ * that the library's code object carries (held by each GPU until the process
+ * ends) instead of the grown-on-demand workspace. A shape whose workspace
+ * (batch * M * N * splits * 4 bytes, when the K split or the epilogue needs one)
+ * exceeds it returns ORMI_HIP_ERR_INVALID and launches nothing. All calls in a
+ * process share the array: the library enqueues each call's kernels under one
+ * lock on one stream, so calls through this ABI never overlap; work the caller
+ * captures from them and replays concurrently on other streams would race. */
+#define ORMI_GEMM_NOALLOC_SCRATCH_BYTES (32u << 20)
+int ormi_hip_gemm_ex_noalloc(const ormi_gemm_desc* desc, const ormi_gemm_epilogue* epi);
+
 /* ---------------------------------------------------------------- timing --
  * HIP events on the library's stream, for measuring kernel time from
  * outside (benchmarks). */

@@ -959,13 +959,15 @@ static void run_dma(int id, const GemmParams& p, dim3 grid, bool a_kc, bool b_kc
 }
 
 // Split-K workspace, grown on demand and kept; every use is ordered on the
-// null stream, so reuse by the next call is safe.
+// null stream, so reuse by the next call is safe. g_ws_mu is held from the
+// moment a call takes the workspace until its kernels are enqueued, so another
+// host thread can neither free it nor interleave its own launches that use it.
 static std::mutex g_ws_mu;
 static void* g_ws = nullptr;
 static size_t g_ws_bytes = 0;
 
-static int workspace(size_t bytes, void** out) {
-    std::lock_guard<std::mutex> lock(g_ws_mu);
+// Caller holds g_ws_mu.
+static int workspace_locked(size_t bytes, void** out) {
     if (bytes > g_ws_bytes) {
         if (g_ws) {
             hipError_t e = hipDeviceSynchronize();
@@ -982,13 +984,52 @@ static int workspace(size_t bytes, void** out) {
     return ORMI_HIP_OK;
 }
 
+// Workspace of the allocation-free entry (ormi_hip_gemm_ex_noalloc): split-K
+// partials and the input of the finish pass live in this array, which the
+// code object carries, so no call allocates. The device holds it for the life
+// of the process. In host code `scratch` names a host-side stand-in, not device
+// memory: kernels and copies get g_scratch, its device address, which
+// gemm_scratch_setup resolves once, with the bound device current. Every call
+// reuses the same bytes (a call's kernels overwrite everything the next one
+// reads: each split's kernel stores its whole partial slice).
+static __device__ __align__(256) unsigned char scratch[ORMI_GEMM_NOALLOC_SCRATCH_BYTES];
+static void* g_scratch = nullptr;
+
+static int scratch_locked(size_t bytes, void** out) {
+    if (bytes > ORMI_GEMM_NOALLOC_SCRATCH_BYTES)
+        return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_gemm_ex_noalloc: this shape needs " + std::to_string(bytes) +
+                                              " bytes of workspace; the allocation-free entry holds at most " +
+                                              std::to_string((size_t)ORMI_GEMM_NOALLOC_SCRATCH_BYTES) +
+                                              " (use ormi_hip_gemm_ex)");
+    if (!g_scratch) return fail(ORMI_HIP_ERR_RUNTIME, "ormi_hip_gemm_ex_noalloc: scratch address not resolved");
+    *out = g_scratch;
+    return ORMI_HIP_OK;
+}
+
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int gemm_scratch_setup() {
+    const hipError_t e = hipGetSymbolAddress(&g_scratch, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) {
+        g_scratch = nullptr;
+        return fail(ORMI_HIP_ERR_RUNTIME, std::string("gemm scratch: hipGetSymbolAddress: ") + hipGetErrorString(e));
+    }
+    return ORMI_HIP_OK;
+}
 
 }  // namespace ormi_hip
 
 using namespace ormi_hip;
 
 namespace ormi_hip {
+// Element offsets [lo, hi] an operand with these extents and strides spans.
+static void span(long long ext, long long stride, long long* lo, long long* hi) {
+    if (ext <= 1 || stride == 0) return;
+    const long long reach = (ext - 1) * stride;
+    if (reach < 0) *lo += reach;
+    else *hi += reach;
+}
+
 // The epilogue as the kernels take it; an error for a malformed one.
 static int make_epi(const ormi_gemm_desc* d, const ormi_gemm_epilogue* in, long long batch, Epi* out) {
     *out = Epi{};
@@ -1010,9 +1051,16 @@ static int make_epi(const ormi_gemm_desc* d, const ormi_gemm_epilogue* in, long 
     const bool aux_used = in->kind == ORMI_GEMM_EPI_UNARY && in->aux;
     if (aux_used && in->aux < c1 && in->aux + batch * d->M * d->N > c0)
         return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_gemm_ex: aux overlaps C");
-    if (needs_d && in->d >= c0 && in->d < c1) {
-        // In place only with C's own layout: each element is read before the
-        // same thread writes it.
+    long long d_lo = 0, d_hi = 0;
+    if (needs_d) {
+        span(d->M, in->d_stride_m, &d_lo, &d_hi);
+        span(d->N, in->d_stride_n, &d_lo, &d_hi);
+        for (int i = 0; i < d->batch_ndim; ++i) span(d->batch_shape[i], in->d_batch_stride[i], &d_lo, &d_hi);
+    }
+    const intptr_t dp = (intptr_t)in->d, cb = (intptr_t)c0, ce = (intptr_t)c1;
+    if (needs_d && dp + d_lo * 4 < ce && dp + d_hi * 4 >= cb) {
+        // D overlaps C anywhere in its span: allowed in place only, with C's own
+        // layout, where each element is read before the same thread writes it.
         bool same = in->d == c0 && in->d_stride_m == d->N && in->d_stride_n == 1;
         long long contig = (long long)d->M * d->N;
         for (int i = d->batch_ndim - 1; i >= 0 && same; --i) {
@@ -1053,9 +1101,10 @@ static void launch_finish(const ormi_gemm_desc* d, const float* ws, int splits, 
 }
 }  // namespace ormi_hip
 
-extern "C" int ormi_hip_gemm(const ormi_gemm_desc* d) { return ormi_hip_gemm_ex(d, nullptr); }
-
-extern "C" int ormi_hip_gemm_ex(const ormi_gemm_desc* d, const ormi_gemm_epilogue* epi_in) {
+namespace ormi_hip {
+// Both GEMM entries: noalloc takes the workspace from `scratch` instead of the
+// grown-on-demand buffer.
+static int gemm_run(const ormi_gemm_desc* d, const ormi_gemm_epilogue* epi_in, bool noalloc) {
     if (!d) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_gemm: null descriptor");
     if (d->M < 0 || d->N < 0 || d->K < 0) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_gemm: negative dimension");
     if (d->batch_ndim < 0 || d->batch_ndim > ORMI_GEMM_MAX_BATCH_DIMS)
@@ -1078,6 +1127,12 @@ extern "C" int ormi_hip_gemm_ex(const ormi_gemm_desc* d, const ormi_gemm_epilogu
     if (rc != ORMI_HIP_OK) return rc;
     rc = ensure_init();
     if (rc != ORMI_HIP_OK) return rc;
+
+    // Held until this call's kernels are enqueued (see g_ws_mu).
+    std::lock_guard<std::mutex> ws_lock(g_ws_mu);
+    auto workspace = [noalloc](size_t bytes, void** out) {
+        return noalloc ? scratch_locked(bytes, out) : workspace_locked(bytes, out);
+    };
 
     GemmParams p{};
     p.a = (const char*)d->a;
@@ -1235,4 +1290,13 @@ extern "C" int ormi_hip_gemm_ex(const ormi_gemm_desc* d, const ormi_gemm_epilogu
     e = hipGetLastError();
     if (e != hipSuccess) return fail(ORMI_HIP_ERR_RUNTIME, std::string("ormi_hip_gemm launch: ") + hipGetErrorString(e));
     return ORMI_HIP_OK;
+}
+}  // namespace ormi_hip
+
+extern "C" int ormi_hip_gemm(const ormi_gemm_desc* d) { return gemm_run(d, nullptr, false); }
+
+extern "C" int ormi_hip_gemm_ex(const ormi_gemm_desc* d, const ormi_gemm_epilogue* epi) { return gemm_run(d, epi, false); }
+
+extern "C" int ormi_hip_gemm_ex_noalloc(const ormi_gemm_desc* d, const ormi_gemm_epilogue* epi) {
+    return gemm_run(d, epi, true);
 }

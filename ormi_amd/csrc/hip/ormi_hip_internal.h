@@ -9,4 +9,7 @@ namespace ormi_hip {
     int ensure_init();
     // Compute units of the bound device (256 on MI355X).
     int compute_units();
+    // Resolve the device address of the allocation-free GEMM's scratch array on
+    // the current device (called once, by ormi_hip_init).
+    int gemm_scratch_setup();
 }

@@ -173,6 +173,8 @@ int ormi_hip_init(int device) {
     if (device < 0 || device >= n) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_init: device index out of range");
     ORMI_HIP_TRY(hipSetDevice(device));
     ORMI_HIP_TRY(hipGetDeviceProperties(&s.props, device));
+    const int rc = gemm_scratch_setup();
+    if (rc != ORMI_HIP_OK) return rc;
     s.arch = s.props.gcnArchName;
     s.device = device;
     s.inited = true;
