@@ -204,6 +204,46 @@ int ormi_hip_gemm_ex(const ormi_gemm_desc* desc, const ormi_gemm_epilogue* epi);
 #define ORMI_GEMM_NOALLOC_SCRATCH_BYTES (32u << 20)
 int ormi_hip_gemm_ex_noalloc(const ormi_gemm_desc* desc, const ormi_gemm_epilogue* epi);
 
+/* ------------------------------------------------------------- reduction --
+ * Replaces the reference's reduction kernel entry
+ *   cuda::sum(in_buf, in_view, axes, out_view, keepdims)
+ * (csrc/backend/cuda/kernels/reduce/cuda_sum.cuh:5-11, implemented with one
+ * atomicAdd per element in sum.cu:12-97), and adds max and argmax. The library
+ * generates, caches and launches the same hipRTC kernels the fusion scheduler
+ * uses for a reduction with no element-wise prologue: a wave64 per row with
+ * DPP reductions, LDS-combined column waves, and a second kernel that finishes
+ * a split reduced range in part order (deterministic, no atomics).
+ * The input is any strided view: x[i0..i(ndim-1)] at in + sum(i_d * strides[d])
+ * elements (a stride of 0 broadcasts, negative strides are allowed). axes lists
+ * the reduced dims (any order, no repeats); naxes == 0 reduces every dim.
+ * out receives prod(kept extents) values, contiguous in the kept dims' order
+ * (keepdims only changes the shape the caller puts on it): fp32 for SUM and
+ * MAX (of the input converted to fp32), int64 indices for ARGMAX (row-major
+ * position within the reduced dims, first occurrence; NaN counts as the
+ * largest). An empty output is a no-op; SUM over an empty range writes 0; MAX
+ * and ARGMAX over an empty range are ORMI_HIP_ERR_INVALID.
+ * Workspace: a reduction split across work-groups needs
+ * ormi_hip_reduce_workspace_size() bytes of device memory for its partials.
+ * Pass it in workspace / workspace_bytes, or leave workspace NULL and the
+ * library uses a buffer of its own (grown on demand, kept). */
+#define ORMI_REDUCE_MAX_DIMS 8
+enum { ORMI_REDUCE_SUM = 0, ORMI_REDUCE_MAX = 1, ORMI_REDUCE_ARGMAX = 2 };
+typedef struct ormi_reduce_desc {
+    int         op;                               /* ORMI_REDUCE_*                   */
+    int         in_dtype;                         /* ORMI_DTYPE_* of the input        */
+    const void* in;
+    int         ndim;                             /* 0..ORMI_REDUCE_MAX_DIMS          */
+    int         shape[ORMI_REDUCE_MAX_DIMS];
+    int64_t     strides[ORMI_REDUCE_MAX_DIMS];    /* elements                         */
+    int         naxes;
+    int         axes[ORMI_REDUCE_MAX_DIMS];
+    void*       out;
+    void*       workspace;                        /* optional (NULL: library-owned)   */
+    size_t      workspace_bytes;
+} ormi_reduce_desc;
+int ormi_hip_reduce_workspace_size(const ormi_reduce_desc* desc, size_t* bytes);
+int ormi_hip_reduce(const ormi_reduce_desc* desc);
+
 /* ---------------------------------------------------------------- timing --
  * HIP events on the library's stream, for measuring kernel time from
  * outside (benchmarks). */

@@ -47,6 +47,10 @@ CORE_SOURCES = sorted(
     + [p for p in (CSRC / "backend").rglob("*.cpp")]
 )
 HIP_SOURCES = sorted((CSRC / "hip").glob("*.hip"))
+# Host C++ of the device layer: the C-ABI reduction entry and the code generator
+# it shares with the core (a second, hidden-symbol copy inside libormi_hip.so).
+DEVICE_HOST_SOURCES = [CSRC / "hip" / "reduce_entry.cpp", CSRC / "backend" / "hip" / "codegen.cpp",
+                       CSRC / "core" / "dtype.cpp", CSRC / "core" / "ops.cpp"]
 BINDING_SOURCES = sorted((CSRC / "bindings").glob("*.cpp"))
 ORACLE_SOURCES = sorted((ORACLE / "cpu_backend").glob("*.cpp"))
 
@@ -91,9 +95,9 @@ def _fresh(src: Path, obj: Path) -> bool:
     return t > src.stat().st_mtime and t > _newest_header()
 
 
-def _compile_cxx(src: Path, includes: list[Path], extra: list[str] | None = None) -> Path:
+def _compile_cxx(src: Path, includes: list[Path], extra: list[str] | None = None, tag: str = "") -> Path:
     rel = src.relative_to(ROOT)
-    obj = OBJDIR / "obj" / (str(rel).replace(os.sep, "__") + ".o")
+    obj = OBJDIR / "obj" / (str(rel).replace(os.sep, "__") + tag + ".o")
     obj.parent.mkdir(parents=True, exist_ok=True)
     if _fresh(src, obj):
         return obj
@@ -133,10 +137,12 @@ def build(verbose: bool = False, incremental: bool = False) -> None:
         # One object per HIP translation unit, compiled in parallel (the GEMM
         # units take the longest), then linked into the shared library.
         hip_objs = [ex.submit(_compile_hip, s) for s in HIP_SOURCES]
+        dev_host_objs = [ex.submit(_compile_cxx, s, core_inc + [CSRC / "hip"], ["-fvisibility=hidden"], ".dev")
+                         for s in DEVICE_HOST_SOURCES]
         core_objs = [ex.submit(_compile_cxx, s, core_inc) for s in CORE_SOURCES]
         bind_objs = [ex.submit(_compile_cxx, s, core_inc + py_inc) for s in BINDING_SOURCES]
         oracle_objs = [ex.submit(_compile_cxx, s, core_inc) for s in ORACLE_SOURCES]
-        hip = [f.result() for f in hip_objs]
+        hip = [f.result() for f in hip_objs] + [f.result() for f in dev_host_objs]
         core = [f.result() for f in core_objs]
         binds = [f.result() for f in bind_objs]
         oracle = [f.result() for f in oracle_objs]

@@ -32,7 +32,7 @@
 #include <sstream>
 #include <unordered_map>
 
-#include "backend/hip/hip_backend.h"
+#include "backend/hip/kernel_gen.h"
 
 namespace ormi::hip {
     using ops::OpEnum;
@@ -419,7 +419,10 @@ namespace ormi::hip {
                     } else {
                         std::vector<std::string> operands{name[in.a]};
                         if (in.b >= 0) operands.push_back(name[in.b]);
-                        expr = HIPLoweringRegistry::get(in.op)(operands);
+                        if (!in.lower)
+                            throw std::runtime_error(std::string("HIP JIT Compiler Error: No lowering rule registered for ") +
+                                                     ops::op_name(in.op));
+                        expr = (*in.lower)(operands);
                     }
                     name[id] = "t" + std::to_string(i);
                     o << ind << "const float " << name[id] << " = " << expr << ";\n";

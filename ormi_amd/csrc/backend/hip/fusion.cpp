@@ -22,6 +22,10 @@ namespace ormi::hip {
 
     void HIPLoweringRegistry::register_func(OpEnum op, LoweringFunc f) { lowering_table()[op] = std::move(f); }
     bool HIPLoweringRegistry::has(OpEnum op) { return lowering_table().count(op) > 0; }
+    const LoweringFunc* HIPLoweringRegistry::find(OpEnum op) {
+        auto it = lowering_table().find(op);
+        return it == lowering_table().end() ? nullptr : &it->second;
+    }
     LoweringFunc HIPLoweringRegistry::get(OpEnum op) {
         auto it = lowering_table().find(op);
         if (it == lowering_table().end())
@@ -115,7 +119,7 @@ namespace ormi::hip {
         if (!n->data) throw std::runtime_error("HIP codegen: leaf is not realized.");
         if (!plan_only && n->device.type != DeviceEnum::HIP) throw std::runtime_error("HIP codegen: operand lives on another device.");
         Leaf L;
-        L.node = n;
+        L.keep = n;
         L.ptr = n->data->ptr;
         L.dtype = n->data->dtype;
         const size_t ndim = shape.size();
@@ -203,6 +207,7 @@ namespace ormi::hip {
             in.a = value_of.at(n->parents[0].get());
             if (ops::op_arity(n->op) == 2) in.b = value_of.at(n->parents[1].get());
             if (n->op == OpEnum::CAST) in.cast = std::get<CastAttrs>(n->attrs).dtype;
+            else in.lower = HIPLoweringRegistry::find(n->op);
             e.insts.push_back(in);
         }
         for (const auto& r : roots) e.roots.push_back(value_of.at(r.get()));
