@@ -598,19 +598,62 @@ def _pmc_kernel(run_dir: Path, counter: str):
     return name, len(by[name]), sum(by[name]) / len(by[name])
 
 
+def _pmc_by_kernel(run_dir: Path, counter: str):
+    """{kernel name: (first dispatch id, [values])} for one counter of one run."""
+    by = {}
+    for f in sorted(run_dir.rglob("*counter_collection.csv")):
+        with open(f, newline="") as fh:
+            for r in csv.DictReader(fh):
+                if r.get("Counter_Name", "").strip() != counter:
+                    continue
+                name = r.get("Kernel_Name", "").strip()
+                did = int(r.get("Dispatch_Id", 0) or 0)
+                first, vals = by.get(name, (did, []))
+                vals.append(float(r.get("Counter_Value", "nan")))
+                by[name] = (min(first, did), vals)
+    return by
+
+
+# Per workload label: the kernels of that run, in order of first dispatch, with
+# their algorithmic (read, write) bytes per launch. A None entry is a kernel the
+# report lists without an algorithmic figure of its own.
+def _pmc_plan():
+    rows, cols = 16384, 8192
+    inb = rows * cols * 4
+    return {
+        "copy": [("copy y = -x", (2 ** 27, 2 ** 27))],
+        "c2": [("C2 fused map", (c2_bytes() - 2 ** 27, 2 ** 27))],
+        "c3": [("C3 row max", (inb, rows * 4)), ("C3 row sum(exp(x - max))", (inb + rows * 4, rows * 4)),
+               ("C3 row mean (sum)", (inb, rows * 4)), ("C3 row mean (scale by 2^-13)", (rows * 4, rows * 4)),
+               ("C3 row argmax", (inb, rows * 8)),
+               ("C3 column sum, main", (inb, None)), ("C3 column sum, finish", (None, cols * 4))],
+        "c4": [("C4 bf16 4096^3", (2 * 4096 * 4096 * 2, 4096 * 4096 * 4)),
+               ("C4 fp32 NN 2048x1024x4096", ((2048 * 1024 + 1024 * 4096) * 4, 2048 * 4096 * 4)),
+               ("C4 fp32 NT dA (K split)", ((2048 * 4096 + 4096 * 1024) * 4, None)),
+               ("C4 fp32 NT dA, finish", (None, 2048 * 1024 * 4)),
+               ("C4 fp32 TN dB", ((1024 * 2048 + 2048 * 4096) * 4, 1024 * 4096 * 4))],
+    }
+
+
 def pmc_report(pmc_dir: Path, out: Path, cmd: str) -> None:
-    """Turn `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE` runs into HBM bytes per
-    launch. Runs live in pmc_dir/<label>_<COUNTER>/; label "copy" is the calibration
-    kernel (y = -x over 8192x4096 fp32: 128 MiB read, 128 MiB written), whose
-    counters scale every other kernel's KiB figures to bytes."""
-    alg = {"copy": (2 ** 27, 2 ** 27), "c2_fused_map": (c2_bytes() - 2 ** 27, 2 ** 27)}
+    """Turn `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE` runs into bytes per
+    launch. Runs live in pmc_dir/<label>_<COUNTER>/. Label "copy" is the
+    calibration kernel (y = -x over 8192x4096 fp32: 128 MiB read, 128 MiB
+    written), whose counters scale every other kernel's KiB figures to bytes; a
+    run pmc_dir/copy_raw/ of TCC_EA0_RDREQ, TCC_EA0_RDREQ_32B and TCC_BUBBLE,
+    when present, shows where the read factor comes from."""
+    plan = _pmc_plan()
     got = {}
-    for label in alg:
-        f_name, f_n, f_kib = _pmc_kernel(pmc_dir / f"{label}_FETCH_SIZE", "FETCH_SIZE")
-        w_name, w_n, w_kib = _pmc_kernel(pmc_dir / f"{label}_WRITE_SIZE", "WRITE_SIZE")
-        got[label] = (f_name, f_n, f_kib, w_kib)
-    sf = alg["copy"][0] / (got["copy"][2] * 1024)
-    sw = alg["copy"][1] / (got["copy"][3] * 1024)
+    for label in plan:
+        f_dir, w_dir = pmc_dir / f"{label}_FETCH_SIZE", pmc_dir / f"{label}_WRITE_SIZE"
+        if not f_dir.exists() or not w_dir.exists():
+            continue
+        fb, wb = _pmc_by_kernel(f_dir, "FETCH_SIZE"), _pmc_by_kernel(w_dir, "WRITE_SIZE")
+        names = sorted((k for k in fb if k in wb and ("ormi_" in k or "gemm" in k)), key=lambda k: fb[k][0])
+        got[label] = [(k, len(fb[k][1]), sum(fb[k][1]) / len(fb[k][1]), sum(wb[k][1]) / len(wb[k][1])) for k in names]
+    copy = got["copy"][0]
+    sf = plan["copy"][0][1][0] / (copy[2] * 1024)
+    sw = plan["copy"][0][1][1] / (copy[3] * 1024)
     lines = [
         "# HBM traffic per launch (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, one run each)",
         "",
@@ -618,13 +661,32 @@ def pmc_report(pmc_dir: Path, out: Path, cmd: str) -> None:
         "",
         f"Scale factors from the copy kernel (y = -x, 8192x4096 fp32, 134217728 B read + 134217728 B written): "
         f"fetch {sf:.4f}, write {sw:.4f} (algorithmic bytes / (KiB x 1024)).",
-        "",
-        "| kernel | fetch KiB/dispatch | write KiB/dispatch | traffic bytes/launch | algorithmic bytes/launch | dispatches | name |",
-        "|---|---|---|---|---|---|---|",
     ]
-    for label, (name, n, fk, wk) in got.items():
-        traffic = int(round(fk * 1024 * sf + wk * 1024 * sw))
-        lines.append(f"| {label} | {fk:.1f} | {wk:.1f} | {traffic} | {sum(alg[label])} | {n} | {name} |")
+    raw = pmc_dir / "copy_raw"
+    if raw.exists():
+        vals = {c: _pmc_by_kernel(raw, c) for c in ("TCC_EA0_RDREQ_sum", "TCC_EA0_RDREQ_32B_sum", "TCC_BUBBLE_sum")}
+        k = copy[0]
+        mean = {c: (sum(v[k][1]) / len(v[k][1]) if k in v else float("nan")) for c, v in vals.items()}
+        rd, r32, bub = mean["TCC_EA0_RDREQ_sum"], mean["TCC_EA0_RDREQ_32B_sum"], mean["TCC_BUBBLE_sum"]
+        lines += ["", f"Raw read requests of the copy kernel (L2 to fabric): TCC_EA0_RDREQ {rd:.0f}, of which 32-byte "
+                  f"{r32:.0f}, TCC_BUBBLE (counted as 128-byte) {bub:.0f}; 134217728 B / RDREQ = "
+                  f"{2 ** 27 / rd:.1f} bytes per request. FETCH_SIZE weighs a request that is neither 32-byte nor "
+                  f"counted by TCC_BUBBLE as 64 bytes."]
+    lines += ["", "| kernel | fetch KiB/dispatch | write KiB/dispatch | read bytes | write bytes | algorithmic read | "
+              "algorithmic write | traffic / algorithmic | dispatches | name |",
+              "|---|---|---|---|---|---|---|---|---|---|"]
+    for label, rows in got.items():
+        for i, (name, n, fk, wk) in enumerate(rows):
+            desc, (ar, aw) = plan[label][i] if i < len(plan[label]) else (name, (None, None))
+            rb, wbyt = int(round(fk * 1024 * sf)), int(round(wk * 1024 * sw))
+            alg = (ar or 0) + (aw or 0)
+            ratio = f"{(rb + wbyt) / alg:.3f}" if ar is not None and aw is not None else "—"
+            lines.append(f"| {desc} | {fk:.1f} | {wk:.1f} | {rb} | {wbyt} | {ar if ar is not None else '—'} | "
+                         f"{aw if aw is not None else '—'} | {ratio} | {n} | `{name[:60]}` |")
+    lines += ["", "Fetch and write bytes count the L2's requests to the fabric, so they include reads the 256 MB "
+              "Infinity Cache serves. A GEMM reads each operand panel once per XCD that needs it (8 L2s): the bf16 "
+              "kernel's 4x8 tile group per XCD needs 8 MB of A and 16 MB of B, 192 MB over the chip against the "
+              "64 MB of its operands, which stay resident in the Infinity Cache."]
     out.write_text("\n".join(lines) + "\n")
     print(out.read_text())
 
@@ -767,8 +829,12 @@ def main():
         return
     if args.pmc_report:
         pmc_report(Path(args.pmc_report[0]), Path(args.pmc_report[1]),
-                   "rocprofv3 --pmc FETCH_SIZE|WRITE_SIZE -d <PMC_DIR>/<label>_<COUNTER> -o run --output-format csv "
-                   "-- python3 bench.py --only copy | --no-extra --no-cpu, --steps 5 --warmup 1")
+                   "for each (label, args) in (copy, --only copy), (c2, --no-extra --no-cpu), (c3, --only c3), "
+                   "(c4, --only c4) and COUNTER in FETCH_SIZE, WRITE_SIZE: rocprofv3 --pmc COUNTER "
+                   "-d <PMC_DIR>/<label>_COUNTER -o run --output-format csv -- python3 bench.py <args> --steps 5 "
+                   "--warmup 1; and rocprofv3 --pmc TCC_EA0_RDREQ_sum TCC_EA0_RDREQ_32B_sum TCC_BUBBLE_sum "
+                   "-d <PMC_DIR>/copy_raw ... -- python3 bench.py --only copy --steps 5 --warmup 1; then "
+                   "python3 bench.py --pmc-report <PMC_DIR> profiles/hbm_traffic.md")
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
