@@ -13,7 +13,8 @@
  *     Copies to the host synchronize (csrc/backend/cuda/allocator.cu:89-91).
  *   - Device pointers belong to the caller. Compiled modules and kernel
  *     handles belong to the library's cache and live until process exit.
- *   - Memory entry points are thread-safe; launches are issued in call order.
+ *   - Memory entry points are thread-safe; launches are issued in call order
+ *     (queued launches included: see ormi_hip_launch_queued).
  */
 #ifndef ORMI_HIP_H
 #define ORMI_HIP_H
@@ -106,6 +107,19 @@ int ormi_hip_rtc_compile_only(const char* source, const char* target,
  * kernelParams array: one pointer per kernel parameter. */
 int ormi_hip_launch(uint64_t handle, const uint32_t grid[3], const uint32_t block[3],
                     uint32_t lds_bytes, void** args);
+
+/* Queued launch of a compiled kernel whose parameters are all 8 bytes wide
+ * (the generated kernels' convention): args holds num_args parameter values
+ * (not pointers to them), copied before the call returns. The launch is issued
+ * to the stream, after every earlier launch, by the library's launch thread,
+ * so the calling thread does not pay the launch itself. Stream order is kept:
+ * every other entry point that touches the device (copies, fills, GEMMs,
+ * reductions, events, synchronize, free) first waits until all queued launches
+ * are issued. An error of a queued launch is returned by the next such call.
+ * Replaces cuLaunchKernel for generated kernels (reference jit.cu:40). */
+#define ORMI_HIP_QUEUED_MAX_ARGS 128
+int ormi_hip_launch_queued(uint64_t handle, const uint32_t grid[3], const uint32_t block[3],
+                           uint32_t lds_bytes, const uint64_t* args, int num_args);
 
 /* Number of distinct code objects compiled so far (cache misses). */
 int ormi_hip_rtc_cache_size(uint64_t* entries);

@@ -1182,9 +1182,13 @@ namespace ormi::hip {
                 cache_store(done);
             }
         }
-        std::vector<uint64_t> vals = k.args;
-        std::vector<void*> ptrs(vals.size());
-        for (size_t i = 0; i < vals.size(); ++i) ptrs[i] = &vals[i];
-        ORMI_HIP_CHECK(ormi_hip_launch(handle, k.grid, k.block, 0, ptrs.data()));
+        if (k.args.size() <= ORMI_HIP_QUEUED_MAX_ARGS) {
+            ORMI_HIP_CHECK(ormi_hip_launch_queued(handle, k.grid, k.block, 0, k.args.data(), (int)k.args.size()));
+        } else {
+            std::vector<uint64_t> vals = k.args;
+            std::vector<void*> ptrs(vals.size());
+            for (size_t i = 0; i < vals.size(); ++i) ptrs[i] = &vals[i];
+            ORMI_HIP_CHECK(ormi_hip_launch(handle, k.grid, k.block, 0, ptrs.data()));
+        }
     }
 }

@@ -1127,6 +1127,8 @@ static int gemm_run(const ormi_gemm_desc* d, const ormi_gemm_epilogue* epi_in, b
     if (rc != ORMI_HIP_OK) return rc;
     rc = ensure_init();
     if (rc != ORMI_HIP_OK) return rc;
+    rc = drain_queue();
+    if (rc != ORMI_HIP_OK) return rc;
 
     // Held until this call's kernels are enqueued (see g_ws_mu).
     std::lock_guard<std::mutex> ws_lock(g_ws_mu);

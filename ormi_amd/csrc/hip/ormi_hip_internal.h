@@ -12,4 +12,7 @@ namespace ormi_hip {
     // Resolve the device address of the allocation-free GEMM's scratch array on
     // the current device (called once, by ormi_hip_init).
     int gemm_scratch_setup();
+    // Wait until the launch queue has issued every launch submitted so far;
+    // returns the error of a queued launch that failed (once).
+    int drain_queue();
 }

@@ -3,8 +3,12 @@
 #include <hip/hip_runtime.h>
 #include <hip/hiprtc.h>
 
+#include <atomic>
+#include <condition_variable>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
+#include <thread>
 #include <string>
 #include <unordered_map>
 #include <vector>
@@ -133,6 +137,137 @@ static int rtc_build(const char* source, const std::string& target, const char* 
     return ORMI_HIP_OK;
 }
 
+// ----------------------------------------------------------- launch queue --
+// Launches of generated kernels (ormi_hip_launch_queued) are recorded here and
+// issued to the null stream, in submission order, by one worker thread. A HIP
+// launch costs the calling thread about 3.5 us on MI355X hosts whatever its
+// form, more than a small fused kernel runs; with the queue the thread that
+// builds graphs pays a copy of the arguments instead, and launching overlaps
+// its next graph. Every other entry point that touches the device first waits
+// until the queue has issued everything submitted before it (drain_queue), so
+// the stream sees exactly the order of the calls, as without the queue.
+struct QueuedLaunch {
+    hipFunction_t fn;
+    uint32_t grid[3], block[3], lds;
+    int nargs;
+    uint64_t args[ORMI_HIP_QUEUED_MAX_ARGS];
+};
+
+struct LaunchQueue {
+    static constexpr uint64_t N = 1024;
+    QueuedLaunch slot[N];
+    std::atomic<uint64_t> head{0};  // submitted
+    std::atomic<uint64_t> tail{0};  // issued
+    std::mutex submit_mu;           // one submitter at a time
+    std::mutex sleep_mu;
+    std::condition_variable wake;
+    std::atomic<bool> sleeping{false};
+    std::atomic<bool> stop{false};
+    std::atomic<bool> failed{false};
+    std::mutex err_mu;
+    std::string error;
+    std::thread worker;
+    bool started = false;
+    int device = 0;
+
+    void run() {
+        if (hipSetDevice(device) != hipSuccess) {
+            record_error("launch queue: hipSetDevice failed");
+        }
+        for (;;) {
+            const uint64_t t = tail.load(std::memory_order_relaxed);
+            if (head.load(std::memory_order_acquire) == t) {
+                if (stop.load()) return;
+                // Spin for a while (launches tend to come in bursts), then sleep.
+                bool got = false;
+                for (int i = 0; i < 20000 && !got; ++i) {
+                    if (head.load(std::memory_order_acquire) != t) got = true;
+                    else if ((i & 63) == 63) std::this_thread::yield();
+                }
+                if (!got) {
+                    std::unique_lock<std::mutex> lock(sleep_mu);
+                    sleeping.store(true);
+                    wake.wait(lock, [&] { return head.load() != t || stop.load(); });
+                    sleeping.store(false);
+                }
+                continue;
+            }
+            QueuedLaunch& q = slot[t % N];
+            void* ptrs[ORMI_HIP_QUEUED_MAX_ARGS];
+            for (int i = 0; i < q.nargs; ++i) ptrs[i] = &q.args[i];
+            const hipError_t e = hipModuleLaunchKernel(q.fn, q.grid[0], q.grid[1], q.grid[2], q.block[0], q.block[1],
+                                                       q.block[2], q.lds, 0, ptrs, nullptr);
+            if (e != hipSuccess) record_error(std::string("queued kernel launch: ") + hipGetErrorString(e));
+            tail.store(t + 1, std::memory_order_release);
+        }
+    }
+    void record_error(const std::string& msg) {
+        std::lock_guard<std::mutex> lock(err_mu);
+        if (!failed.load()) error = msg;
+        failed.store(true);
+    }
+};
+
+static LaunchQueue& launch_queue() {
+    static LaunchQueue* q = new LaunchQueue();  // never destroyed: the worker is joined at exit
+    return *q;
+}
+
+static void stop_launch_queue() {
+    LaunchQueue& q = launch_queue();
+    if (!q.started) return;
+    q.stop.store(true);
+    {
+        std::lock_guard<std::mutex> lock(q.sleep_mu);
+        q.wake.notify_all();
+    }
+    q.worker.join();
+    q.started = false;
+}
+
+// Wait until every queued launch has been issued; report a failed one.
+int drain_queue() {
+    LaunchQueue& q = launch_queue();
+    if (q.started) {
+        while (q.tail.load(std::memory_order_acquire) != q.head.load(std::memory_order_acquire)) std::this_thread::yield();
+    }
+    if (q.failed.load()) {
+        std::lock_guard<std::mutex> lock(q.err_mu);
+        q.failed.store(false);
+        return fail(ORMI_HIP_ERR_RUNTIME, q.error);
+    }
+    return ORMI_HIP_OK;
+}
+
+static int submit_launch(hipFunction_t fn, const uint32_t grid[3], const uint32_t block[3], uint32_t lds,
+                         const uint64_t* args, int nargs) {
+    LaunchQueue& q = launch_queue();
+    std::lock_guard<std::mutex> lock(q.submit_mu);
+    if (!q.started) {
+        q.device = state().device;
+        q.worker = std::thread([&q] { q.run(); });
+        q.started = true;
+        std::atexit(stop_launch_queue);
+    }
+    const uint64_t h = q.head.load(std::memory_order_relaxed);
+    while (h - q.tail.load(std::memory_order_acquire) >= LaunchQueue::N) std::this_thread::yield();
+    QueuedLaunch& s = q.slot[h % LaunchQueue::N];
+    s.fn = fn;
+    for (int i = 0; i < 3; ++i) {
+        s.grid[i] = grid[i];
+        s.block[i] = block[i];
+    }
+    s.lds = lds;
+    s.nargs = nargs;
+    std::memcpy(s.args, args, sizeof(uint64_t) * (size_t)nargs);
+    q.head.store(h + 1, std::memory_order_seq_cst);
+    if (q.sleeping.load(std::memory_order_seq_cst)) {
+        std::lock_guard<std::mutex> sl(q.sleep_mu);
+        q.wake.notify_one();
+    }
+    return ORMI_HIP_OK;
+}
+
 }  // namespace ormi_hip
 
 using namespace ormi_hip;
@@ -146,6 +281,13 @@ using namespace ormi_hip;
 #define ORMI_ENSURE_INIT()                    \
     do {                                      \
         int rc_ = ensure_init();              \
+        if (rc_ != ORMI_HIP_OK) return rc_;   \
+    } while (0)
+
+// Issue every queued launch first (stream order; see the launch queue).
+#define ORMI_HIP_DRAIN()                      \
+    do {                                      \
+        int rc_ = drain_queue();              \
         if (rc_ != ORMI_HIP_OK) return rc_;   \
     } while (0)
 
@@ -205,6 +347,7 @@ int ormi_hip_malloc(void** ptr, size_t bytes) {
 
 int ormi_hip_free(void* ptr) {
     if (!ptr) return ORMI_HIP_OK;
+    ORMI_HIP_DRAIN();
     ORMI_HIP_TRY(hipFree(ptr));
     return ORMI_HIP_OK;
 }
@@ -213,6 +356,7 @@ int ormi_hip_fill(void* dst, const void* value, size_t elem_bytes, size_t count)
     if (count == 0) return ORMI_HIP_OK;
     if (!dst || !value) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_fill: null pointer");
     ORMI_ENSURE_INIT();
+    ORMI_HIP_DRAIN();
     const unsigned block = 256, grid = grid_for(count, block);
     switch (elem_bytes) {
         case 1: { unsigned char v; std::memcpy(&v, value, 1); fill_kernel<unsigned char><<<grid, block>>>((unsigned char*)dst, v, count); break; }
@@ -232,6 +376,7 @@ int ormi_hip_memcpy_h2d(void* dst, const void* src, size_t bytes) {
     if (bytes == 0) return ORMI_HIP_OK;
     if (!dst || !src) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_memcpy_h2d: null pointer");
     ORMI_ENSURE_INIT();
+    ORMI_HIP_DRAIN();
     ORMI_HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
     return ORMI_HIP_OK;
 }
@@ -240,6 +385,7 @@ int ormi_hip_memcpy_d2h(void* dst, const void* src, size_t bytes) {
     if (bytes == 0) return ORMI_HIP_OK;
     if (!dst || !src) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_memcpy_d2h: null pointer");
     ORMI_ENSURE_INIT();
+    ORMI_HIP_DRAIN();
     ORMI_HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
     return ORMI_HIP_OK;
 }
@@ -248,12 +394,14 @@ int ormi_hip_memcpy_d2d(void* dst, const void* src, size_t bytes) {
     if (bytes == 0) return ORMI_HIP_OK;
     if (!dst || !src) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_memcpy_d2d: null pointer");
     ORMI_ENSURE_INIT();
+    ORMI_HIP_DRAIN();
     ORMI_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, 0));
     return ORMI_HIP_OK;
 }
 
 int ormi_hip_synchronize(void) {
     ORMI_ENSURE_INIT();
+    ORMI_HIP_DRAIN();
     ORMI_HIP_TRY(hipDeviceSynchronize());
     return ORMI_HIP_OK;
 }
@@ -264,6 +412,7 @@ int ormi_hip_convert(void* dst, int dst_dtype, const void* src, int src_dtype, s
     if (dst_dtype < 0 || dst_dtype > ORMI_DTYPE_I64 || src_dtype < 0 || src_dtype > ORMI_DTYPE_I64)
         return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_convert: unknown dtype code");
     ORMI_ENSURE_INIT();
+    ORMI_HIP_DRAIN();
     const unsigned block = 256, grid = grid_for(count, block);
     convert_kernel<<<grid, block>>>(dst, dst_dtype, src, src_dtype, count);
     ORMI_HIP_TRY(hipGetLastError());
@@ -345,8 +494,27 @@ int ormi_hip_launch(uint64_t handle, const uint32_t grid[3], const uint32_t bloc
     if (grid[0] == 0 || grid[1] == 0 || grid[2] == 0) return ORMI_HIP_OK;  // empty launch: nothing to do
     if (block[0] * block[1] * block[2] == 0 || block[0] * block[1] * block[2] > 1024)
         return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_launch: block size must be 1..1024 threads");
+    ORMI_HIP_DRAIN();
     ORMI_HIP_TRY(hipModuleLaunchKernel(fn, grid[0], grid[1], grid[2], block[0], block[1], block[2], lds_bytes, 0, args, nullptr));
     return ORMI_HIP_OK;
+}
+
+int ormi_hip_launch_queued(uint64_t handle, const uint32_t grid[3], const uint32_t block[3], uint32_t lds_bytes,
+                           const uint64_t* args, int num_args) {
+    if (!grid || !block || (num_args > 0 && !args)) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_launch_queued: null argument");
+    if (num_args < 0 || num_args > ORMI_HIP_QUEUED_MAX_ARGS)
+        return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_launch_queued: more than ORMI_HIP_QUEUED_MAX_ARGS arguments");
+    hipFunction_t fn;
+    {
+        RtcCache& c = rtc_cache();
+        std::lock_guard<std::mutex> lock(c.mu);
+        if (handle == 0 || handle > c.entries.size()) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_launch_queued: unknown kernel handle");
+        fn = c.entries[handle - 1].function;
+    }
+    if (grid[0] == 0 || grid[1] == 0 || grid[2] == 0) return ORMI_HIP_OK;
+    if (block[0] * block[1] * block[2] == 0 || block[0] * block[1] * block[2] > 1024)
+        return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_launch_queued: block size must be 1..1024 threads");
+    return submit_launch(fn, grid, block, lds_bytes, args, num_args);
 }
 
 int ormi_hip_event_create(void** event) {
@@ -360,6 +528,7 @@ int ormi_hip_event_create(void** event) {
 
 int ormi_hip_event_record(void* event) {
     if (!event) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_event_record: null event");
+    ORMI_HIP_DRAIN();
     ORMI_HIP_TRY(hipEventRecord((hipEvent_t)event, 0));
     return ORMI_HIP_OK;
 }
