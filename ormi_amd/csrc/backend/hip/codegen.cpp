@@ -30,6 +30,7 @@
 #include <cstdlib>
 #include <mutex>
 #include <sstream>
+#include <string_view>
 #include <unordered_map>
 
 #include "backend/hip/kernel_gen.h"
@@ -584,6 +585,15 @@ namespace ormi::hip {
                      const std::string& layout = std::string()) {
             k.args = g.args.vals;
             k.block[0] = (uint32_t)block;
+            k.ptr_slots.clear();
+            for (size_t i = 0; i < g.args.decls.size(); ++i) {
+                const ArgDecl& d = g.args.decls[i];
+                if (!d.is_ptr) continue;
+                const std::string_view name(d.name);
+                if (name == "L") k.ptr_slots.push_back({(int)i, d.i});
+                else if (name == "out") k.ptr_slots.push_back({(int)i, -1 - std::max(d.i, 0)});
+                else if (name == "outp" && g.args.vals[i] != 0) k.ptr_slots.push_back({(int)i, -1});
+            }
             std::string sig = signature(g, kind);
             sig += "|b";
             append_int(sig, block);
@@ -618,12 +628,8 @@ namespace ormi::hip {
     }
 
     // ------------------------------------------------------------------ map --
-    KernelLaunch plan_map(const Expr& expr, const std::vector<int>& shape, void* out, DType out_dtype, int cu) {
-        return plan_map_multi(expr, shape, {out}, {out_dtype}, cu);
-    }
-
-    KernelLaunch plan_map_multi(const Expr& expr, const std::vector<int>& shape, const std::vector<void*>& outs,
-                                const std::vector<DType>& out_dtypes, int cu) {
+    static KernelLaunch plan_map_multi_uncached(const Expr& expr, const std::vector<int>& shape, const std::vector<void*>& outs,
+                                                const std::vector<DType>& out_dtypes, int cu) {
         if (outs.size() != expr.roots.size() || outs.size() != out_dtypes.size() || outs.empty())
             throw std::runtime_error("HIP codegen: one output buffer and dtype per root.");
         const size_t nout = outs.size();
@@ -827,8 +833,8 @@ namespace ormi::hip {
     }
 
     // ------------------------------------------------------------- reduce --
-    ReducePlan plan_reduce(const Expr& expr, const std::vector<int>& in_shape, const std::vector<int>& axes_in, ReduceOp op,
-                           void* out, int cu) {
+    static ReducePlan plan_reduce_uncached(const Expr& expr, const std::vector<int>& in_shape, const std::vector<int>& axes_in,
+                                           ReduceOp op, void* out, int cu) {
         const Tuning& tn = tuning();
         const int n = (int)in_shape.size();
         std::vector<bool> red(n, axes_in.empty());
@@ -1157,6 +1163,124 @@ namespace ormi::hip {
     // Point the split-reduction kernels at the workspace: values first, then
     // indices. The first kernel's outp/outi are args 0 and 1; the second
     // kernel's pvals/pidx are args 1 and 2.
+    // ------------------------------------------------------ request cache --
+    // A plan depends only on the request's structure: the tape, each leaf's
+    // dtype, scalar flag and strides, the alignment of every buffer address,
+    // the shape (and axes and op), the compute units and the tuning. Repeat
+    // requests (every step of a training loop) take the plan from this cache and
+    // rewrite only the buffer addresses (ptr_slots), skipping the generator's
+    // signature and argument construction.
+    namespace {
+        struct KeyBuf {
+            std::string s;
+            void i64(long long v) { s.append(reinterpret_cast<const char*>(&v), sizeof v); }
+        };
+        void key_expr(KeyBuf& kb, const Expr& e) {
+            kb.i64((long long)e.leaves.size());
+            for (const Leaf& L : e.leaves) {
+                kb.i64((long long)L.dtype | ((long long)L.scalar << 8) | ((long long)L.st.size() << 16) |
+                       ((long long)((uintptr_t)L.ptr & 255) << 32));
+                for (long long v : L.st) kb.i64(v);
+            }
+            kb.i64((long long)e.insts.size());
+            for (const Inst& in : e.insts)
+                kb.i64((long long)in.op | ((long long)(in.a + 1) << 8) | ((long long)(in.b + 1) << 28) |
+                       ((long long)in.cast << 56));
+            for (int r : e.roots) kb.i64(r);
+            kb.i64(-1);
+        }
+        struct RequestCache {
+            std::mutex mu;
+            std::unordered_map<std::string, KernelLaunch> maps;
+            std::unordered_map<std::string, ReducePlan> reduces;
+        };
+        RequestCache& request_cache() {
+            static auto* c = new RequestCache();
+            return *c;
+        }
+        constexpr size_t kMaxRequests = 8192;
+        // A cached launch whose kernel has been compiled since: take its handle
+        // and drop the source text.
+        void refresh_handle(KernelLaunch& k) {
+            if (k.handle || k.key.empty()) return;
+            KernelLaunch probe;
+            if (cache_lookup(k.key, probe) && probe.handle) {
+                k.handle = probe.handle;
+                k.source.clear();
+                k.source.shrink_to_fit();
+            }
+        }
+        void patch(KernelLaunch& k, const Expr& e, const void* const* outs) {
+            for (const auto& [slot, src] : k.ptr_slots)
+                k.args[slot] = (uint64_t)(uintptr_t)(src >= 0 ? e.leaves[src].ptr : outs[-1 - src]);
+        }
+    }  // namespace
+
+    KernelLaunch plan_map_multi(const Expr& expr, const std::vector<int>& shape, const std::vector<void*>& outs,
+                                const std::vector<DType>& out_dtypes, int cu) {
+        if (outs.size() != expr.roots.size() || outs.size() != out_dtypes.size() || outs.empty())
+            throw std::runtime_error("HIP codegen: one output buffer and dtype per root.");
+        KeyBuf kb;
+        kb.i64('M');
+        kb.i64(cu);
+        kb.i64((long long)shape.size());
+        for (int d : shape) kb.i64(d);
+        for (size_t r = 0; r < outs.size(); ++r) kb.i64((long long)out_dtypes[r] | ((long long)((uintptr_t)outs[r] & 255) << 8));
+        key_expr(kb, expr);
+        RequestCache& rc = request_cache();
+        {
+            std::lock_guard<std::mutex> lock(rc.mu);
+            auto it = rc.maps.find(kb.s);
+            if (it != rc.maps.end()) {
+                refresh_handle(it->second);
+                KernelLaunch k = it->second;
+                patch(k, expr, outs.data());
+                return k;
+            }
+        }
+        KernelLaunch k = plan_map_multi_uncached(expr, shape, outs, out_dtypes, cu);
+        std::lock_guard<std::mutex> lock(rc.mu);
+        if (rc.maps.size() >= kMaxRequests) rc.maps.clear();
+        rc.maps.emplace(std::move(kb.s), k);
+        return k;
+    }
+
+    KernelLaunch plan_map(const Expr& expr, const std::vector<int>& shape, void* out, DType out_dtype, int cu) {
+        return plan_map_multi(expr, shape, {out}, {out_dtype}, cu);
+    }
+
+    ReducePlan plan_reduce(const Expr& expr, const std::vector<int>& in_shape, const std::vector<int>& axes, ReduceOp op,
+                           void* out, int cu) {
+        KeyBuf kb;
+        kb.i64('R');
+        kb.i64(cu);
+        kb.i64((long long)op | ((long long)((uintptr_t)out & 255) << 8));
+        kb.i64((long long)in_shape.size());
+        for (int d : in_shape) kb.i64(d);
+        kb.i64((long long)axes.size());
+        for (int a : axes) kb.i64(a);
+        key_expr(kb, expr);
+        const void* outs[1] = {out};
+        RequestCache& rc = request_cache();
+        {
+            std::lock_guard<std::mutex> lock(rc.mu);
+            auto it = rc.reduces.find(kb.s);
+            if (it != rc.reduces.end()) {
+                refresh_handle(it->second.first);
+                if (it->second.two_pass) refresh_handle(it->second.second);
+                ReducePlan plan = it->second;
+                patch(plan.first, expr, outs);
+                if (plan.two_pass) patch(plan.second, expr, outs);
+                return plan;
+            }
+        }
+        ReducePlan plan = plan_reduce_uncached(expr, in_shape, axes, op, out, cu);
+        std::lock_guard<std::mutex> lock(rc.mu);
+        if (rc.reduces.size() >= kMaxRequests) rc.reduces.clear();
+        rc.reduces.emplace(std::move(kb.s), plan);
+        return plan;
+    }
+
     void bind_workspace(ReducePlan& plan, void* ws) {
         if (!plan.two_pass) return;
         const size_t nvals = plan.workspace_bytes / (sizeof(float) + sizeof(int));

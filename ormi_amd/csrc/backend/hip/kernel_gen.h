@@ -83,6 +83,10 @@ namespace ormi::hip {
         uint32_t block[3] = {256, 1, 1};
         std::vector<uint64_t> args;  // every parameter is 8 bytes
         PlanInfo plan;
+        // Arguments that hold a buffer address, as (argument index, source):
+        // source >= 0 is that leaf's pointer, -1 - r is output r. A repeat
+        // request reuses the plan and rewrites only these.
+        std::vector<std::pair<int, int>> ptr_slots;
     };
 
     // Launch-shape knobs of the generated kernels. Defaults are the values

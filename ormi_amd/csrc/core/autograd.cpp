@@ -10,27 +10,32 @@
 namespace ormi {
     // Post-order DFS with an explicit stack; the visiting order matches the
     // reference's recursive build_topo (csrc/core/autograd.cpp:12-22) without
-    // its recursion-depth limit.
-    std::vector<std::shared_ptr<Node>> topo_order(const std::shared_ptr<Node>& root) {
-        std::vector<std::shared_ptr<Node>> topo;
+    // its recursion-depth limit. Raw pointers: root keeps every node it reaches
+    // alive for the walk (no reference-count traffic per step).
+    static std::vector<Node*> topo_nodes(Node* root) {
+        std::vector<Node*> topo;
         if (!root) return topo;
         std::unordered_set<Node*> visited;
-        std::vector<std::pair<std::shared_ptr<Node>, size_t>> stack;
-        visited.insert(root.get());
+        visited.reserve(64);
+        std::vector<std::pair<Node*, size_t>> stack;
+        visited.insert(root);
         stack.push_back({root, 0});
         while (!stack.empty()) {
             auto& [node, next] = stack.back();
             if (next < node->parents.size()) {
-                auto p = node->parents[next++];
-                if (p && !visited.count(p.get())) {
-                    visited.insert(p.get());
-                    stack.push_back({p, 0});
-                }
+                Node* p = node->parents[next++].get();
+                if (p && visited.insert(p).second) stack.push_back({p, 0});
             } else {
                 topo.push_back(node);
                 stack.pop_back();
             }
         }
+        return topo;
+    }
+
+    std::vector<std::shared_ptr<Node>> topo_order(const std::shared_ptr<Node>& root) {
+        std::vector<std::shared_ptr<Node>> topo;
+        for (Node* n : topo_nodes(root.get())) topo.push_back(n->shared_from_this());
         return topo;
     }
 
@@ -50,23 +55,24 @@ namespace ormi {
     // Reverse-mode pass that only builds lazy gradient nodes
     // (reference: csrc/core/autograd.cpp:24-47).
     void compute_gradients(std::shared_ptr<Node> root) {
-        auto topo = topo_order(root);
+        const auto topo = topo_nodes(root.get());
         if (!root->grad) {
             long long n = 1;
             for (int d : root->view.shape) n *= d;
             auto seed = n == 1 ? scalar_seed(root->view.shape, root->device.type) : ones(root->view.shape, root->device.type);
             root->grad = std::make_shared<Node>(seed, false, root->device);
         }
+        const auto& rules = Registry<AdjointFunc>::get_map();
         for (auto it = topo.rbegin(); it != topo.rend(); ++it) {
-            auto node = *it;
+            Node* node = *it;
             if (!node->grad || node->op == ops::OpEnum::LEAF) continue;
-            auto adjoint = Registry<AdjointFunc>::get(node->op);
-            if (!adjoint) throw std::runtime_error("No Adjoint rule registered for operation.");
-            adjoint(node);
+            auto rule = rules.find(node->op);
+            if (rule == rules.end() || !rule->second) throw std::runtime_error("No Adjoint rule registered for operation.");
+            rule->second(node->shared_from_this());
         }
     }
 
     void zero_grad_graph(std::shared_ptr<Node> root) {
-        for (auto& node : topo_order(root)) node->grad = nullptr;
+        for (Node* node : topo_nodes(root.get())) node->grad = nullptr;
     }
 }

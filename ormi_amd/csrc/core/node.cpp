@@ -34,8 +34,8 @@ namespace ormi {
         if (op == ops::OpEnum::ARGMAX || op == ops::OpEnum::STEP || op == ops::OpEnum::EQ) requires_grad = false;
 
         view.shape = infer_shape(op, parents, attrs);
-        auto stride_func = Registry<StrideInferFunc>::get(op);
-        view.strides = stride_func ? stride_func(parents, attrs, view.shape) : calc_contiguous_strides(view.shape);
+        const StrideInferFunc* stride_func = Registry<StrideInferFunc>::find(op);
+        view.strides = stride_func ? (*stride_func)(parents, attrs, view.shape) : calc_contiguous_strides(view.shape);
         dtype = result_dtype(op, parents, attrs);
     }
 

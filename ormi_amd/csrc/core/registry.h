@@ -24,9 +24,14 @@ namespace ormi {
         static std::unordered_map<ops::OpEnum, FuncType>& get_map();
         static void add(ops::OpEnum op, FuncType func) { get_map()[op] = std::move(func); }
         static FuncType get(ops::OpEnum op) {
+            const FuncType* f = find(op);
+            return f ? *f : FuncType(nullptr);
+        }
+        // The registered rule, or nullptr (no copy of the function object).
+        static const FuncType* find(ops::OpEnum op) {
             auto& m = get_map();
             auto it = m.find(op);
-            return it == m.end() ? FuncType(nullptr) : it->second;
+            return it == m.end() || !it->second ? nullptr : &it->second;
         }
     };
 

@@ -53,9 +53,9 @@ namespace ormi {
 
     std::vector<int> infer_shape(ops::OpEnum op, const std::vector<std::shared_ptr<Node>>& parents, const OpAttributes& attrs) {
         if (op == ops::OpEnum::LEAF || op == ops::OpEnum::CONST || parents.empty()) return {};
-        auto func = Registry<ShapeInferFunc>::get(op);
+        const ShapeInferFunc* func = Registry<ShapeInferFunc>::find(op);
         if (!func) throw std::runtime_error("Shape inference rule not registered for this OpEnum.");
-        return func(parents, attrs);
+        return (*func)(parents, attrs);
     }
 
     std::vector<int> infer_unary_shape(const std::vector<std::shared_ptr<Node>>& parents, const OpAttributes&) {

@@ -78,7 +78,15 @@ def _scalar_leaf(value: float, device: Device) -> Node:
     return node
 
 
+_binary_node = ormi_backend._binary
+_unary_node = ormi_backend._unary
+_ADD, _SUB, _MUL, _DIV = OpEnum.ADD, OpEnum.SUB, OpEnum.MUL, OpEnum.DIV
+
+
 class Tensor:
+    # Two attributes, no per-instance dict: every graph op creates one Tensor.
+    __slots__ = ("device", "_node")
+
     def __init__(self, data=None, device=None, requires_grad: bool = False, _node: Node | None = None,
                  dtype: str | None = None):
         self.device = _parse_device(device)
@@ -96,7 +104,7 @@ class Tensor:
     def _wrap(cls, node: Node, device: Device) -> "Tensor":
         """A Tensor over an existing node with an already-parsed device (the
         constructor's work minus argument parsing; every op result uses it)."""
-        t = cls.__new__(cls)
+        t = _new_tensor(cls)
         t.device = device
         t._node = node
         return t
@@ -120,9 +128,14 @@ class Tensor:
 
     @property
     def grad(self):
-        if self._node and self._node.grad:
-            return Tensor._wrap(self._node.grad, self.device)
-        return None
+        node = self._node
+        g = node.grad if node is not None else None
+        if g is None:
+            return None
+        t = _new_tensor(Tensor)
+        t.device = self.device
+        t._node = g
+        return t
 
     # ------------------------------------------------------------- operators
     def _ensure_tensor(self, other) -> "Tensor":
@@ -135,22 +148,49 @@ class Tensor:
         return Tensor(data=other, device=self.device)
 
     def _binary(self, op, a: "Tensor", b: "Tensor") -> "Tensor":
-        return Tensor._wrap(ormi_backend._binary(op, a._node, b._node), self.device)
+        t = _new_tensor(Tensor)
+        t.device = self.device
+        t._node = _binary_node(op, a._node, b._node)
+        return t
 
     def _unary(self, op) -> "Tensor":
-        return Tensor._wrap(ormi_backend._unary(op, self._node), self.device)
+        t = _new_tensor(Tensor)
+        t.device = self.device
+        t._node = _unary_node(op, self._node)
+        return t
+
+    def _other_node(self, other) -> Node:
+        """The node of a right operand: a Tensor on this device (the common case
+        first), a Python scalar (a cached 0-d leaf), or array data."""
+        if type(other) is Tensor and other.device is self.device:
+            return other._node
+        if type(other) is float or type(other) is int:
+            return _scalar_leaf(float(other), self.device)
+        return self._ensure_tensor(other)._node
 
     def __add__(self, other):
-        return self._binary(OpEnum.ADD, self, self._ensure_tensor(other))
+        t = _new_tensor(Tensor)
+        t.device = self.device
+        t._node = _binary_node(_ADD, self._node, self._other_node(other))
+        return t
 
     def __sub__(self, other):
-        return self._binary(OpEnum.SUB, self, self._ensure_tensor(other))
+        t = _new_tensor(Tensor)
+        t.device = self.device
+        t._node = _binary_node(_SUB, self._node, self._other_node(other))
+        return t
 
     def __mul__(self, other):
-        return self._binary(OpEnum.MUL, self, self._ensure_tensor(other))
+        t = _new_tensor(Tensor)
+        t.device = self.device
+        t._node = _binary_node(_MUL, self._node, self._other_node(other))
+        return t
 
     def __truediv__(self, other):
-        return self._binary(OpEnum.DIV, self, self._ensure_tensor(other))
+        t = _new_tensor(Tensor)
+        t.device = self.device
+        t._node = _binary_node(_DIV, self._node, self._other_node(other))
+        return t
 
     def __pow__(self, power):
         return self._binary(OpEnum.POW, self, self._ensure_tensor(power))
@@ -271,7 +311,7 @@ class Tensor:
         ormi_backend.compute_gradients(self._node)
 
     def zero_grad(self):
-        if self._node:
+        if self._node is not None:
             self._node.grad = None
 
     def zero_grad_graph(self):
@@ -281,6 +321,9 @@ class Tensor:
     def __repr__(self):
         state = "realized" if (self._node and self._node.is_realized) else "lazy"
         return f"Tensor(op={self.op.name}, shape={self.shape}, state={state}, device={self.device.type.name})"
+
+
+_new_tensor = object.__new__
 
 
 def realize_all(*tensors: Tensor) -> None:
