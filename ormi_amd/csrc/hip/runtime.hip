@@ -243,6 +243,11 @@ static int submit_launch(hipFunction_t fn, const uint32_t grid[3], const uint32_
                          const uint64_t* args, int nargs) {
     LaunchQueue& q = launch_queue();
     std::lock_guard<std::mutex> lock(q.submit_mu);
+    if (q.failed.load()) {  // an earlier queued launch failed: report it here, as the next call
+        std::lock_guard<std::mutex> el(q.err_mu);
+        q.failed.store(false);
+        return fail(ORMI_HIP_ERR_RUNTIME, q.error);
+    }
     if (!q.started) {
         q.device = state().device;
         q.worker = std::thread([&q] { q.run(); });

@@ -85,3 +85,23 @@ def test_queued_launch_rejects_bad_arguments(cabi, hip):
     assert cabi.ormi_hip_launch_queued(1, grid, block, 0, args, 129) == 3         # too many arguments
     assert b"ORMI_HIP_QUEUED_MAX_ARGS" in cabi.ormi_hip_last_error()
     assert cabi.ormi_hip_synchronize() == 0
+
+
+def test_kernel_with_more_arguments_than_the_queue_holds(ob, hip):
+    """A 130-leaf element-wise sum is one generated kernel with more than
+    ORMI_HIP_QUEUED_MAX_ARGS (128) parameters: it takes the synchronous launch
+    path, in order with the queued ones around it."""
+    from ormi_amd import Tensor
+
+    rng = np.random.default_rng(83)
+    arrs = [rng.integers(-8, 8, 256).astype(np.float32) for _ in range(130)]
+    ts = [Tensor(a, hip) for a in arrs]
+    before = (ts[0] * 2.0).realize()          # queued
+    total = ts[0]
+    for t in ts[1:]:
+        total = total + t
+    plan = ob._plan_kernel(total._node)
+    assert plan["source"].count("const float* __restrict__ L") >= 128
+    after = (total * 1.0).realize()           # the big kernel, then a queued map over it
+    assert np.array_equal(after.numpy(), np.sum(arrs, axis=0, dtype=np.float32))
+    assert np.array_equal(before.numpy(), arrs[0] * 2)
