@@ -7,6 +7,7 @@
 #include <condition_variable>
 #include <cstdlib>
 #include <cstring>
+#include <deque>
 #include <mutex>
 #include <thread>
 #include <string>
@@ -135,6 +136,106 @@ static int rtc_build(const char* source, const std::string& target, const char* 
     hiprtcGetCode(prog, code.data());
     hiprtcDestroyProgram(&prog);
     return ORMI_HIP_OK;
+}
+
+// ---------------------------------------------------------- upload ring --
+// Host-to-device copies are stream-ordered, not synchronous: the bytes are
+// copied into a pinned ring and an asynchronous copy from there is enqueued on
+// the null stream, so an upload neither waits for the kernels before it nor
+// blocks the host while the DMA runs. The caller's buffer is free on return.
+// Each enqueued piece records an event; a piece that would overwrite ring
+// bytes an earlier copy has not read yet waits on the newest such copy's
+// event (the stream is in order, so every older copy is then done as well).
+// Uploads larger than one piece go through in PIECE-sized parts, the host
+// copy of a part overlapping the DMA of the one before.
+struct UploadRing {
+    static constexpr size_t RING = 64u << 20;   // pinned bytes
+    static constexpr size_t PIECE = 16u << 20;  // largest single copy
+    static constexpr size_t ALIGN = 256;
+    static constexpr size_t MAX_PENDING = 4096;  // enqueued pieces not yet known complete
+    struct Region {
+        size_t beg, end;
+        hipEvent_t ev;
+    };
+    std::mutex mu;
+    char* base = nullptr;
+    bool unavailable = false;  // pinned allocation failed: copies are synchronous
+    size_t head = 0;
+    std::deque<Region> pending;  // in enqueue order
+    std::vector<hipEvent_t> spare;
+
+    int event(hipEvent_t* ev) {
+        if (!spare.empty()) {
+            *ev = spare.back();
+            spare.pop_back();
+            return ORMI_HIP_OK;
+        }
+        const hipError_t e = hipEventCreateWithFlags(ev, hipEventDisableTiming);
+        if (e != hipSuccess) return fail(ORMI_HIP_ERR_RUNTIME, std::string("upload ring: hipEventCreate: ") + hipGetErrorString(e));
+        return ORMI_HIP_OK;
+    }
+    void retire(size_t count) {  // the oldest count entries are complete
+        for (; count > 0; --count) {
+            spare.push_back(pending.front().ev);
+            pending.pop_front();
+        }
+    }
+    // Position of n bytes (n <= PIECE) that no pending copy still reads.
+    int reserve(size_t n, size_t* pos) {
+        size_t p = (head + ALIGN - 1) / ALIGN * ALIGN;
+        if (p + n > RING) p = 0;
+        // Completed entries at the front need no wait.
+        while (!pending.empty() && hipEventQuery(pending.front().ev) == hipSuccess) retire(1);
+        size_t last = SIZE_MAX;
+        for (size_t i = 0; i < pending.size(); ++i)
+            if (pending[i].beg < p + n && p < pending[i].end) last = i;
+        if (last == SIZE_MAX && pending.size() >= MAX_PENDING) last = 0;
+        if (last != SIZE_MAX) {
+            const hipError_t e = hipEventSynchronize(pending[last].ev);
+            if (e != hipSuccess) return fail(ORMI_HIP_ERR_RUNTIME, std::string("upload ring: hipEventSynchronize: ") + hipGetErrorString(e));
+            retire(last + 1);
+        }
+        *pos = p;
+        head = p + n;
+        return ORMI_HIP_OK;
+    }
+    int upload(char* dst, const char* src, size_t bytes) {
+        std::lock_guard<std::mutex> lock(mu);
+        if (!base && !unavailable) {
+            if (hipHostMalloc((void**)&base, RING, hipHostMallocDefault) != hipSuccess) {
+                base = nullptr;
+                unavailable = true;
+                (void)hipGetLastError();
+            }
+        }
+        if (unavailable) {
+            const hipError_t e = hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice);
+            if (e != hipSuccess) return fail(ORMI_HIP_ERR_RUNTIME, std::string("hipMemcpy: ") + hipGetErrorString(e));
+            return ORMI_HIP_OK;
+        }
+        for (size_t off = 0; off < bytes; off += PIECE) {
+            const size_t n = bytes - off < PIECE ? bytes - off : PIECE;
+            size_t p;
+            int rc = reserve(n, &p);
+            if (rc != ORMI_HIP_OK) return rc;
+            std::memcpy(base + p, src + off, n);
+            hipEvent_t ev;
+            if ((rc = event(&ev)) != ORMI_HIP_OK) return rc;
+            hipError_t e = hipMemcpyAsync(dst + off, base + p, n, hipMemcpyHostToDevice, 0);
+            if (e == hipSuccess) e = hipEventRecord(ev, 0);
+            if (e != hipSuccess) {
+                spare.push_back(ev);
+                return fail(ORMI_HIP_ERR_RUNTIME, std::string("upload ring: ") + hipGetErrorString(e));
+            }
+            pending.push_back({p, p + n, ev});
+        }
+        return ORMI_HIP_OK;
+    }
+};
+
+static UploadRing& upload_ring() {
+    static UploadRing* r = new UploadRing();  // never destroyed: pinned memory lives until exit
+    return *r;
 }
 
 // ----------------------------------------------------------- launch queue --
@@ -382,8 +483,7 @@ int ormi_hip_memcpy_h2d(void* dst, const void* src, size_t bytes) {
     if (!dst || !src) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_memcpy_h2d: null pointer");
     ORMI_ENSURE_INIT();
     ORMI_HIP_DRAIN();
-    ORMI_HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
-    return ORMI_HIP_OK;
+    return upload_ring().upload((char*)dst, (const char*)src, bytes);
 }
 
 int ormi_hip_memcpy_d2h(void* dst, const void* src, size_t bytes) {
