@@ -75,7 +75,10 @@ int ormi_hip_memset_d32(void* dst, uint32_t value, size_t count);    /* cuMemset
 /* Fill count elements of elem_bytes (1, 2, 4 or 8) with the pattern at value
  * (a kernel, so it is safe inside stream capture). fill_n for every dtype. */
 int ormi_hip_fill(void* dst, const void* value, size_t elem_bytes, size_t count);
-int ormi_hip_memcpy_h2d(void* dst, const void* src, size_t bytes);   /* cuMemcpyHtoD allocator.cu:94 */
+/* cuMemcpyHtoD allocator.cu:94, stream-ordered: src is copied into pinned
+ * staging before the call returns (the caller may reuse it at once) and the
+ * device copy runs after the work already on the stream, without blocking. */
+int ormi_hip_memcpy_h2d(void* dst, const void* src, size_t bytes);
 int ormi_hip_memcpy_d2h(void* dst, const void* src, size_t bytes);   /* cuMemcpyDtoH allocator.cu:90 */
 int ormi_hip_memcpy_d2d(void* dst, const void* src, size_t bytes);   /* cuMemcpyDtoD allocator.cu:62 */
 int ormi_hip_synchronize(void);
