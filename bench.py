@@ -526,8 +526,61 @@ def vendor_gemm(out_md: Path, cmd: str, rounds: int = 3, n: int = 20) -> None:
         tt, to = best[name]
         lines.append(f"| {name} | {g.M}x{g.N}x{g.K} | {tt:.1f} | {fl / tt / 1e6:.1f} | {to:.1f} | {fl / to / 1e6:.1f} | "
                      f"{to / tt:.3f} |")
+    del cases
+    # The C5 step both ways, alternating, each timed over sustained back-to-back
+    # steps (the clock the GEMMs run at falls as the card heats under load).
+    c5_steps = 20
+    t_c5 = [], []
+    for _ in range(rounds):
+        t_c5[0].append(torch_c5_step_ms(torch, c5_steps))
+        t_c5[1].append(bench_c5(ev, c5_steps)["step_ms"])
+    lines += ["", f"C5 MLP training step (BASELINE config 5), {c5_steps} back-to-back steps after 2 untimed, best of "
+              f"{rounds} rounds, the two alternating: PyTorch (hipBLASLt GEMMs, torch autograd, erf GELU, one kernel "
+              "per element-wise op) against this build's lazy graph (fused epilogues).", "",
+              "| C5 step | PyTorch ms | ours ms | ours / PyTorch time |", "|---|---|---|---|",
+              f"| 1024x(1024-4096-4096-1024) fp32 | {min(t_c5[0]):.3f} | {min(t_c5[1]):.3f} | "
+              f"{min(t_c5[1]) / min(t_c5[0]):.3f} |"]
     out_md.write_text("\n".join(lines) + "\n")
     print(out_md.read_text())
+
+
+def torch_c5_step_ms(torch, steps: int) -> float:
+    """The C5 step written in PyTorch on the same inputs as bench_c5 (seed 4):
+    fp32 matmuls (hipBLASLt), erf GELU, MSE, autograd, SGD lr 1e-3. For the
+    vendor comparison only."""
+    torch.backends.cuda.matmul.allow_tf32 = False
+    F = torch.nn.functional
+    rng = np.random.default_rng(4)
+    dims = [1024, 4096, 4096, 1024]
+    X = torch.from_numpy(rng.normal(0, 1, (1024, 1024)).astype(np.float32)).cuda()
+    Y = torch.from_numpy(rng.normal(0, 1, (1024, 1024)).astype(np.float32)).cuda()
+    ws = [torch.from_numpy(rng.uniform(-math.sqrt(6 / i), math.sqrt(6 / i), (i, o)).astype(np.float32)).cuda()
+          .requires_grad_() for i, o in zip(dims, dims[1:])]
+
+    def step(ws):
+        h = X
+        for i, w in enumerate(ws):
+            h = h @ w
+            if i < len(ws) - 1:
+                h = F.gelu(h)
+        d = h - Y
+        loss = (d * d).sum() * (1.0 / (1024 * 1024))
+        grads = torch.autograd.grad(loss, ws)
+        with torch.no_grad():
+            ws = [(w - g * 1e-3).requires_grad_() for w, g in zip(ws, grads)]
+        return loss, ws
+
+    for _ in range(2):
+        _, ws = step(ws)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with gc_paused():
+        a.record()
+        for _ in range(steps):
+            loss, ws = step(ws)
+        b.record()
+        torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps
 
 
 def bench_c5(ev: Events, steps: int) -> dict:
