@@ -544,6 +544,86 @@ def vendor_gemm(out_md: Path, cmd: str, rounds: int = 3, n: int = 20) -> None:
     print(out_md.read_text())
 
 
+def gemm_k_sweep(out_md: Path, cmd: str, rounds: int = 3, n: int = 10) -> None:
+    """Time of the fp32 GEMM against K at the C5 output shapes (1024x4096: one
+    128x128 tile per compute unit; 4096x4096: four), per epilogue, through
+    ormi_hip_gemm_ex. Every (K, epilogue) pair is timed in each of `rounds`
+    interleaved rounds (the clock depends on what ran before) with HIP events
+    over n launches; the best is kept. A line through K = 1024 and 4096 splits
+    each time into a fixed part per launch (launch, first loads, epilogue
+    stores, tail) and a part per 1024 of K (the main loop)."""
+    ev = Events()
+    lib = ev.lib
+
+    class Epi(ctypes.Structure):
+        _fields_ = [("kind", ctypes.c_int), ("fn", ctypes.c_int), ("form", ctypes.c_int), ("s", ctypes.c_void_p),
+                    ("d", ctypes.c_void_p), ("d_stride_m", ctypes.c_int64), ("d_stride_n", ctypes.c_int64),
+                    ("d_batch_stride", ctypes.c_int64 * 4), ("aux", ctypes.c_void_p)]
+
+    lib.ormi_hip_malloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
+    lib.ormi_hip_memcpy_h2d.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]
+    lib.ormi_hip_free.argtypes = [ctypes.c_void_p]
+    lib.ormi_hip_gemm_ex.argtypes = [ctypes.POINTER(_GemmDesc), ctypes.POINTER(Epi)]
+    lib.ormi_hip_last_error.restype = ctypes.c_char_p
+    rng = np.random.default_rng(0)
+    held = []
+
+    def put(a):
+        p = ctypes.c_void_p()
+        assert lib.ormi_hip_malloc(ctypes.byref(p), a.nbytes) == 0, lib.ormi_hip_last_error()
+        assert lib.ormi_hip_memcpy_h2d(p, a.ctypes.data, a.nbytes) == 0, lib.ormi_hip_last_error()
+        held.append(p)
+        return p
+
+    kmax, ks = 4096, (256, 1024, 4096)
+    lines = ["# fp32 GEMM: time against K, fixed cost per launch", "", f"Command (from the repo root): `{cmd}`", "",
+             f"NN layout, direct-load kernel (the default configuration), N(0, 1/64) operands. Best of {rounds} "
+             f"interleaved rounds of {n} launches (HIP events). fixed = the line through K = 1024 and K = 4096 "
+             "at K = 0; per 1024 K = its slope, against 2·M·N·1024 flop at 157.3 TFLOP/s. Epilogues: none; GELU "
+             "storing the product too (the forward layers); the SGD update reading and writing D (the weight "
+             "gradients).", "",
+             "| M x N | epilogue | " + " | ".join(f"K {k} us" for k in ks) + " | fixed us | per 1024 K us | loop vs peak |",
+             "|---|---|" + "---|" * (len(ks) + 3)]
+    for M, N in ((1024, 4096), (4096, 4096)):
+        A = put((rng.standard_normal((M, kmax)) / 64).astype(np.float32))
+        B = put((rng.standard_normal((kmax, N)) / 64).astype(np.float32))
+        C = put(np.zeros((M, N), np.float32))
+        X = put(np.zeros((M, N), np.float32))
+        D = put(np.ones((M, N), np.float32))
+        S = put(np.array([1e-3], np.float32))
+        epis = {"none": None, "GELU + product": Epi(kind=2, fn=7, form=0, aux=X),
+                "SGD (D - p s)": Epi(kind=1, fn=0, form=1, s=S, d=D, d_stride_m=N, d_stride_n=1)}
+        best = collections.defaultdict(lambda: math.inf)
+        for r in range(rounds):
+            for K in ks:
+                order = list(epis.items()) if r % 2 == 0 else list(epis.items())[::-1]
+                for name, e in order:
+                    g = _GemmDesc(dtype=0, M=M, N=N, K=K, a=A, a_stride_m=kmax, a_stride_k=1, b=B, b_stride_k=N,
+                                  b_stride_n=1, c=C)
+                    ep = ctypes.byref(e) if e is not None else None
+                    for _ in range(2):
+                        assert lib.ormi_hip_gemm_ex(ctypes.byref(g), ep) == 0, lib.ormi_hip_last_error()
+                    ev.sync()
+                    e0, e1 = ev.new(), ev.new()
+                    ev.record(e0)
+                    for _ in range(n):
+                        lib.ormi_hip_gemm_ex(ctypes.byref(g), ep)
+                    ev.record(e1)
+                    best[(K, name)] = min(best[(K, name)], ev.elapsed_ms(e0, e1) / n * 1e3)
+        for name in epis:
+            t1, t4 = best[(1024, name)], best[(4096, name)]
+            slope = (t4 - t1) / 3.0
+            fixed = t1 - slope
+            ideal = 2.0 * M * N * 1024 / (FP32_PEAK_TFLOPS * 1e6)
+            lines.append(f"| {M}x{N} | {name} | " + " | ".join(f"{best[(k, name)]:.1f}" for k in ks)
+                         + f" | {fixed:.1f} | {slope:.1f} | {ideal / slope:.1%} |")
+        for p in held:
+            lib.ormi_hip_free(p)
+        held.clear()
+    out_md.write_text("\n".join(lines) + "\n")
+    print(out_md.read_text())
+
+
 def torch_c5_step_ms(torch, steps: int) -> float:
     """The C5 step written in PyTorch on the same inputs as bench_c5 (seed 4):
     fp32 matmuls (hipBLASLt), erf GELU, MSE, autograd, SGD lr 1e-3. For the
@@ -753,40 +833,55 @@ def pmc_report(pmc_dir: Path, out: Path, cmd: str) -> None:
 
 
 def mfma_report(pmc_dir: Path, out: Path, cmd: str) -> None:
-    """MFMA utilisation per GEMM kernel from one `rocprofv3 --pmc
-    SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_MFMA SQ_LDS_BANK_CONFLICT GRBM_GUI_ACTIVE` run:
-    busy cycles summed over SIMDs / (SIMDs x the kernel's active cycles per XCC),
-    the formula of rocprofv3's derived MfmaUtil. SIMD and XCC counts come from the
-    run's agent info."""
+    """MFMA utilisation and shader clock per GEMM kernel from one `rocprofv3
+    --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_MFMA SQ_LDS_BANK_CONFLICT
+    GRBM_GUI_ACTIVE --kernel-trace` run: busy cycles summed over SIMDs / (SIMDs x
+    the kernel's active cycles per XCC), the formula of rocprofv3's derived
+    MfmaUtil; clock = active cycles per XCC / dispatch duration. Dispatches of
+    one kernel are grouped by their MFMA count (one group per GEMM shape). SIMD
+    and XCC counts come from the run's agent info."""
     agent = {}
     for f in sorted(pmc_dir.rglob("*agent_info.csv")):
         for r in csv.DictReader(open(f, newline="")):
             if r.get("Name", "").startswith("gfx"):
                 agent = r
     simds, xcc = int(agent.get("Simd_Count", 1024)), int(agent.get("Num_Xcc", 8))
-    per = collections.defaultdict(lambda: collections.defaultdict(list))
+    disp = collections.defaultdict(dict)  # (name, dispatch) -> counters, duration
     for f in sorted(pmc_dir.rglob("*counter_collection.csv")):
         for r in csv.DictReader(open(f, newline="")):
             name = r.get("Kernel_Name", "").strip()
-            if "gemm" in name:
-                per[name][r["Counter_Name"].strip()].append(float(r["Counter_Value"]))
+            if "gemm" not in name:
+                continue
+            d = disp[(name, r["Dispatch_Id"])]
+            d[r["Counter_Name"].strip()] = float(r["Counter_Value"])
+            if "End_Timestamp" in r:
+                d["us"] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3
+    groups = collections.defaultdict(list)
+    for (name, _), d in disp.items():
+        if d.get("GRBM_GUI_ACTIVE") and "SQ_VALU_MFMA_BUSY_CYCLES" in d:
+            groups[(name, d.get("SQ_INSTS_MFMA", 0.0))].append(d)
     lines = [
-        "# GEMM MFMA utilisation (rocprofv3 counters)", "",
+        "# GEMM MFMA utilisation and shader clock (rocprofv3 counters)", "",
         f"Command (from the repo root): `{cmd}`", "",
-        f"Device: {agent.get('Name', '?')}, {simds} SIMDs, {xcc} XCCs. util = SQ_VALU_MFMA_BUSY_CYCLES / "
-        f"(SIMDs x GRBM_GUI_ACTIVE / XCCs), averaged over dispatches; counters serialize kernels, so this is the "
-        "busy fraction of the matrix pipes while the kernel runs.", "",
-        "| kernel | dispatches | MFMA util | MFMA instructions / dispatch | LDS bank conflicts / dispatch |",
-        "|---|---|---|---|---|",
+        f"Device: {agent.get('Name', '?')}, {simds} SIMDs, {xcc} XCCs, datasheet engine clock "
+        f"{agent.get('Max_Engine_Clk_Fcompute', '?')} MHz. util = SQ_VALU_MFMA_BUSY_CYCLES / (SIMDs x "
+        "GRBM_GUI_ACTIVE / XCCs), averaged over dispatches; clock = GRBM_GUI_ACTIVE / XCCs / duration. Counters "
+        "serialize kernels, so these are the figures while the kernel runs. Dispatches are grouped by kernel and "
+        "MFMA count (one row per GEMM shape); the clock range runs from the first dispatch to the last.", "",
+        "| kernel | MFMA instructions / dispatch | dispatches | avg us | MFMA util | clock GHz (first - last, min) "
+        "| LDS bank conflicts / dispatch |",
+        "|---|---|---|---|---|---|---|",
     ]
-    for name, cs in sorted(per.items()):
-        busy, act = cs.get("SQ_VALU_MFMA_BUSY_CYCLES", []), cs.get("GRBM_GUI_ACTIVE", [])
-        if not busy or not act:
-            continue
-        util = sum(b / (simds * a / xcc) for b, a in zip(busy, act)) / len(busy)
-        mf = cs.get("SQ_INSTS_MFMA", [0.0])
-        bc = cs.get("SQ_LDS_BANK_CONFLICT", [0.0])
-        lines.append(f"| `{name[:110]}` | {len(busy)} | {util * 100:.1f}% | {sum(mf) / len(mf):.4g} | {sum(bc) / len(bc):.4g} |")
+    for (name, mf), ds in sorted(groups.items(), key=lambda kv: (kv[0][0], -kv[0][1])):
+        if mf == 0:
+            continue  # no matrix work (the split-K finish pass)
+        util = sum(d["SQ_VALU_MFMA_BUSY_CYCLES"] / (simds * d["GRBM_GUI_ACTIVE"] / xcc) for d in ds) / len(ds)
+        us = [d.get("us", float("nan")) for d in ds]
+        clk = [d["GRBM_GUI_ACTIVE"] / xcc / (d["us"] * 1e3) for d in ds if d.get("us")]
+        bc = sum(d.get("SQ_LDS_BANK_CONFLICT", 0.0) for d in ds) / len(ds)
+        clk_s = f"{clk[0]:.2f} - {clk[-1]:.2f}, {min(clk):.2f}" if clk else "-"
+        lines.append(f"| `{name[:110]}` | {mf:.4g} | {len(ds)} | {sum(us) / len(us):.1f} | {util * 100:.1f}% | "
+                     f"{clk_s} | {bc:.4g} |")
     out.write_text("\n".join(lines) + "\n")
     print(out.read_text())
 
@@ -870,17 +965,25 @@ def main():
                     help="summarize a rocprofv3 --pmc run of --only c4 into MFMA utilisation (no GPU needed)")
     ap.add_argument("--wave-report", nargs=3, metavar=("PMC_A", "PMC_B", "OUT_MD"),
                     help="summarize the two rocprofv3 --pmc passes of WAVE_COUNTERS over --only c4 (no GPU needed)")
+    ap.add_argument("--gemm-k-sweep", metavar="OUT_MD",
+                    help="fp32 GEMM time against K at the C5 output shapes: fixed cost per launch and loop rate")
     ap.add_argument("--vendor-gemm", metavar="OUT_MD",
                     help="time the C4/C5 GEMM shapes against torch.matmul (hipBLASLt) and write a markdown summary")
     args = ap.parse_args()
+    if args.gemm_k_sweep:
+        gemm_k_sweep(Path(args.gemm_k_sweep), f"python3 bench.py --gemm-k-sweep {args.gemm_k_sweep}")
+        return
     if args.vendor_gemm:
         vendor_gemm(Path(args.vendor_gemm), "python3 bench.py --vendor-gemm profiles/gemm_vs_hipblaslt.md")
         return
     if args.mfma_report:
-        mfma_report(Path(args.mfma_report[0]), Path(args.mfma_report[1]),
+        only = args.only or "c4"
+        out_md = Path(args.mfma_report[1])
+        mfma_report(Path(args.mfma_report[0]), out_md,
                     "rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_MFMA SQ_LDS_BANK_CONFLICT GRBM_GUI_ACTIVE "
-                    "-d gpurun_out/pmc_mfma -o run --output-format csv -- python3 bench.py --only c4 --steps 5 --warmup 1; "
-                    "python3 bench.py --mfma-report gpurun_out/pmc_mfma profiles/gemm_mfma_util.md")
+                    f"--kernel-trace -d gpurun_out/pmc_mfma_{only} -o run --output-format csv -- python3 bench.py "
+                    f"--only {only} --steps {30 if only == 'c5' else 5} --warmup 1; python3 bench.py --only {only} "
+                    f"--mfma-report gpurun_out/pmc_mfma_{only} {out_md.as_posix()}")
         return
     if args.wave_report:
         wave_report(args.wave_report[:2], Path(args.wave_report[2]),
