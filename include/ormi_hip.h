@@ -261,6 +261,60 @@ typedef struct ormi_reduce_desc {
 int ormi_hip_reduce_workspace_size(const ormi_reduce_desc* desc, size_t* bytes);
 int ormi_hip_reduce(const ormi_reduce_desc* desc);
 
+/* ------------------------------------------------------------------ map --
+ * Replaces the reference's element-wise JIT entry cuda::execute_jit(root)
+ * (csrc/backend/cuda/jit.cu:13-44) and the tape it compiles
+ * (csrc/backend/cuda/compiler.cu:22-51: realized nodes become leaves, every
+ * other node one instruction over earlier values). The caller passes that tape;
+ * the library generates one gfx950 kernel for it (128-bit accesses, row-aligned
+ * tiles, grid-stride over the compute units; the fusion scheduler's generator),
+ * caches it by structure, and launches it on its stream.
+ * Values: 0..num_leaves-1 are the leaves, num_leaves + k is insts[k]; an
+ * instruction reads only earlier values. Arithmetic is fp32 whatever the leaf
+ * dtypes (leaves are converted on load, as the reference computes in float).
+ * Leaf strides are in elements and aligned to the map's shape (0 on a
+ * broadcast dim, negative allowed); a scalar leaf reads its element 0 at every
+ * position (the reference's 1-element rule, csrc/backend/cpu/jit.cpp:24).
+ * Each output is a contiguous buffer of the map's shape holding one value,
+ * stored as its dtype; several outputs make one kernel that evaluates the tape
+ * once (multi-output fusion). Outputs must not overlap each other or a leaf.
+ * An empty shape (a zero extent) is a no-op. Buffers may be released through
+ * ormi_hip_free at once: it waits until the launch has been issued. */
+#define ORMI_MAP_MAX_DIMS 8
+#define ORMI_MAP_MAX_OUTPUTS 16
+enum {
+    ORMI_MAP_NEG = 0, ORMI_MAP_EXP = 1, ORMI_MAP_LOG = 2, ORMI_MAP_SIN = 3, ORMI_MAP_COS = 4,
+    ORMI_MAP_ADD = 5, ORMI_MAP_SUB = 6, ORMI_MAP_MUL = 7, ORMI_MAP_DIV = 8, ORMI_MAP_POW = 9,
+    ORMI_MAP_RELU = 10, ORMI_MAP_STEP = 11, ORMI_MAP_TANH = 12, ORMI_MAP_TANH_GRAD = 13,
+    ORMI_MAP_SIGMOID = 14, ORMI_MAP_SIGMOID_GRAD = 15, ORMI_MAP_GELU = 16, ORMI_MAP_GELU_GRAD = 17,
+    ORMI_MAP_EQ = 18,   /* 1.0f where a == b, else 0.0f */
+    ORMI_MAP_CAST = 19  /* round to bf16 or f16 (f32: unchanged); integer results come from an output dtype */
+};
+typedef struct ormi_map_leaf {
+    const void* ptr;
+    int         dtype;                          /* ORMI_DTYPE_*                       */
+    int         scalar;                         /* nonzero: element 0 everywhere      */
+    int64_t     strides[ORMI_MAP_MAX_DIMS];     /* elements, aligned to shape         */
+} ormi_map_leaf;
+typedef struct ormi_map_inst {
+    int op;                                     /* ORMI_MAP_*                         */
+    int a, b;                                   /* operand values; b only for binary  */
+    int dtype;                                  /* ORMI_MAP_CAST: ORMI_DTYPE_BF16/F16/F32 */
+} ormi_map_inst;
+typedef struct ormi_map_desc {
+    int                  ndim;                  /* 0..ORMI_MAP_MAX_DIMS               */
+    int                  shape[ORMI_MAP_MAX_DIMS];
+    int                  num_leaves;
+    const ormi_map_leaf* leaves;
+    int                  num_insts;
+    const ormi_map_inst* insts;
+    int                  num_outputs;           /* 1..ORMI_MAP_MAX_OUTPUTS            */
+    const int*           output_values;         /* value stored by each output        */
+    void* const*         outputs;
+    const int*           output_dtypes;         /* ORMI_DTYPE_*                       */
+} ormi_map_desc;
+int ormi_hip_map(const ormi_map_desc* desc);
+
 /* ---------------------------------------------------------------- timing --
  * HIP events on the library's stream, for measuring kernel time from
  * outside (benchmarks). */

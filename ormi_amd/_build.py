@@ -47,9 +47,11 @@ CORE_SOURCES = sorted(
     + [p for p in (CSRC / "backend").rglob("*.cpp")]
 )
 HIP_SOURCES = sorted((CSRC / "hip").glob("*.hip"))
-# Host C++ of the device layer: the C-ABI reduction entry and the code generator
-# it shares with the core (a second, hidden-symbol copy inside libormi_hip.so).
-DEVICE_HOST_SOURCES = [CSRC / "hip" / "reduce_entry.cpp", CSRC / "backend" / "hip" / "codegen.cpp",
+# Host C++ of the device layer: the C-ABI reduction and map entries and the code
+# generator they share with the core (a second, hidden-symbol copy inside
+# libormi_hip.so).
+DEVICE_HOST_SOURCES = [CSRC / "hip" / "reduce_entry.cpp", CSRC / "hip" / "map_entry.cpp",
+                       CSRC / "backend" / "hip" / "codegen.cpp",
                        CSRC / "core" / "dtype.cpp", CSRC / "core" / "ops.cpp"]
 BINDING_SOURCES = sorted((CSRC / "bindings").glob("*.cpp"))
 ORACLE_SOURCES = sorted((ORACLE / "cpu_backend").glob("*.cpp"))

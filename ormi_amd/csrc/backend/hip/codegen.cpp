@@ -38,6 +38,33 @@
 namespace ormi::hip {
     using ops::OpEnum;
 
+    const LoweringFunc* builtin_lowering(OpEnum op) {
+        using A = const std::vector<std::string>&;
+        static const std::unordered_map<OpEnum, LoweringFunc> table = {
+            {OpEnum::ADD, [](A v) { return "(" + v[0] + " + " + v[1] + ")"; }},
+            {OpEnum::SUB, [](A v) { return "(" + v[0] + " - " + v[1] + ")"; }},
+            {OpEnum::MUL, [](A v) { return "(" + v[0] + " * " + v[1] + ")"; }},
+            {OpEnum::DIV, [](A v) { return "(" + v[0] + " / " + v[1] + ")"; }},
+            {OpEnum::POW, [](A v) { return "powf(" + v[0] + ", " + v[1] + ")"; }},
+            {OpEnum::EQ, [](A v) { return "ormi_eq(" + v[0] + ", " + v[1] + ")"; }},
+            {OpEnum::NEG, [](A v) { return "(-" + v[0] + ")"; }},
+            {OpEnum::EXP, [](A v) { return "ormi_exp(" + v[0] + ")"; }},
+            {OpEnum::LOG, [](A v) { return "logf(" + v[0] + ")"; }},
+            {OpEnum::SIN, [](A v) { return "sinf(" + v[0] + ")"; }},
+            {OpEnum::COS, [](A v) { return "cosf(" + v[0] + ")"; }},
+            {OpEnum::RELU, [](A v) { return "ormi_relu(" + v[0] + ")"; }},
+            {OpEnum::STEP, [](A v) { return "ormi_step(" + v[0] + ")"; }},
+            {OpEnum::TANH, [](A v) { return "ormi_tanh(" + v[0] + ")"; }},
+            {OpEnum::TANH_GRAD, [](A v) { return "ormi_tanh_grad(" + v[0] + ")"; }},
+            {OpEnum::SIGMOID, [](A v) { return "ormi_sigmoid(" + v[0] + ")"; }},
+            {OpEnum::SIGMOID_GRAD, [](A v) { return "ormi_sigmoid_grad(" + v[0] + ")"; }},
+            {OpEnum::GELU, [](A v) { return "ormi_gelu(" + v[0] + ")"; }},
+            {OpEnum::GELU_GRAD, [](A v) { return "ormi_gelu_grad(" + v[0] + ")"; }},
+        };
+        auto it = table.find(op);
+        return it == table.end() ? nullptr : &it->second;
+    }
+
     static const char* kDeviceHeader =
 #include "ormi_device_text.inc"
         ;

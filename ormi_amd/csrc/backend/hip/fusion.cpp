@@ -34,29 +34,17 @@ namespace ormi::hip {
     }
 
     namespace {
-        struct RegisterLowering {
-            RegisterLowering(OpEnum op, LoweringFunc f) { HIPLoweringRegistry::register_func(op, std::move(f)); }
-        };
-        using A = const std::vector<std::string>&;
-        RegisterLowering l_add(OpEnum::ADD, [](A v) { return "(" + v[0] + " + " + v[1] + ")"; });
-        RegisterLowering l_sub(OpEnum::SUB, [](A v) { return "(" + v[0] + " - " + v[1] + ")"; });
-        RegisterLowering l_mul(OpEnum::MUL, [](A v) { return "(" + v[0] + " * " + v[1] + ")"; });
-        RegisterLowering l_div(OpEnum::DIV, [](A v) { return "(" + v[0] + " / " + v[1] + ")"; });
-        RegisterLowering l_pow(OpEnum::POW, [](A v) { return "powf(" + v[0] + ", " + v[1] + ")"; });
-        RegisterLowering l_eq(OpEnum::EQ, [](A v) { return "ormi_eq(" + v[0] + ", " + v[1] + ")"; });
-        RegisterLowering l_neg(OpEnum::NEG, [](A v) { return "(-" + v[0] + ")"; });
-        RegisterLowering l_exp(OpEnum::EXP, [](A v) { return "ormi_exp(" + v[0] + ")"; });
-        RegisterLowering l_log(OpEnum::LOG, [](A v) { return "logf(" + v[0] + ")"; });
-        RegisterLowering l_sin(OpEnum::SIN, [](A v) { return "sinf(" + v[0] + ")"; });
-        RegisterLowering l_cos(OpEnum::COS, [](A v) { return "cosf(" + v[0] + ")"; });
-        RegisterLowering l_relu(OpEnum::RELU, [](A v) { return "ormi_relu(" + v[0] + ")"; });
-        RegisterLowering l_step(OpEnum::STEP, [](A v) { return "ormi_step(" + v[0] + ")"; });
-        RegisterLowering l_tanh(OpEnum::TANH, [](A v) { return "ormi_tanh(" + v[0] + ")"; });
-        RegisterLowering l_tanhg(OpEnum::TANH_GRAD, [](A v) { return "ormi_tanh_grad(" + v[0] + ")"; });
-        RegisterLowering l_sig(OpEnum::SIGMOID, [](A v) { return "ormi_sigmoid(" + v[0] + ")"; });
-        RegisterLowering l_sigg(OpEnum::SIGMOID_GRAD, [](A v) { return "ormi_sigmoid_grad(" + v[0] + ")"; });
-        RegisterLowering l_gelu(OpEnum::GELU, [](A v) { return "ormi_gelu(" + v[0] + ")"; });
-        RegisterLowering l_gelug(OpEnum::GELU_GRAD, [](A v) { return "ormi_gelu_grad(" + v[0] + ")"; });
+        // The built-in lowerings go into the registry at load time; a backend
+        // extension may register more (or replace one) afterwards.
+        struct RegisterBuiltins {
+            RegisterBuiltins() {
+                for (OpEnum op : {OpEnum::ADD, OpEnum::SUB, OpEnum::MUL, OpEnum::DIV, OpEnum::POW, OpEnum::EQ, OpEnum::NEG,
+                                  OpEnum::EXP, OpEnum::LOG, OpEnum::SIN, OpEnum::COS, OpEnum::RELU, OpEnum::STEP,
+                                  OpEnum::TANH, OpEnum::TANH_GRAD, OpEnum::SIGMOID, OpEnum::SIGMOID_GRAD, OpEnum::GELU,
+                                  OpEnum::GELU_GRAD})
+                    HIPLoweringRegistry::register_func(op, *builtin_lowering(op));
+            }
+        } register_builtins;
     }
 
     static bool cast_target_is_float(const Node& n) {

@@ -2,7 +2,8 @@
 // Depends on the dtype and op enums only (no graph types), so the generator is
 // built twice: into the host core, where the fusion scheduler feeds it, and
 // into the device layer libormi_hip.so, where ormi_hip_reduce feeds it a plain
-// strided input. Both emit the same kernels for the same request.
+// strided input and ormi_hip_map a caller's tape. Both emit the same kernels
+// for the same request.
 #pragma once
 #include <cstdint>
 #include <functional>
@@ -26,6 +27,11 @@ namespace ormi::hip {
     // Operand expressions -> HIP C expression of one op (the reference's
     // CUDALoweringRegistry shape, csrc/backend/cuda/lowering_registry.h:11-38).
     using LoweringFunc = std::function<std::string(const std::vector<std::string>&)>;
+    // The built-in lowering of an element-wise op (device functions of
+    // ormi_device.h), or nullptr for an op without one (CAST is lowered by the
+    // generator itself). Every path that builds a tape takes its lowerings from
+    // here, so the same tape gives the same kernel text.
+    const LoweringFunc* builtin_lowering(ops::OpEnum op);
 
     // ---------------------------------------------------------- fusion IR --
     // A realized input of a fused kernel, with its strides aligned to the
@@ -135,12 +141,4 @@ namespace ormi::hip {
     // Compile (cached) and launch.
     void launch(const KernelLaunch& k);
 
-    // Source text of a planned kernel: a plan that hit the kernel cache after
-    // its kernel was compiled carries only the handle, and this returns the
-    // text the cache kept (diagnostics and compile-only checks).
-    std::string kernel_source(const KernelLaunch& k);
-    // hipRTC options every generated kernel is compiled with.
-    const std::vector<std::string>& rtc_options();
-    // Compile (cached) and launch.
-    void launch(const KernelLaunch& k);
 }
