@@ -12,19 +12,45 @@ namespace ormi {
     // reference's recursive build_topo (csrc/core/autograd.cpp:12-22) without
     // its recursion-depth limit. Raw pointers: root keeps every node it reaches
     // alive for the walk (no reference-count traffic per step).
+    // The visited set is a plain array while the graph is small (a training
+    // step's graph is tens of nodes: a linear scan beats hashing and its
+    // per-insert allocations) and a hash set past kLinear nodes.
+    namespace {
+        struct VisitedSet {
+            static constexpr size_t kLinear = 48;
+            std::vector<Node*> small;
+            std::unordered_set<Node*> big;
+            VisitedSet() { small.reserve(kLinear); }
+            bool insert(Node* n) {  // true when n was not in the set
+                if (big.empty()) {
+                    for (Node* m : small)
+                        if (m == n) return false;
+                    if (small.size() < kLinear) {
+                        small.push_back(n);
+                        return true;
+                    }
+                    big.reserve(4 * kLinear);
+                    big.insert(small.begin(), small.end());
+                }
+                return big.insert(n).second;
+            }
+        };
+    }
+
     static std::vector<Node*> topo_nodes(Node* root) {
         std::vector<Node*> topo;
         if (!root) return topo;
-        std::unordered_set<Node*> visited;
-        visited.reserve(64);
+        topo.reserve(32);
+        VisitedSet visited;
         std::vector<std::pair<Node*, size_t>> stack;
+        stack.reserve(32);
         visited.insert(root);
         stack.push_back({root, 0});
         while (!stack.empty()) {
             auto& [node, next] = stack.back();
             if (next < node->parents.size()) {
                 Node* p = node->parents[next++].get();
-                if (p && visited.insert(p).second) stack.push_back({p, 0});
+                if (p && visited.insert(p)) stack.push_back({p, 0});
             } else {
                 topo.push_back(node);
                 stack.pop_back();

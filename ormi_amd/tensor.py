@@ -311,8 +311,9 @@ class Tensor:
         ormi_backend.compute_gradients(self._node)
 
     def zero_grad(self):
-        if self._node is not None:
-            self._node.grad = None
+        node = self._node
+        if node is not None:
+            node._clear_grad()
 
     def zero_grad_graph(self):
         if self._node:
