@@ -63,6 +63,7 @@ namespace {
         r->shape.assign(d->shape, d->shape + d->ndim);
         for (int e : r->shape) {
             if (e < 0) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_map: negative extent");
+            if (e > 0 && r->numel > (1LL << 62) / e) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_map: more than 2^62 elements");
             r->numel *= e;
         }
         if (d->num_leaves < 0 || (d->num_leaves > 0 && !d->leaves))

@@ -55,6 +55,7 @@ namespace {
         r->shape.assign(d->shape, d->shape + d->ndim);
         for (int e : r->shape) {
             if (e < 0) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_reduce: negative extent");
+            if (e > 0 && r->in_numel > (1LL << 62) / e) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_reduce: more than 2^62 elements");
             r->in_numel *= e;
         }
         std::vector<bool> reduced(d->ndim, d->naxes == 0);

@@ -222,10 +222,17 @@ struct UploadRing {
             hipEvent_t ev;
             if ((rc = event(&ev)) != ORMI_HIP_OK) return rc;
             hipError_t e = hipMemcpyAsync(dst + off, base + p, n, hipMemcpyHostToDevice, 0);
-            if (e == hipSuccess) e = hipEventRecord(ev, 0);
             if (e != hipSuccess) {
                 spare.push_back(ev);
-                return fail(ORMI_HIP_ERR_RUNTIME, std::string("upload ring: ") + hipGetErrorString(e));
+                return fail(ORMI_HIP_ERR_RUNTIME, std::string("upload ring: hipMemcpyAsync: ") + hipGetErrorString(e));
+            }
+            e = hipEventRecord(ev, 0);
+            if (e != hipSuccess) {
+                // The copy is queued but untracked: wait for it, so no later
+                // piece overwrites ring bytes it has not read yet.
+                spare.push_back(ev);
+                (void)hipStreamSynchronize(0);
+                return fail(ORMI_HIP_ERR_RUNTIME, std::string("upload ring: hipEventRecord: ") + hipGetErrorString(e));
             }
             pending.push_back({p, p + n, ev});
         }

@@ -72,6 +72,7 @@ def mapc(cabi):
 @pytest.mark.parametrize("case,msg", [
     (dict(ndim=9), b"ndim must be 0..8"),
     (dict(shape=(4, -1)), b"negative extent"),
+    (dict(shape=(1 << 30,) * 3), b"more than 2^62 elements"),
     (dict(leaf_dtype=9), b"leaf 0 has an unknown dtype"),
     (dict(op=77), b"instruction 0 has an unknown op"),
     (dict(a=1), b"operand a must be an earlier value"),

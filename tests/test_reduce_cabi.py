@@ -48,6 +48,7 @@ def desc(op, dtype, ptr, shape, strides, axes, out, ws=None, ws_bytes=0):
     (dict(axes=(2,)), b"axis out of range"),
     (dict(axes=(1, 1)), b"repeated axis"),
     (dict(shape=(4, -1)), b"negative extent"),
+    (dict(shape=(1 << 30, 1 << 30, 1 << 30)), b"more than 2^62 elements"),
 ])
 def test_reduce_descriptor_validation(cabi, fields, msg):
     base = dict(op=SUM, in_dtype=F32, shape=(4, 6), axes=(1,))
