@@ -54,7 +54,7 @@ def test_reduce_descriptor_validation(cabi, fields, msg):
     base = dict(op=SUM, in_dtype=F32, shape=(4, 6), axes=(1,))
     base.update(fields)
     shape = base["shape"]
-    d = desc(base["op"], base["in_dtype"], 0x1000, shape, [6, 1][:len(shape)], base["axes"], 0x2000)
+    d = desc(base["op"], base["in_dtype"], 0x1000, shape, [6] * (len(shape) - 1) + [1], base["axes"], 0x2000)
     if "ndim" in fields:
         d.ndim = fields["ndim"]
     if "naxes" in fields:
