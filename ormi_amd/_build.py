@@ -5,6 +5,8 @@ Outputs
   ormi_amd/lib/libormi_core.so     graph, autograd, runtime, HIP backend host code (g++)
   ormi_amd/ormi_backend*.so        pybind11 module (g++)
   oracle/_build/libormi_cpu_oracle.so  CPU oracle, test infrastructure only (g++)
+  oracle/_ref/libormi_ref.so       the reference's own CPU path, a second checker (make -f
+                                   oracle/Makefile.ref; only where /root/reference exists)
 
 Run `python -m ormi_amd._build` (or __graft_entry__.build()). Every call
 recompiles everything; objects go to ormi_amd/_build/.
@@ -26,6 +28,7 @@ LIBDIR = PKG / "lib"
 OBJDIR = PKG / "_build"
 GENDIR = OBJDIR / "gen"
 ORACLE = ROOT / "oracle"
+REF_CSRC = Path("/root/reference/ormi-core/csrc")  # reference sources: read and compiled, never copied
 ORACLE_OUT = ORACLE / "_build"
 
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
@@ -63,8 +66,8 @@ CORE_LIB = LIBDIR / "libormi_core.so"
 ORACLE_LIB = ORACLE_OUT / "libormi_cpu_oracle.so"
 
 
-def _run(cmd: list[str]) -> None:
-    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+def _run(cmd: list[str], cwd: Path | None = None) -> None:
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True, cwd=cwd)
     out = "\n".join(l for l in proc.stdout.splitlines() if "packed-fp32-ops" not in l)
     if proc.returncode != 0:
         raise RuntimeError(f"build step failed ({proc.returncode}): {' '.join(cmd)}\n{out}")
@@ -157,6 +160,10 @@ def build(verbose: bool = False, incremental: bool = False) -> None:
     rel_lib = os.path.relpath(LIBDIR, ORACLE_OUT)
     _run(["g++", "-shared", *map(str, oracle), "-o", str(ORACLE_LIB), f"-L{LIBDIR}", "-lormi_core",
           f"-Wl,-rpath,$ORIGIN/{rel_lib}", "-Wl,--no-undefined"])
+    # The reference's own CPU path, a second checker for the oracle, where its
+    # sources are (this container; other machines use the prebuilt file).
+    if REF_CSRC.is_dir():
+        _run(["make", "-s", "-f", "oracle/Makefile.ref", f"REF={REF_CSRC}"] + ([] if incremental else ["-B"]), cwd=ROOT)
 
 
 def built() -> bool:
