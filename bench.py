@@ -176,9 +176,10 @@ def cpu_baseline_c2(target_s: float = 10.0) -> dict:
 def cpu_baselines_extra() -> dict:
     """The reference's CPU path beside the other configs, each on a bounded sample
     of a few seconds: the oracle (restatement of Ormi's CPU backend, one core, as
-    its loops are unthreaded) for C1 and the C3 reductions, and numpy float32
-    matmul (its bundled OpenBLAS, all host threads) standing in for the
-    reference's cblas_sgemm for the C4 GEMMs."""
+    its loops are unthreaded) for C1 and the C3 reductions; where the
+    reference's own CPU path is built (oracle/_ref), it too for the C3 sums; and
+    numpy float32 matmul (its bundled OpenBLAS, all host threads) standing in for
+    the reference's cblas_sgemm for the C4 GEMMs."""
     import oracle
     from ormi_amd import Tensor
 
@@ -221,6 +222,15 @@ def cpu_baselines_extra() -> dict:
         t = timed(fn, 2)
         c3[k] = {"ms": round(t * 1e3, 2), "GB/s": round(nb / t / 1e9, 4)}
     out["C3"] = c3
+    if oracle.ref_available():
+        # The reference's own CPU path (oracle/_ref, built from its sources) on
+        # the C3 ops it has: the row sum behind the mean, and the column sum.
+        # Each call also copies the sample in and the result out (about 1% of it).
+        ref = {"kind": "reference", "cores": 1, "sample": c3["sample"]}
+        for k, axis in (("row_sum", 1), ("col_sum", 0)):
+            t = timed(lambda axis=axis: oracle.ref_run([(x, False)], [("SUM", 0, -1, [axis], 0)], [1]), 2)
+            ref[k] = {"ms": round(t * 1e3, 2), "GB/s": round(nb / t / 1e9, 4)}
+        out["C3_reference"] = ref
     try:
         from threadpoolctl import threadpool_info
 
