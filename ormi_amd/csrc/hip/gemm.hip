@@ -1114,9 +1114,9 @@ static int gemm_run(const ormi_gemm_desc* d, const ormi_gemm_epilogue* epi_in, b
     long long batch = 1;
     for (int i = 0; i < d->batch_ndim; ++i) {
         if (d->batch_shape[i] <= 0) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_gemm: batch extents must be positive");
-        batch *= d->batch_shape[i];
+        batch *= d->batch_shape[i];  // <= 65535 * (2^31 - 1) before the check below: no overflow
+        if (batch > 65535) return fail(ORMI_HIP_ERR_UNSUPPORTED, "ormi_hip_gemm: more than 65535 batches");
     }
-    if (batch > 65535) return fail(ORMI_HIP_ERR_UNSUPPORTED, "ormi_hip_gemm: more than 65535 batches");
     if ((long long)d->M * d->N == 0) return ORMI_HIP_OK;
     // With K == 0 the operands hold no elements (an empty buffer may have no
     // address) and are never read.

@@ -67,6 +67,11 @@ def test_gemm_descriptor_validation(cabi):
     assert cabi.ormi_hip_gemm(ctypes.byref(d)) == ORMI_HIP_ERR_INVALID and b"null" in cabi.ormi_hip_last_error()
     d = GemmDesc(dtype=0, M=4, N=4, K=0)  # K == 0 reads no operand, but C is written
     assert cabi.ormi_hip_gemm(ctypes.byref(d)) == ORMI_HIP_ERR_INVALID and b"null" in cabi.ormi_hip_last_error()
+    # batch extents whose product overflows 64 bits are refused, not wrapped
+    d = GemmDesc(dtype=0, M=4, N=4, K=4, batch_ndim=4)
+    for i in range(4):
+        d.batch_shape[i] = 1 << 30
+    assert cabi.ormi_hip_gemm(ctypes.byref(d)) == ORMI_HIP_ERR_UNSUPPORTED and b"65535" in cabi.ormi_hip_last_error()
 
 
 class GemmEpilogue(ctypes.Structure):
