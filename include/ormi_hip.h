@@ -278,6 +278,7 @@ int ormi_hip_reduce(const ormi_reduce_desc* desc);
  * Each output is a contiguous buffer of the map's shape holding one value,
  * stored as its dtype; several outputs make one kernel that evaluates the tape
  * once (multi-output fusion). Outputs must not overlap each other or a leaf.
+ * Every leaf and output address is aligned to its element size.
  * An empty shape (a zero extent) is a no-op. Buffers may be released through
  * ormi_hip_free at once: it waits until the launch has been issued. */
 #define ORMI_MAP_MAX_DIMS 8

@@ -10,6 +10,7 @@
 // text on either path, then launches it through the library's queue.
 //
 // Built with -fvisibility=hidden: only the extern "C" function is exported.
+#include <cstdint>
 #include <exception>
 #include <string>
 #include <vector>
@@ -80,6 +81,8 @@ namespace {
             Leaf L;
             if (!to_dtype(s.dtype, &L.dtype)) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_map: leaf " + std::to_string(i) + " has an unknown dtype");
             if (!s.ptr && r->numel > 0) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_map: leaf " + std::to_string(i) + " is null");
+            if ((uintptr_t)s.ptr % ormi::dtype_size(L.dtype) != 0)
+                return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_map: leaf " + std::to_string(i) + " is not aligned to its element size");
             L.ptr = s.ptr;
             L.scalar = s.scalar != 0;
             L.st.assign(d->ndim, 0);
@@ -114,6 +117,8 @@ namespace {
             DType dt;
             if (!to_dtype(d->output_dtypes[o], &dt)) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_map: output " + std::to_string(o) + " has an unknown dtype");
             if (!d->outputs[o] && r->numel > 0) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_map: output " + std::to_string(o) + " is null");
+            if ((uintptr_t)d->outputs[o] % ormi::dtype_size(dt) != 0)
+                return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_map: output " + std::to_string(o) + " is not aligned to its element size");
             e.roots.push_back(v);
             r->outs.push_back(d->outputs[o]);
             r->out_dtypes.push_back(dt);

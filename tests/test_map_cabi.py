@@ -83,12 +83,14 @@ def mapc(cabi):
     (dict(num_outputs=0), b"num_outputs must be 1..16"),
     (dict(null_leaf=True), b"leaf 0 is null"),
     (dict(null_out=True), b"output 0 is null"),
+    (dict(leaf_ptr=0x1002), b"leaf 0 is not aligned to its element size"),
+    (dict(out_ptr=0x2001), b"output 0 is not aligned to its element size"),
 ])
 def test_map_rejects_bad_descriptors(mapc, case, msg):
     shape = case.get("shape", (4, 8))
-    leaves = [(None if case.get("null_leaf") else 0x1000, case.get("leaf_dtype", F32), False, (8, 1))]
+    leaves = [(None if case.get("null_leaf") else case.get("leaf_ptr", 0x1000), case.get("leaf_dtype", F32), False, (8, 1))]
     insts = [(case.get("op", "NEG"), case.get("a", 0), case.get("b", 0), case.get("cast", F32))]
-    outs = [(case.get("out_value", 1), None if case.get("null_out") else 0x2000, case.get("out_dtype", F32))]
+    outs = [(case.get("out_value", 1), None if case.get("null_out") else case.get("out_ptr", 0x2000), case.get("out_dtype", F32))]
     d, keep = make_desc(shape, leaves, insts, outs)
     if "ndim" in case:
         d.ndim = case["ndim"]
