@@ -254,17 +254,19 @@ def cpu_baselines_extra() -> dict:
     return out
 
 
-def traffic_from_profile(kernel: str):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary
-    (profiles/hbm_traffic.md, written by `bench.py --pmc-report`), or None."""
+def traffic_from_profile(label: str):
+    """HBM bytes per launch (read + write) of the row `label` of the committed
+    rocprofv3 --pmc summary (profiles/hbm_traffic.md, written by
+    `bench.py --pmc-report`: columns kernel, fetch KiB, write KiB, read bytes,
+    write bytes, ...), or None when the summary has no such row."""
     f = ROOT / "profiles" / "hbm_traffic.md"
     if not f.exists():
         return None
     for line in f.read_text().splitlines():
         cells = [c.strip() for c in line.strip().strip("|").split("|")]
-        if len(cells) >= 4 and cells[0] == kernel:
+        if len(cells) >= 5 and cells[0] == label:
             try:
-                return int(cells[3])
+                return int(cells[3]) + int(cells[4])
             except ValueError:
                 return None
     return None
@@ -307,7 +309,7 @@ def bench_c2(args, ev: Events) -> dict:
         "step_s": step_s,
         "value": nbytes / step_s / 1e9,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile("c2_fused_map"),
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile("C2 fused map"),
                      "kernel_us": round(kernel_ms * 1e3, 2), "bytes_per_launch": nbytes, "launches_timed": n},
     }
 
