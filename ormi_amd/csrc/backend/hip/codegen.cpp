@@ -257,6 +257,9 @@ namespace ormi::hip {
             int vec_dim = -1;  // dim whose coordinate advances by VEC
             int rows = 0;      // map tile alignment to the last dim (plan_map_multi)
             bool nt_loads = false;
+            // Output dtypes of a map: bf16 and fp16 share a storage type, so the
+            // argument list alone does not tell their stores apart.
+            std::vector<DType> out_dtypes;
             ArgList args;
             std::unique_ptr<std::ostringstream> body_;  // created when a source is generated
 
@@ -531,6 +534,12 @@ namespace ormi::hip {
                 append_int(s, d.j);
                 s += ';';
             }
+            // Element types, which the storage types above do not fix: bf16
+            // and fp16 are both unsigned short, but load and store differently.
+            s += '|';
+            for (const auto& L : g.e.leaves) s += char('a' + (int)L.dtype);
+            s += '/';
+            for (DType dt : g.out_dtypes) s += char('a' + (int)dt);
             s += '|';
             for (const auto& d : g.c.dims) s += char('0' + (int)d.group);
             s += '|';
@@ -663,6 +672,7 @@ namespace ormi::hip {
         const Tuning& tn = tuning();
         const int block = 256, unroll = tn.map_unroll;
         Gen g(expr);
+        g.out_dtypes = out_dtypes;
         g.nt_loads = tn.map_nt_loads;
         g.want_off32 = tn.map_off32;
         for (int s : shape) g.c.dims.push_back({(long long)s, G_M});

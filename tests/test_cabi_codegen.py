@@ -339,3 +339,24 @@ def test_column_kernels_keyed_by_column_waves(ob, cpu, cabi):
             rc, _ = _compile_only(cabi, d["source"], ob._rtc_options())
             assert rc == ORMI_HIP_OK, (shape, red, cabi.ormi_hip_last_error())
     assert all(len(names) == 3 for names in seen.values()), seen
+
+
+def test_kernel_cache_tells_bf16_from_f16(ob, cpu):
+    """bf16 and fp16 share a storage type (unsigned short). The generator's
+    kernel cache must still key on the element type: a bf16 leaf (or output)
+    planned after an otherwise identical fp16 one gets its own kernel, with its
+    own conversion. Before the element types were in the key, the second plan
+    reused the first kernel and read bf16 bits as fp16."""
+    from ormi_amd import Tensor
+
+    a = np.linspace(-2, 2, 8 * 64, dtype=np.float32).reshape(8, 64)
+    p16 = ob._plan_kernel(Tensor(a, "cpu", dtype="float16").tanh()._node)
+    pbf = ob._plan_kernel(Tensor(a, "cpu", dtype="bfloat16").tanh()._node)
+    assert p16["name"] != pbf["name"]
+    assert "ormi_f16_to_f32(" in p16["source"] and "ormi_bf16_to_f32(" not in p16["source"].split("extern")[1]
+    assert "ormi_bf16_to_f32(" in pbf["source"].split("extern")[1]
+    o16 = ob._plan_kernel((Tensor(a, "cpu") * 2.0).astype("float16")._node)
+    obf = ob._plan_kernel((Tensor(a, "cpu") * 2.0).astype("bfloat16")._node)
+    assert o16["name"] != obf["name"]
+    assert "ormi_f32_to_bf16(" in obf["source"].split("extern")[1]
+    assert "ormi_f32_to_bf16(" not in o16["source"].split("extern")[1]

@@ -55,27 +55,35 @@ def _make_spec(seed):
         leaves.append((f"L{i}", arr, dtype))
         names.append(f"L{i}")
     ops, cur = [], names[0]
+    rank = {n: a.ndim for n, a, _ in leaves}  # a value's rank: the largest of its operands'
     for j in range(int(rng.integers(3, 9))):
         r = rng.random()
         out = f"v{j}"
         if r < 0.35:
             ops.append((out, str(rng.choice(UNARY)), [cur]))
+            rank[out] = rank[cur]
         elif r < 0.8:
             other = str(rng.choice(names + [o for o, _, _ in ops]))
             ops.append((out, str(rng.choice(BINARY[:3])), [cur, other]))
+            rank[out] = max(rank[cur], rank[other])
         else:
             ops.append((out, "scale", [cur, float(rng.uniform(-1.5, 1.5))]))
+            rank[out] = rank[cur]
         cur = out
     if nd >= 2 and rng.random() < 0.3:
         ops.append(("vt", "transpose", [cur]))
+        rank["vt"] = rank[cur]
         cur = "vt"
+    # reduce over an axis the value has (a chain over leaves that all dropped
+    # leading dims has fewer than nd)
+    rk = max(rank[cur], 1)
     red = rng.random()
     if red < 0.25:
-        ops.append(("r", "sum", [cur, int(rng.integers(0, nd)), bool(rng.random() < 0.5)]))
+        ops.append(("r", "sum", [cur, int(rng.integers(0, rk)), bool(rng.random() < 0.5)]))
     elif red < 0.4:
-        ops.append(("r", "max", [cur, int(rng.integers(0, nd)), bool(rng.random() < 0.5)]))
+        ops.append(("r", "max", [cur, int(rng.integers(0, rk)), bool(rng.random() < 0.5)]))
     elif red < 0.5:
-        ops.append(("r", "argmax", [cur, int(rng.integers(0, nd))]))
+        ops.append(("r", "argmax", [cur, int(rng.integers(0, rk))]))
     elif red < 0.6:
         ops.append(("r", "bf16", [cur]))
     else:
