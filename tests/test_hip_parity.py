@@ -730,6 +730,25 @@ def test_f16_leaves_and_casts_match_numpy(cpu, hip):
     assert np.isnan(got[0]) and same_bits(got[1:], np.array([np.inf, -np.inf, -0.0, np.inf, 0.0], np.float32))
 
 
+def test_bf16_and_f16_kernels_of_one_structure_stay_apart(hip):
+    """The same element-wise structure over an fp16 leaf, then over a bf16 leaf
+    (and fp16 then bf16 outputs), in one process: each must use its own kernel.
+    Both types are stored as unsigned short; a kernel cache keyed on storage
+    types alone once handed the bf16 request the fp16 kernel, which read bf16
+    bits as fp16. Exact ops only (x * 0.5 + 0.25 is exact for these inputs), so
+    the results are compared bit for bit."""
+    rng = np.random.default_rng(347)
+    x = rng.uniform(-2, 2, (3, 8, 64)).astype(np.float32)
+    xh, xb = f16_round(x), bf16_round(x)
+    for dtype, want in (("float16", xh), ("bfloat16", xb), ("float16", xh)):
+        got = (T(x, hip, dtype=dtype) * 0.5 + 0.25).numpy()
+        assert np.array_equal(got, want * np.float32(0.5) + np.float32(0.25)), dtype
+    y = rng.uniform(-2, 2, (3, 8, 64)).astype(np.float32)
+    for dtype, rnd in (("float16", f16_round), ("bfloat16", bf16_round), ("float16", f16_round)):
+        got = (T(y, hip) * 0.5).astype(dtype).numpy()
+        assert np.array_equal(got, rnd(y * np.float32(0.5))), dtype
+
+
 @pytest.mark.parametrize("m,k,n", [(256, 256, 256), (264, 128, 136), (300, 200, 104), (33, 17, 9), (512, 1024, 768)])
 def test_f16_gemm_layouts(cpu, hip, m, k, n):
     """f16 x f16 -> fp32 (v_mfma_f32_32x32x16_f16 on the fast paths, the generic
