@@ -1,5 +1,5 @@
 """Seeded random graphs: element-wise chains over broadcast and strided views,
-reductions on random axes, bf16 leaves and casts, realized on the HIP device
+reductions on random axes, bf16 and fp16 leaves and casts, realized on the HIP device
 and on the CPU oracle. Exact ops must agree bit for bit; the rest within fp32
 rounding of the transcendentals (rtol 1e-5) and the summation-order bound."""
 import numpy as np
@@ -37,6 +37,8 @@ def _graph(dev, spec):
             vals[out] = a.argmax(args[1])
         elif op == "bf16":
             vals[out] = a.astype("bfloat16")
+        elif op == "f16":
+            vals[out] = a.astype("float16")
     return vals[spec["ops"][-1][0]], vals
 
 
@@ -51,7 +53,8 @@ def _make_spec(seed):
         drop = int(rng.integers(0, nd))
         lshape = lshape[drop:] if rng.random() < 0.3 else lshape
         arr = rng.uniform(-2, 2, lshape).astype(np.float32)
-        dtype = "bfloat16" if rng.random() < 0.15 else None
+        r = rng.random()
+        dtype = "bfloat16" if r < 0.15 else ("float16" if r > 0.9 else None)
         leaves.append((f"L{i}", arr, dtype))
         names.append(f"L{i}")
     ops, cur = [], names[0]
@@ -85,7 +88,7 @@ def _make_spec(seed):
     elif red < 0.5:
         ops.append(("r", "argmax", [cur, int(rng.integers(0, rk))]))
     elif red < 0.6:
-        ops.append(("r", "bf16", [cur]))
+        ops.append(("r", "bf16" if rng.random() < 0.5 else "f16", [cur]))
     else:
         ops.append(("r", "scale", [cur, 1.0]))
     return {"leaves": leaves, "ops": ops}
@@ -106,7 +109,7 @@ def test_random_graph_matches_oracle(cpu, hip, seed):
         at = np.take_along_axis(x, np.expand_dims(got, args[1]), args[1]).squeeze(args[1])
         np.testing.assert_allclose(at, x.max(args[1]), rtol=1e-4, atol=1e-4, err_msg=str(spec["ops"]))
         return
-    tol = 2 ** -7 if last == "bf16" else 1e-4
+    tol = 2 ** -7 if last == "bf16" else (2 ** -10 if last == "f16" else 1e-4)
     np.testing.assert_allclose(got.astype(np.float64), want.astype(np.float64), rtol=tol, atol=tol, equal_nan=True,
                                err_msg=str(spec["ops"]))
 
