@@ -36,6 +36,11 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 FP32_PEAK_TFLOPS = 157.3
+# Untimed work before each timed measurement, in milliseconds of wall time.
+# The card's clocks rise over the first tens of milliseconds of sustained
+# work: in one process, sets of 30 bf16 4096^3 GEMMs timed one after another
+# took 136, 127, 120, 118, 116, then 114 us per launch.
+WARM_MS = 60.0
 METRIC = json.loads((ROOT / "BASELINE.json").read_text())["metric"]
 
 
@@ -83,42 +88,41 @@ def gc_paused():
             gc.enable()
 
 
-def timed_launches(ev: Events, make, n: int) -> float:
-    """Average ms per iteration over n back-to-back realizations of pre-built
-    graphs (make(i) returns a Tensor or a list of Tensors to realize). A first
-    set of n graphs is realized and dropped untimed, so the allocator's pool
-    already holds every output block the timed set needs (steady state, as in a
-    training loop): the timed region issues launches, not hipMalloc calls."""
+def timed_launches(ev: Events, make, n: int, rounds: int = 3) -> float:
+    """Median over `rounds` timed sets of the average ms per iteration, each set
+    n back-to-back realizations of pre-built graphs (make(i) returns a Tensor
+    or a list of Tensors to realize). Untimed sets come first: the first fills
+    the allocator's pool with every output block a set needs (steady state, as
+    in a training loop: the timed region issues launches, not hipMalloc calls),
+    and more follow until this work has run for WARM_MS of wall time."""
     def as_list(g):
         return g if isinstance(g, (list, tuple)) else [g]
 
-    def release(sets):
+    def run_set(timed: bool):
+        graphs = [as_list(make(i)) for i in range(n)]
+        ev.sync()
+        a, b = ev.new(), ev.new()
+        with gc_paused():
+            ev.record(a)
+            for gs in graphs:
+                for g in gs:
+                    g.realize()
+            ev.record(b)
+        ms = ev.elapsed_ms(a, b) / n
         # Autograd graphs hold reference cycles until zero_grad_graph (the
         # reference's contract); objects that own one release it here.
-        for gs in sets:
+        for gs in graphs:
             for g in gs:
                 if hasattr(g, "release"):
                     g.release()
+        return ms if timed else None
 
-    warm = [as_list(make(i)) for i in range(n)]
-    for gs in warm:
-        for g in gs:
-            g.realize()
-    ev.sync()
-    release(warm)
-    del warm
-    graphs = [as_list(make(i)) for i in range(n)]
-    ev.sync()
-    a, b = ev.new(), ev.new()
-    with gc_paused():
-        ev.record(a)
-        for gs in graphs:
-            for g in gs:
-                g.realize()
-        ev.record(b)
-    ms = ev.elapsed_ms(a, b) / n
-    release(graphs)
-    return ms
+    t0 = time.perf_counter()
+    run_set(False)
+    while (time.perf_counter() - t0) * 1e3 < WARM_MS:
+        run_set(False)
+    times = sorted(run_set(True) for _ in range(rounds))
+    return times[len(times) // 2]
 
 
 # ------------------------------------------------------------------ workloads
@@ -289,6 +293,13 @@ def bench_c2(args, ev: Events) -> dict:
     # Give the allocator pool the blocks the ring cycles through (the ring's 4
     # outputs plus the one being written), so no timed step calls hipMalloc.
     [c2_graph(*sets[i % 3]).realize() for i in range(ring.maxlen + 1)]
+    # Untimed steps for WARM_MS of wall time, then the W warm-up steps.
+    t0, i = time.perf_counter(), 0
+    while (time.perf_counter() - t0) * 1e3 < WARM_MS:
+        ring.append(c2_graph(*sets[i % 3]).realize())
+        i += 1
+        if i % 64 == 0:
+            ev.sync()
     for i in range(args.warmup):
         ring.append(c2_graph(*sets[i % 3]).realize())
     ev.sync()
@@ -507,7 +518,10 @@ def vendor_gemm(out_md: Path, cmd: str, rounds: int = 3, n: int = 20) -> None:
                                         ("C5 fp32 H1 W2 (NN)", 1024, 4096, 4096, False, False, False),
                                         ("C5 fp32 dW2 = H1^T dH2 (TN)", 4096, 4096, 1024, True, False, False),
                                         ("C5 fp32 dH1 = dH2 W2^T (NT)", 1024, 4096, 4096, False, True, False),
-                                        ("C4 bf16 4096^3 (NN), fp32 out", 4096, 4096, 4096, False, False, True)]:
+                                        ("C4 bf16 4096^3 (NN), fp32 out", 4096, 4096, 4096, False, False, True),
+                                        ("bf16 4096^3 NT, fp32 out", 4096, 4096, 4096, False, True, True),
+                                        ("bf16 4096^3 TN, fp32 out", 4096, 4096, 4096, True, False, True),
+                                        ("bf16 8192^3 NN, fp32 out", 8192, 8192, 8192, False, False, True)]:
         dt = torch.bfloat16 if bf16 else torch.float32
         a_st = (torch.randn(K, M, device="cuda", generator=gen) / 64).to(dt) if ta else \
             (torch.randn(M, K, device="cuda", generator=gen) / 64).to(dt)
@@ -520,24 +534,30 @@ def vendor_gemm(out_md: Path, cmd: str, rounds: int = 3, n: int = 20) -> None:
         g.a_stride_m, g.a_stride_k = (1, M) if ta else (K, 1)
         g.b_stride_k, g.b_stride_n = (1, K) if tb else (N, 1)
         fn = (lambda A=A, B=B: torch.mm(A, B, out_dtype=torch.float32)) if bf16 else (lambda A=A, B=B: A @ B)
-        cases.append((name, fn, g, 2 * M * N * K, bf16, (a_st, b_st, C)))
+        # hipBLASLt with a bf16 output (half the store) as a reference point.
+        fn16 = (lambda A=A, B=B: torch.mm(A, B)) if bf16 else None
+        cases.append((name, (fn, fn16), g, 2 * M * N * K, bf16, (a_st, b_st, C)))
     best = {}
     for _ in range(rounds):
-        for name, fn, g, fl, bf16, keep in cases:
+        for name, (fn, fn16), g, fl, bf16, keep in cases:
             tt, to = t_torch(fn), t_ours(g)
-            b0 = best.get(name, (math.inf, math.inf))
-            best[name] = (min(b0[0], tt), min(b0[1], to))
+            t16 = t_torch(fn16) if fn16 else math.inf
+            b0 = best.get(name, (math.inf, math.inf, math.inf))
+            best[name] = (min(b0[0], tt), min(b0[1], to), min(b0[2], t16))
     lines = ["# GEMM: ormi_hip_gemm against torch.matmul (hipBLASLt) on the same box", "",
              f"Command (from the repo root): `{cmd}`", "",
              f"torch {torch.__version__}; one process, the same device buffers, the two alternating per shape; "
              f"HIP events over {n} back-to-back launches, best of {rounds} rounds. Operands N(0, 1/64) "
-             "(the C4 distribution); T = stored transposed (a view, as autograd passes it).", "",
-             "| GEMM | M x N x K | hipBLASLt us | TFLOP/s | ours us | TFLOP/s | ours / hipBLASLt time |",
-             "|---|---|---|---|---|---|---|"]
-    for name, fn, g, fl, bf16, keep in cases:
-        tt, to = best[name]
+             "(the C4 distribution); T = stored transposed (a view, as autograd passes it). The last column times "
+             "hipBLASLt on the same bf16 product with a bf16 output, which stores half the bytes; the C4 config "
+             "asks for an fp32 output.", "",
+             "| GEMM | M x N x K | hipBLASLt us | TFLOP/s | ours us | TFLOP/s | ours / hipBLASLt time | "
+             "hipBLASLt bf16-out us |",
+             "|---|---|---|---|---|---|---|---|"]
+    for name, fns, g, fl, bf16, keep in cases:
+        tt, to, t16 = best[name]
         lines.append(f"| {name} | {g.M}x{g.N}x{g.K} | {tt:.1f} | {fl / tt / 1e6:.1f} | {to:.1f} | {fl / to / 1e6:.1f} | "
-                     f"{to / tt:.3f} |")
+                     f"{to / tt:.3f} | {'—' if math.isinf(t16) else f'{t16:.1f}'} |")
     del cases
     # The C5 step both ways, alternating, each timed over sustained back-to-back
     # steps (the clock the GEMMs run at falls as the card heats under load).
@@ -546,7 +566,7 @@ def vendor_gemm(out_md: Path, cmd: str, rounds: int = 3, n: int = 20) -> None:
     for _ in range(rounds):
         t_c5[0].append(torch_c5_step_ms(torch, c5_steps))
         t_c5[1].append(bench_c5(ev, c5_steps)["step_ms"])
-    lines += ["", f"C5 MLP training step (BASELINE config 5), {c5_steps} back-to-back steps after 2 untimed, best of "
+    lines += ["", f"C5 MLP training step (BASELINE config 5), {c5_steps} back-to-back steps after untimed ones, best of "
               f"{rounds} rounds, the two alternating: PyTorch (hipBLASLt GEMMs, torch autograd, erf GELU, one kernel "
               "per element-wise op) against this build's lazy graph (fused epilogues).", "",
               "| C5 step | PyTorch ms | ours ms | ours / PyTorch time |", "|---|---|---|---|",
@@ -662,9 +682,10 @@ def torch_c5_step_ms(torch, steps: int) -> float:
             ws = [(w - g * 1e-3).requires_grad_() for w, g in zip(ws, grads)]
         return loss, ws
 
-    for _ in range(2):
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < WARM_MS:
         _, ws = step(ws)
-    torch.cuda.synchronize()
+        torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with gc_paused():
         a.record()
@@ -711,8 +732,12 @@ def bench_c5(ev: Events, steps: int) -> dict:
     loss0, ws = step(ws)
     first = float(loss0.numpy())
     del loss0
-    _, ws = step(ws)  # second untimed step: the pool now holds a step's blocks
-    ev.sync()
+    # Untimed steps (the pool holds a step's blocks after the second) for
+    # WARM_MS of wall time.
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < WARM_MS:
+        _, ws = step(ws)
+        ev.sync()
     e0, e1 = ev.new(), ev.new()
     with gc_paused():
         ev.record(e0)
@@ -840,6 +865,31 @@ def pmc_report(pmc_dir: Path, out: Path, cmd: str) -> None:
               "Infinity Cache serves. A GEMM reads each operand panel once per XCD that needs it (8 L2s): the bf16 "
               "kernel's 4x8 tile group per XCD needs 8 MB of A and 16 MB of B, 192 MB over the chip against the "
               "64 MB of its operands, which stay resident in the Infinity Cache."]
+    out.write_text("\n".join(lines) + "\n")
+    print(out.read_text())
+
+
+def trace_report(run_dir: Path, out: Path, title: str, cmd: str) -> None:
+    """Per-kernel durations from a `rocprofv3 --kernel-trace` run (the
+    *kernel_trace.csv under run_dir): calls, mean, median, min and max in
+    microseconds, and the share of GPU time. The trace counts every dispatch of
+    the run, warm-up launches included; the median is the steady-state figure."""
+    by = collections.defaultdict(list)
+    for f in sorted(run_dir.rglob("*kernel_trace.csv")):
+        with open(f, newline="") as fh:
+            for r in csv.DictReader(fh):
+                by[r["Kernel_Name"].strip()].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    if not by:
+        raise SystemExit(f"--trace-report: no kernel trace under {run_dir}")
+    total = sum(sum(v) for v in by.values())
+    lines = [f"# {title}", "", f"Command (from the repo root): `{cmd}`", "",
+             "rocprofv3 kernel trace, durations in microseconds. Every dispatch of the run is counted, the untimed "
+             "warm-up launches included; the median is the steady-state figure.", "",
+             "| kernel | calls | mean us | median us | min us | max us | % of GPU time |", "|---|---|---|---|---|---|---|"]
+    for name, v in sorted(by.items(), key=lambda kv: -sum(kv[1])):
+        v = sorted(v)
+        lines.append(f"| `{name[:110]}` | {len(v)} | {sum(v) / len(v):.2f} | {v[len(v) // 2]:.2f} | {v[0]:.2f} | "
+                     f"{v[-1]:.2f} | {100 * sum(v) / total:.2f} |")
     out.write_text("\n".join(lines) + "\n")
     print(out.read_text())
 
@@ -979,9 +1029,16 @@ def main():
                     help="summarize the two rocprofv3 --pmc passes of WAVE_COUNTERS over --only c4 (no GPU needed)")
     ap.add_argument("--gemm-k-sweep", metavar="OUT_MD",
                     help="fp32 GEMM time against K at the C5 output shapes: fixed cost per launch and loop rate")
+    ap.add_argument("--trace-report", nargs=3, metavar=("RUN_DIR", "OUT_MD", "TITLE"),
+                    help="summarize a rocprofv3 --kernel-trace run into per-kernel durations (no GPU needed); "
+                         "--trace-cmd gives the command that made the run")
+    ap.add_argument("--trace-cmd", default="", help="the rocprofv3 command recorded by --trace-report")
     ap.add_argument("--vendor-gemm", metavar="OUT_MD",
                     help="time the C4/C5 GEMM shapes against torch.matmul (hipBLASLt) and write a markdown summary")
     args = ap.parse_args()
+    if args.trace_report:
+        trace_report(Path(args.trace_report[0]), Path(args.trace_report[1]), args.trace_report[2], args.trace_cmd)
+        return
     if args.gemm_k_sweep:
         gemm_k_sweep(Path(args.gemm_k_sweep), f"python3 bench.py --gemm-k-sweep {args.gemm_k_sweep}")
         return
@@ -1025,7 +1082,7 @@ def main():
     if args.only:
         n = max(10, min(args.steps, 30))
         res = {"copy": lambda: bench_copy(args, ev), "c1": lambda: bench_c1(ev, n), "c3": lambda: bench_c3(ev, n),
-               "c4": lambda: bench_c4(ev, n), "c5": lambda: bench_c5(ev, max(3, min(args.steps // 10, 10)))}[args.only]()
+               "c4": lambda: bench_c4(ev, n), "c5": lambda: bench_c5(ev, max(10, min(args.steps, 30)))}[args.only]()
         print(json.dumps({"only": args.only, **res}), flush=True)
         return
     main_res = bench_c2(args, ev)
@@ -1036,7 +1093,7 @@ def main():
         extra["C1_fused_pointwise_rowsum_1024"] = bench_c1(ev, n)
         extra["C3_reductions_16384x8192"] = bench_c3(ev, n)
         extra["C4_gemm"] = bench_c4(ev, n)
-        extra["C5_mlp_step_ms"] = bench_c5(ev, max(3, min(args.steps // 10, 10)))
+        extra["C5_mlp_step_ms"] = bench_c5(ev, max(10, min(args.steps, 30)))
     cpu = None if args.no_cpu else cpu_baseline_c2()
     if not args.no_cpu and not args.no_extra:
         log("CPU baselines of the other configs")

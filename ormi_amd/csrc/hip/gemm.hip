@@ -388,6 +388,41 @@ __global__ __launch_bounds__(256) void gemm_finish_kernel(FinishParams f) {
     }
 }
 
+// The finish pass without an epilogue, for C contiguous over the n elements
+// of a split and 16-byte aligned (n % 4 == 0): a flat grid-stride walk over
+// float4 groups, U groups per thread with every split's loads issued before
+// the sums, in split order like gemm_finish_kernel.
+template <int U>
+__global__ __launch_bounds__(256) void gemm_finish_flat_kernel(float* __restrict__ c, const float* __restrict__ ws,
+                                                               long long n4, int splits) {
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    const ormi_f4* w = (const ormi_f4*)ws;
+    ormi_f4* out = (ormi_f4*)c;
+    for (long long g0 = (long long)blockIdx.x * blockDim.x + threadIdx.x; g0 < n4; g0 += stride * U) {
+        ormi_f4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const long long g = g0 + u * stride;
+            if (g < n4) v[u] = w[g];
+        }
+        for (int q = 1; q < splits; ++q) {
+            ormi_f4 t[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const long long g = g0 + u * stride;
+                if (g < n4) t[u] = w[q * n4 + g];
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) v[u] += t[u];
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const long long g = g0 + u * stride;
+            if (g < n4) __builtin_nontemporal_store(v[u], out + g);
+        }
+    }
+}
+
 // Any strides, any shape: 16x16 output tile per block, fp32 accumulation.
 template <int DT>
 __device__ __forceinline__ float gemm_elem(const void* p, long long i) {
@@ -1093,9 +1128,16 @@ static void launch_finish(const ormi_gemm_desc* d, const float* ws, int splits, 
     f.batch_ndim = d->batch_ndim;
     for (int i = 0; i < d->batch_ndim; ++i) f.batch_shape[i] = d->batch_shape[i];
     f.epi = epi;
+    const bool vec = d->N % 4 == 0 && ((uintptr_t)d->c & 15u) == 0 && ((uintptr_t)epi.aux & 15u) == 0;
+    if (vec && epi.kind == ORMI_GEMM_EPI_NONE) {
+        constexpr int U = 4;
+        const long long n4 = f.n / 4;
+        const long long blocks = std::max(1LL, std::min((n4 + 256LL * U - 1) / (256LL * U), (long long)compute_units() * 8));
+        gemm_finish_flat_kernel<U><<<(unsigned)blocks, 256>>>(f.c, ws, n4, splits);
+        return;
+    }
     const int gx = std::min((d->N + 1023) / 1024, 64);
     const int gy = std::max(1, std::min({f.rows, compute_units() * 32 / gx, 65535}));
-    const bool vec = d->N % 4 == 0 && ((uintptr_t)d->c & 15u) == 0 && ((uintptr_t)epi.aux & 15u) == 0;
     if (vec) gemm_finish_kernel<true><<<dim3(gx, gy), 256>>>(f);
     else gemm_finish_kernel<false><<<dim3(gx, gy), 256>>>(f);
 }
