@@ -909,13 +909,235 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_il_kernel(GemmParams p) {
     }
 }
 
+// ------------------------------------------------------------------------
+// Interleaved GEMM with whole-line loads of a k-contiguous A. In a 32-deep
+// k-tile each row of a k-contiguous operand is 64 bytes, half a cache line,
+// so every direct load of gemm_il_kernel touches 16 half lines. Here A is
+// loaded 64 k deep: 8 rows of one whole 128-byte line per load instruction.
+// A sits in 3 pair slots of 32 KB ([BM rows][64 k], the BK-64 swizzle), B in
+// 4 slots of 16 KB as in gemm_il_kernel: 160 KB. Pair q (k-tiles 2q, 2q+1) is
+// loaded half per k-tile during k-tiles 2q-4 and 2q-3, into the slot of pair
+// q-3, whose last reads completed at the barrier of k-tile 2q-5; B k-tile
+// kt+3 is loaded during kt into the slot of kt-1. Per k-tile kt:
+//   step 0: MFMAs on k-step 0 | reads of k-step 1, A loads (half kt & 1 of pair kt/2 + 2)
+//   wait: loads of k-tile kt-2 and older landed, own reads done; barrier
+//   step 1: MFMAs on k-step 1 | reads of k-step 0 of kt+1, B loads (k-tile kt+3)
+// Loads past the end re-read the last pair or tile into a slot no step reads,
+// so every vmcnt bound is a constant. K must be a multiple of 64.
+template <typename Tr, int BM, int BN, int WGM, int WGN, bool B_KC>
+struct IlpStep {
+    static constexpr int NW = WGM * WGN;
+    static constexpr int WTM = BM / WGM, WTN = BN / WGN, TM = WTM / 32, TN = WTN / 32;
+    static constexpr int A_SLOT = BM * 64 * 2, B_SLOT = BN * 32 * 2;
+    using PlanA = DmaPlan<BM, true, NW, 64>;
+    using PlanB = DmaPlan<BN, B_KC, NW, 32>;
+    static constexpr int PA = PlanA::PER / 2, PB = PlanB::PER;  // loads per step
+    static_assert(PA == PB, "both steps issue the same number of loads");
+    static constexpr int RB = B_KC ? 1 : 2;
+    static constexpr int NR = TM + TN * RB;  // reads per step
+    static constexpr int NO = NR + PA;       // memory instructions per step
+    static constexpr int NM = TM * TN;       // MFMAs per step
+
+    // Memory instruction o of step S: reads in the order the next step's MFMAs
+    // consume them (A0, B0 .. B(TN-1), A1 .. A(TM-1)), then the loads.
+    template <int S, int H>
+    __device__ __forceinline__ static void mem_op(int o, u32x4_t (&fa)[TM], u32x4_t (&fb)[TN], const lds_char* ra,
+                                                  int aks, const lds_char* rb, int bks, int wm, int wn, lds_char* la,
+                                                  lds_char* lb, const char* ta, const char* tb, const PlanA& pa,
+                                                  const PlanB& pb) {
+        if (o < 1) {
+            fa[0] = frag<BM, true, 64>(ra, wm * WTM, aks);
+        } else if (o < 1 + TN * RB) {
+            const int j = (o - 1) / RB, h = (o - 1) % RB;
+            frag_part<BN, B_KC, 32>(fb[j], rb, wn * WTN + j * 32, bks, h);
+        } else if (o < NR) {
+            const int i = 1 + (o - 1 - TN * RB);
+            fa[i] = frag<BM, true, 64>(ra, wm * WTM + i * 32, aks);
+        } else if (S == 0) {
+            pa.issue_one(la, ta, H * PA + (o - NR));
+        } else {
+            pb.issue_one(lb, tb, o - NR);
+        }
+    }
+
+    template <int S, int H>
+    __device__ __forceinline__ static void run(f32x16_t (&acc)[TM][TN], const u32x4_t (&ua)[TM], const u32x4_t (&ub)[TN],
+                                               u32x4_t (&fa)[TM], u32x4_t (&fb)[TN], const lds_char* ra, int aks,
+                                               const lds_char* rb, int bks, int wm, int wn, lds_char* la, lds_char* lb,
+                                               const char* ta, const char* tb, const PlanA& pa, const PlanB& pb) {
+#pragma unroll
+        for (int n = 0; n < NM; ++n) {
+            Tr::mma(ua[n / TN], ub[n % TN], acc[n / TN][n % TN]);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int o = n * NO / NM; o < (n + 1) * NO / NM; ++o) {
+                mem_op<S, H>(o, fa, fb, ra, aks, rb, bks, wm, wn, la, lb, ta, tb, pa, pb);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
+};
+
+template <typename Tr, int BM, int BN, int WGM, int WGN, bool B_KC>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_ilp_kernel(GemmParams p) {
+    using Step = IlpStep<Tr, BM, BN, WGM, WGN, B_KC>;
+    constexpr int TM = Step::TM, TN = Step::TN, WTM = Step::WTM, WTN = Step::WTN;
+    constexpr int A_SLOT = Step::A_SLOT, B_SLOT = Step::B_SLOT, PA = Step::PA;
+    constexpr int A_SLOTS = 3, B_SLOTS = 4;
+    __shared__ __attribute__((aligned(1024))) char smem[A_SLOTS * A_SLOT + B_SLOTS * B_SLOT];
+
+    const int T = p.tiles_m * p.tiles_n;
+    int t = blockIdx.x;
+    if ((T & 7) == 0) t = (t & 7) * (T >> 3) + (t >> 3);
+    constexpr int GROUP = 4;
+    const int group_size = GROUP * p.tiles_n;
+    const int g = t / group_size, first_m = g * GROUP;
+    const int gm = min(p.tiles_m - first_m, GROUP);
+    const int m0 = (first_m + (t % group_size) % gm) * BM;
+    const int n0 = ((t % group_size) / gm) * BN;
+
+    const int split = blockIdx.z % p.splits;
+    int bidx = blockIdx.z / p.splits;
+    long long a_off = 0, b_off = 0;
+    const long long c_off = ((long long)split * p.batch + bidx) * p.M * p.N;
+    for (int d = p.batch_ndim - 1; d >= 0; --d) {
+        const int coord = bidx % p.batch_shape[d];
+        bidx /= p.batch_shape[d];
+        a_off += coord * p.a_bs[d];
+        b_off += coord * p.b_bs[d];
+    }
+    float* c = p.c + c_off;
+    const int kbeg = split * p.k_per_split;
+    const int kend = min(p.K, kbeg + p.k_per_split);
+    const int NP = kend > kbeg ? (kend - kbeg) / 64 : 0;  // pairs of k-tiles
+    const int KT = 2 * NP;
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave / WGN, wn = wave % WGN;
+
+    typename Step::PlanA pa;
+    typename Step::PlanB pb;
+    pa.init(p.a_sm, p.a_sk, m0, p.M);
+    pb.init(p.b_sn, p.b_sk, n0, p.N);
+    const char* ta = p.a + a_off * 2 + Step::PlanA::origin(p.a_sm, p.a_sk, m0, kbeg);
+    const char* tb = p.b + b_off * 2 + Step::PlanB::origin(p.b_sn, p.b_sk, n0, kbeg);
+    const long long a_step = Step::PlanA::kstep(p.a_sk), b_step = Step::PlanB::kstep(p.b_sk);
+    lds_char* const lds = (lds_char*)smem;
+    lds_char* const ab = lds;                        // A pair slots
+    lds_char* const bb = lds + A_SLOTS * A_SLOT;     // B slots
+    asm volatile("" ::"s"(c), "s"(p.M), "s"(p.N));
+
+    f32x16_t acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    if (NP > 0) {
+        // Prologue: virtual k-tiles -4 .. -1, each an A half then a B k-tile
+        // (A pairs 0 and 1, B k-tiles 0 .. 2). ta / tb address the next pair
+        // or k-tile to load, clamped to the last.
+        {
+            const char* ua = DmaPlan<BM, true, Step::NW, 64>::uniform(ta);
+#pragma unroll
+            for (int d = 0; d < PA; ++d) pa.issue_one(ab, ua, d);
+#pragma unroll
+            for (int d = 0; d < PA; ++d) pa.issue_one(ab, ua, PA + d);
+            const char* ub = DmaPlan<BN, B_KC, Step::NW, 32>::uniform(tb);
+            pb.issue(bb, ub);
+            if (1 < NP) ta += a_step;
+            if (1 < KT) tb += b_step;
+            ua = DmaPlan<BM, true, Step::NW, 64>::uniform(ta);
+#pragma unroll
+            for (int d = 0; d < PA; ++d) pa.issue_one(ab + A_SLOT, ua, d);
+            ub = DmaPlan<BN, B_KC, Step::NW, 32>::uniform(tb);
+            pb.issue(bb + B_SLOT, ub);
+            if (2 < KT) tb += b_step;
+#pragma unroll
+            for (int d = 0; d < PA; ++d) pa.issue_one(ab + A_SLOT, ua, PA + d);
+            ub = DmaPlan<BN, B_KC, Step::NW, 32>::uniform(tb);
+            pb.issue(bb + 2 * B_SLOT, ub);
+            if (2 < NP) ta += a_step;
+            if (3 < KT) tb += b_step;
+        }
+        // k-tile 0 (A pair 0, B k-tile 0) landed: loads of virtual k-tiles -2
+        // and -1 may stay in flight.
+        wait_vmcnt<4 * PA>();
+        lds_barrier();
+        u32x4_t fa[2][TM], fb[2][TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) fa[0][i] = frag<BM, true, 64>(ab, wm * WTM + i * 32, 0);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) fb[0][j] = frag<BN, B_KC, 32>(bb, wn * WTN + j * 32, 0);
+
+        int aslot = 0, bslot = 0;
+        constexpr int V = 3 * PA;  // loads of k-tile kt-1 and step 0 of kt
+        for (int q = 0; q < NP; ++q) {
+            const int aload = aslot == 0 ? 2 : aslot - 1;  // slot of pair q+2 (pair q-1's)
+            const int anext = aslot == 2 ? 0 : aslot + 1;
+            const lds_char* ra = ab + aslot * A_SLOT;
+            lds_char* la = ab + aload * A_SLOT;
+            const char* ua = DmaPlan<BM, true, Step::NW, 64>::uniform(ta);
+            // ---- k-tile 2q (A half 0 of pair q+2)
+            {
+                const int bn = (bslot + 1) & 3, bl = (bslot + 3) & 3;
+                const char* ub = DmaPlan<BN, B_KC, Step::NW, 32>::uniform(tb);
+                Step::template run<0, 0>(acc, fa[0], fb[0], fa[1], fb[1], ra, 1, bb + bslot * B_SLOT, 1, wm, wn, la,
+                                         bb + bl * B_SLOT, ua, ub, pa, pb);
+                __builtin_amdgcn_s_waitcnt((V & 15) | ((V >> 4) << 14) | (7 << 4));
+                lds_barrier();
+                Step::template run<1, 0>(acc, fa[1], fb[1], fa[0], fb[0], ra, 2, bb + bn * B_SLOT, 0, wm, wn, la,
+                                         bb + bl * B_SLOT, ua, ub, pa, pb);
+                if (2 * q + 4 < KT) tb += b_step;
+                bslot = bn;
+            }
+            // ---- k-tile 2q+1 (A half 1 of pair q+2); the next k-tile reads pair q+1
+            {
+                const int bn = (bslot + 1) & 3, bl = (bslot + 3) & 3;
+                const char* ub = DmaPlan<BN, B_KC, Step::NW, 32>::uniform(tb);
+                Step::template run<0, 1>(acc, fa[0], fb[0], fa[1], fb[1], ra, 3, bb + bslot * B_SLOT, 1, wm, wn, la,
+                                         bb + bl * B_SLOT, ua, ub, pa, pb);
+                __builtin_amdgcn_s_waitcnt((V & 15) | ((V >> 4) << 14) | (7 << 4));
+                lds_barrier();
+                Step::template run<1, 1>(acc, fa[1], fb[1], fa[0], fb[0], ab + anext * A_SLOT, 0, bb + bn * B_SLOT, 0,
+                                         wm, wn, la, bb + bl * B_SLOT, ua, ub, pa, pb);
+                if (2 * q + 5 < KT) tb += b_step;
+                bslot = bn;
+            }
+            if (q + 3 < NP) ta += a_step;
+            aslot = anext;
+        }
+        // No load may still be writing this workgroup's LDS when it exits.
+        wait_vmcnt<0>();
+    }
+
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int col = n0 + wn * WTN + j * 32 + (lane & 31);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (row < p.M && col < p.N) c[(long long)row * p.N + col] = acc[i][j][r];
+            }
+        }
+    }
+}
+
 // Direct-load 16-bit configurations (ORMI_GEMM_DMA_CFG):
 //   two-stage, BK 64:  0: 256x256, 2x2 waves   1: 256x256, 2x4   2: 256x256, 4x2   3: 128x128, 2x2
 //   multi-stage, BK 32: 4: 256x256, 2x2, 4 stages   5: 256x256, 2x4, 4 stages
 //                       6: 256x256, 2x2, 5 stages   7: 256x256, 4x2, 4 stages
 //   interleaved, BK 32: 8: 256x256, 2x2, 3 stages   9: 256x256, 2x2, 4 stages
 //                       10: 256x256, 2x4, 4 stages  11: 256x256, 4x2, 4 stages
-// The default, 9, measured fastest on MI355X for NN, NT and TN at 4096^3.
+//   interleaved with whole-line A loads (A k-contiguous, K % 64 == 0, else 9):
+//                       12: 256x256, 2x2, 3 A pair slots + 4 B slots
+// The defaults: 12 where it applies (NN 4096^3 116.8 -> 112.4 us, NT 121.6 ->
+// 114.3 us on one box, bit-identical), otherwise 9, the fastest of 0-11 on
+// MI355X for NN, NT and TN at 4096^3.
 template <typename Tr, int BM, int BN, int WGM, int WGN>
 struct DmaLauncher {
     static constexpr Cfg cfg{BM, BN, 64};
@@ -958,6 +1180,17 @@ struct IlLauncher {
         else go<false, false>(p, grid);
     }
 };
+// Whole-line A loads (gemm_ilp_kernel) for a k-contiguous A; the interleaved
+// 4-stage kernel otherwise.
+template <typename Tr, int BM, int BN, int WGM, int WGN>
+struct IlpLauncher {
+    static constexpr Cfg cfg{BM, BN, 64};
+    static void run(const GemmParams& p, dim3 grid, bool a_kc, bool b_kc) {
+        if (a_kc && b_kc) gemm_ilp_kernel<Tr, BM, BN, WGM, WGN, true><<<grid, 64 * WGM * WGN>>>(p);
+        else if (a_kc) gemm_ilp_kernel<Tr, BM, BN, WGM, WGN, false><<<grid, 64 * WGM * WGN>>>(p);
+        else IlLauncher<Tr, BM, BN, WGM, WGN, 4>::run(p, grid, a_kc, b_kc);
+    }
+};
 template <typename Tr>
 static Cfg cfg_dma(int id) {
     switch (id) {
@@ -972,6 +1205,7 @@ static Cfg cfg_dma(int id) {
         case 8: return IlLauncher<Tr, 256, 256, 2, 2, 3>::cfg;
         case 9: return IlLauncher<Tr, 256, 256, 2, 2, 4>::cfg;
         case 10: return IlLauncher<Tr, 256, 256, 2, 4, 4>::cfg;
+        case 12: return IlpLauncher<Tr, 256, 256, 2, 2>::cfg;
         default: return IlLauncher<Tr, 256, 256, 4, 2, 4>::cfg;
     }
 }
@@ -989,6 +1223,7 @@ static void run_dma(int id, const GemmParams& p, dim3 grid, bool a_kc, bool b_kc
         case 8: IlLauncher<Tr, 256, 256, 2, 2, 3>::run(p, grid, a_kc, b_kc); break;
         case 9: IlLauncher<Tr, 256, 256, 2, 2, 4>::run(p, grid, a_kc, b_kc); break;
         case 10: IlLauncher<Tr, 256, 256, 2, 4, 4>::run(p, grid, a_kc, b_kc); break;
+        case 12: IlpLauncher<Tr, 256, 256, 2, 2>::run(p, grid, a_kc, b_kc); break;
         default: IlLauncher<Tr, 256, 256, 4, 2, 4>::run(p, grid, a_kc, b_kc); break;
     }
 }
@@ -1247,7 +1482,9 @@ static int gemm_run(const ormi_gemm_desc* d, const ormi_gemm_epilogue* epi_in, b
     // less than 4 GB.
     const long long a_span = a_kc ? 256LL * d->a_stride_m * 2 : 64LL * d->a_stride_k * 2 + 512;
     const long long b_span = b_kc ? 256LL * d->b_stride_n * 2 : 64LL * d->b_stride_k * 2 + 512;
-    const int dma_id = env_cfg("ORMI_GEMM_DMA_CFG", 9);
+    // Default: whole-line A loads (12) when A is k-contiguous and K is in
+    // whole 64-deep pairs, else the interleaved 4-stage kernel (9).
+    const int dma_id = env_cfg("ORMI_GEMM_DMA_CFG", a_kc && d->K % 64 == 0 ? 12 : 9);
     const int dma_bk = f32 ? 64 : cfg_dma<TrBF16>(dma_id).BK;
     const bool dma = !f32 && env_cfg("ORMI_GEMM_DMA", 1) != 0 && d->K % dma_bk == 0 && (a_kc || d->M % 8 == 0) &&
                      (b_kc || d->N % 8 == 0) && a_span < (1LL << 32) && b_span < (1LL << 32);
