@@ -323,6 +323,155 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32dma_kernel(GemmParams 
     }
 }
 
+// Persistent form of gemm_f32dma_kernel for an output in whole tiles, one
+// batch, no K split and more tiles than work-groups (one per compute unit):
+// work-group b takes tiles b, b + G, b + 2G, ... (G work-groups, same tile
+// order as the one-tile kernel) and runs them as one stream of k-tiles
+// through the same LDS ring, so the loads of a tile's first k-tiles are in
+// flight while the previous tile finishes, and its stores drain while the
+// next tile's MFMAs run. The per-launch fill, the epilogue's latency and the
+// work-group turnover are paid once per work-group instead of once per tile.
+template <int BM, int BN, int BK, int WGM, int WGN, int STAGES, bool A_KC, bool B_KC, bool EPI>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32dma_persist_kernel(GemmParams p) {
+    static_assert(STAGES >= 2 && STAGES <= 5, "2 to 5 stages");
+    using St = Il32<BM, BN, BK, WGM, WGN, A_KC, B_KC>;
+    constexpr int TM = St::TM, TN = St::TN, WTM = St::WTM, WTN = St::WTN, KS = St::KS;
+    constexpr int A_BYTES = St::A_BYTES, STAGE = St::STAGE, PER_TILE = St::PER_TILE;
+    __shared__ __attribute__((aligned(1024))) char smem[STAGES * STAGE];
+
+    const int T = p.tiles_m * p.tiles_n, G = gridDim.x;
+    const int mine = (T - (int)blockIdx.x + G - 1) / G;  // tiles of this work-group
+    const int KT = p.K / BK;
+    const long long GT = (long long)mine * KT;  // k-tiles in its stream
+    // Tile i of this work-group: XCD-aware remap, then groups of 4 tile rows.
+    auto tile_origin = [&](int i, int& m0, int& n0) {
+        int t = (int)blockIdx.x + i * G;
+        if ((T & 7) == 0) t = (t & 7) * (T >> 3) + (t >> 3);
+        constexpr int GROUP = 4;
+        const int group_size = GROUP * p.tiles_n;
+        const int g = t / group_size, first_m = g * GROUP;
+        const int gm = min(p.tiles_m - first_m, GROUP);
+        m0 = (first_m + (t % group_size) % gm) * BM;
+        n0 = ((t % group_size) / gm) * BN;
+    };
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave / WGN, wn = wave % WGN;
+    typename St::PlanA pa;
+    typename St::PlanB pb;
+    // Whole tiles: a tile's per-lane offsets do not depend on where it lies.
+    pa.init(p.a_sm, p.a_sk, 0, p.M);
+    pb.init(p.b_sn, p.b_sk, 0, p.N);
+    const long long a_step = St::PlanA::kstep(p.a_sk), b_step = St::PlanB::kstep(p.b_sk);
+    // Next k-tile of the stream to load: tile li, k-tile lkt, at ta / tb; it
+    // stays on the last one once the stream is exhausted.
+    int li = 0, lkt = 0;
+    const char* ta;
+    const char* tb;
+    auto set_load_tile = [&](int i) {
+        int m0, n0;
+        tile_origin(i, m0, n0);
+        ta = p.a + St::PlanA::origin(p.a_sm, p.a_sk, m0, 0);
+        tb = p.b + St::PlanB::origin(p.b_sn, p.b_sk, n0, 0);
+    };
+    auto advance = [&]() {
+        if (lkt + 1 < KT) {
+            ++lkt;
+            ta += a_step;
+            tb += b_step;
+        } else if (li + 1 < mine) {
+            ++li;
+            lkt = 0;
+            set_load_tile(li);
+        }
+    };
+    set_load_tile(0);
+    lds_char* const lds = (lds_char*)smem;
+    float* const c = p.c;
+    asm volatile("" ::"s"(c), "s"(p.M), "s"(p.N));
+
+    f32x16_t acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    if (GT > 0) {
+#pragma unroll
+        for (int s = 0; s < STAGES - 1; ++s) {
+            const char* ua = uniform_ptr(ta);
+            const char* ub = uniform_ptr(tb);
+#pragma unroll
+            for (int d = 0; d < St::PA; ++d) pa.issue_one(lds + s * STAGE, ua, d);
+#pragma unroll
+            for (int d = 0; d < St::PB; ++d) pb.issue_one(lds + s * STAGE + A_BYTES, ub, d);
+            if (s + 1 < GT) advance();
+        }
+        wait_vmcnt<(STAGES - 2) * PER_TILE>();
+        lds_barrier();
+        u32x4_t fa[2][TM], fb[2][TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) fa[0][i] = frag32<BM, A_KC, BK>(lds, wm * WTM + i * 32, 0);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) fb[0][j] = frag32<BN, B_KC, BK>(lds + A_BYTES, wn * WTN + j * 32, 0);
+
+        int stage = 0, free_stage = STAGES - 1, tile = 0, kt = 0, cm0, cn0;
+        tile_origin(0, cm0, cn0);
+        for (long long g = 0; g < GT; ++g) {
+            const int next = stage + 1 == STAGES ? 0 : stage + 1;
+            const lds_char* cur = lds + stage * STAGE;
+            lds_char* fs = lds + free_stage * STAGE;
+            const char* ua = uniform_ptr(ta);
+            const char* ub = uniform_ptr(tb);
+            Steps<St, 0>::run(acc, fa, fb, cur, wm, wn, fs, ua, ub, pa, pb);
+            wait_vmcnt_lds<(STAGES - 2) * PER_TILE>();
+            lds_barrier();
+            St::template run<KS - 1>(acc, fa[1], fb[1], fa[0], fb[0], lds + next * STAGE, 0, wm, wn, fs, ua, ub, pa, pb);
+            // Keeps the step's fragment reads among its MFMAs: without it the
+            // compiler sinks them below the branches that follow, and the next
+            // k-tile's first MFMAs wait out their whole latency.
+            asm volatile("" ::: "memory");
+            if (g + STAGES < GT) advance();
+            stage = next;
+            free_stage = free_stage + 1 == STAGES ? 0 : free_stage + 1;
+            if (++kt == KT) {
+                // Tile done: its stores go out while the next tile's k-tiles,
+                // already loading, run on fresh accumulators.
+                if constexpr (EPI) {
+                    float dv[TM][TN][16];
+                    epi_tile<TM, TN, false>(p.epi, c, p.epi.aux, p.epi.d, p.N, cm0 + wm * WTM, cn0 + wn * WTN, acc, dv,
+                                            epi_reads_d(p.epi));
+                } else {
+#pragma unroll
+                    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+                        for (int j = 0; j < TN; ++j) {
+                            const int col = cn0 + wn * WTN + j * 32 + (lane & 31);
+#pragma unroll
+                            for (int r = 0; r < 16; ++r) {
+                                const int row = cm0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                                c[(long long)row * p.N + col] = acc[i][j][r];
+                            }
+                        }
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+                kt = 0;
+                if (++tile < mine) tile_origin(tile, cm0, cn0);
+            }
+        }
+        // No load may still be writing this workgroup's LDS when it exits.
+        wait_vmcnt<0>();
+    }
+}
+
 template <int BM, int BN, int BK, int WGM, int WGN, int STAGES>
 struct F32DmaLauncher {
     template <bool A_KC, bool B_KC>
@@ -335,6 +484,17 @@ struct F32DmaLauncher {
         else if (a_kc) go<true, false>(p, grid, epi);
         else if (b_kc) go<false, true>(p, grid, epi);
         else go<false, false>(p, grid, epi);
+    }
+    template <bool A_KC, bool B_KC>
+    static void go_persist(const GemmParams& p, int groups, bool epi) {
+        if (epi) gemm_f32dma_persist_kernel<BM, BN, BK, WGM, WGN, STAGES, A_KC, B_KC, true><<<groups, 64 * WGM * WGN>>>(p);
+        else gemm_f32dma_persist_kernel<BM, BN, BK, WGM, WGN, STAGES, A_KC, B_KC, false><<<groups, 64 * WGM * WGN>>>(p);
+    }
+    static void run_persist(const GemmParams& p, int groups, bool a_kc, bool b_kc, bool epi) {
+        if (a_kc && b_kc) go_persist<true, true>(p, groups, epi);
+        else if (a_kc) go_persist<true, false>(p, groups, epi);
+        else if (b_kc) go_persist<false, true>(p, groups, epi);
+        else go_persist<false, false>(p, groups, epi);
     }
 };
 
@@ -354,6 +514,9 @@ void cfg32_dma(int id, int* bm, int* bn, int* bk) {
     *bm = 128;
     *bn = id == 2 ? 256 : 128;
     *bk = id == 4 || id == 5 ? 64 : 32;
+}
+void run32_dma_persist(const GemmParams& p, int groups, bool a_kc, bool b_kc, bool epi) {
+    F32DmaLauncher<128, 128, 32, 2, 4, 4>::run_persist(p, groups, a_kc, b_kc, epi);
 }
 void run32_dma(int id, const GemmParams& p, dim3 grid, bool a_kc, bool b_kc, bool epi) {
     if (id < 0 || id > 5) id = 1;

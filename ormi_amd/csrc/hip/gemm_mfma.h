@@ -553,5 +553,9 @@ void run32_epi(int id, const GemmParams& p, dim3 grid, bool a_kc, bool b_kc);
 void cfg32_dma(int id, int* bm, int* bn, int* bk);
 // epi: apply p.epi in the store (M, N and K in whole tiles, no K split).
 void run32_dma(int id, const GemmParams& p, dim3 grid, bool a_kc, bool b_kc, bool epi);
+// The persistent form of the default direct-load configuration (1): `groups`
+// work-groups walk the p.tiles_m x p.tiles_n tiles; whole tiles, one batch,
+// no K split.
+void run32_dma_persist(const GemmParams& p, int groups, bool a_kc, bool b_kc, bool epi);
 
 }  // namespace ormi_hip

@@ -156,3 +156,74 @@ def test_direct_load_epilogue_in_kernel(lib, cfg):
     assert lib.ormi_hip_gemm_ex(ctypes.byref(g), ctypes.byref(e)) == 0, lib.ormi_hip_last_error()
     np.testing.assert_array_equal(lib.read(aux, (M, N)), plain)
     np.testing.assert_array_equal(lib.read(g.c, (M, N)), np.maximum(plain, 0))
+
+
+def _persist(on: bool):
+    os.environ["ORMI_GEMM_PERSIST"] = "1" if on else "0"
+
+
+# More whole 128x128 tiles than compute units: 512 tiles (a multiple of 8, the
+# XCD-aware order), 289 (not a multiple of 8; some work-groups get 2 tiles,
+# others 1), and 1024 (4 per work-group) with K = 64 (two k-tiles per tile:
+# the stream crosses tiles inside the first loads).
+PERSIST_SHAPES = [(2048, 4096, 256), (2176, 2176, 160), (4096, 4096, 64)]
+
+
+@pytest.mark.parametrize("layout", ["NN", "NT", "TN", "TT"])
+def test_persistent_kernel_matches_one_tile_kernel(lib, layout):
+    """The persistent form runs each tile's MFMAs in the same order as the
+    one-tile kernel, so the products are bit-identical; both stay within the
+    fp32 bound of the float64 product."""
+    use(1)
+    rng = np.random.default_rng(94)
+    try:
+        for M, N, K in PERSIST_SHAPES:
+            A = (rng.standard_normal((M, K)) / 8).astype(np.float32)
+            B = (rng.standard_normal((K, N)) / 8).astype(np.float32)
+            _persist(True)
+            got = run(lib, A, B, layout)
+            _persist(False)
+            want = run(lib, A, B, layout)
+            np.testing.assert_array_equal(got, want, err_msg=f"{layout} {M}x{N}x{K}")
+            err = np.abs(got - A.astype(np.float64) @ B.astype(np.float64))
+            assert np.all(err <= bound(A, B)), (layout, M, N, K)
+    finally:
+        os.environ.pop("ORMI_GEMM_PERSIST", None)
+
+
+@pytest.mark.parametrize("kind", ["sgd", "gelu_aux", "gelu_grad"])
+def test_persistent_kernel_epilogues_match_one_tile_kernel(lib, kind):
+    """Epilogues in the persistent kernel's stores (the C5 weight gradient is
+    the SGD form over 1024 tiles): bit-identical to the one-tile kernel's,
+    D read in place for the SGD update."""
+    use(1)
+    rng = np.random.default_rng(95)
+    M, N, K = 2048, 4096, 128
+    A = (rng.standard_normal((M, K)) / 8).astype(np.float32)
+    B = (rng.standard_normal((K, N)) / 8).astype(np.float32)
+    D = rng.standard_normal((M, N)).astype(np.float32)
+    s = lib.dev(np.array([1e-3], np.float32))
+    outs = []
+    try:
+        for on in (True, False):
+            # In-store epilogues take the persistent kernel only when asked (2).
+            os.environ["ORMI_GEMM_PERSIST"] = "2" if on else "0"
+            g = GemmDesc(dtype=0, M=M, N=N, K=K, a=lib.dev(A), b=lib.dev(B), c=lib.dev(D.copy()))
+            g.a_stride_m, g.a_stride_k, g.b_stride_k, g.b_stride_n = K, 1, N, 1
+            aux = None
+            if kind == "sgd":
+                e = GemmEpilogue(kind=1, form=1, s=s, d=g.c, d_stride_m=N, d_stride_n=1)
+            elif kind == "gelu_aux":
+                aux = lib.dev(np.zeros((M, N)))
+                e = GemmEpilogue(kind=2, fn=7, aux=aux)
+            else:
+                e = GemmEpilogue(kind=3, fn=8, d=lib.dev(D), d_stride_m=N, d_stride_n=1)
+            assert lib.ormi_hip_gemm_ex(ctypes.byref(g), ctypes.byref(e)) == 0, lib.ormi_hip_last_error()
+            outs.append((lib.read(g.c, (M, N)), lib.read(aux, (M, N)) if aux is not None else None))
+    finally:
+        os.environ.pop("ORMI_GEMM_PERSIST", None)
+    (c1, x1), (c0, x0) = outs
+    np.testing.assert_array_equal(c1, c0)
+    if x1 is not None:
+        np.testing.assert_array_equal(x1, x0)
+    assert np.all(np.isfinite(c1))
