@@ -305,7 +305,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32dma_kernel(GemmParams 
 
     if constexpr (EPI) {
         float dv[TM][TN][16];
-        epi_tile<TM, TN, false>(p.epi, c, p.epi.aux ? p.epi.aux + c_off : nullptr, p.epi.d + d_off, p.N, m0 + wm * WTM,
+        epi_tile<TM, TN, false>(p.epi, p.epi.s ? *p.epi.s : 0.0f, c, p.epi.aux ? p.epi.aux + c_off : nullptr, p.epi.d + d_off, p.N, m0 + wm * WTM,
                                 n0 + wn * WTN, acc, dv, epi_reads_d(p.epi));
         return;
     }
@@ -388,7 +388,11 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32dma_persist_kernel(Gem
     set_load_tile(0);
     lds_char* const lds = (lds_char*)smem;
     float* const c = p.c;
-    asm volatile("" ::"s"(c), "s"(p.M), "s"(p.N));
+    // The epilogue's scale is read once, before the loop: a load of it at
+    // each tile's end would make the compiler drain every outstanding load.
+    const float sv =
+        EPI && p.epi.s ? __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(*p.epi.s))) : 0.0f;
+    asm volatile("" ::"s"(c), "s"(p.M), "s"(p.N), "s"(sv));
 
     f32x16_t acc[TM][TN];
 #pragma unroll
@@ -441,8 +445,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32dma_persist_kernel(Gem
                 // already loading, run on fresh accumulators.
                 if constexpr (EPI) {
                     float dv[TM][TN][16];
-                    epi_tile<TM, TN, false>(p.epi, c, p.epi.aux, p.epi.d, p.N, cm0 + wm * WTM, cn0 + wn * WTN, acc, dv,
-                                            epi_reads_d(p.epi));
+                    epi_tile<TM, TN, false>(p.epi, sv, c, p.epi.aux, p.epi.d, p.N, cm0 + wm * WTM, cn0 + wn * WTN, acc,
+                                            dv, epi_reads_d(p.epi));
                 } else {
 #pragma unroll
                     for (int i = 0; i < TM; ++i) {

@@ -333,10 +333,9 @@ struct TileLoader {
 // otherwise 32x32 block t + 1's are loaded before block t is stored (a lane's
 // blocks are distinct elements, so this holds when D is C itself).
 template <int TM, int TN, bool EARLY_D>
-__device__ __forceinline__ void epi_tile(const Epi& e, float* c, float* aux, const float* dd, int ldc, int row0, int col0,
-                                         const f32x16_t (&acc)[TM][TN], float (&dv)[TM][TN][16], bool reads_d) {
+__device__ __forceinline__ void epi_tile(const Epi& e, float sv, float* c, float* aux, const float* dd, int ldc, int row0,
+                                         int col0, const f32x16_t (&acc)[TM][TN], float (&dv)[TM][TN][16], bool reads_d) {
     const int lane = threadIdx.x & 63;
-    const float sv = e.s ? *e.s : 0.0f;
     if (!reads_d) {
 #pragma unroll
         for (int i = 0; i < TM; ++i)
@@ -539,7 +538,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_kernel(GemmParams p)
     } else {
         // Only without a K split (the host runs the finish pass otherwise),
         // so c_off is the batch offset and aux shares it.
-        epi_tile<TM, TN, EARLY_D>(p.epi, c, p.epi.aux ? p.epi.aux + c_off : nullptr, p.epi.d + d_off, p.N,
+        epi_tile<TM, TN, EARLY_D>(p.epi, p.epi.s ? *p.epi.s : 0.0f, c, p.epi.aux ? p.epi.aux + c_off : nullptr, p.epi.d + d_off, p.N,
                                   m0 + wm * WTM, n0 + wn * WTN, acc, dv, reads_d);
     }
 }
