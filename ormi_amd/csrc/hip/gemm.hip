@@ -423,6 +423,52 @@ __global__ __launch_bounds__(256) void gemm_finish_flat_kernel(float* __restrict
     }
 }
 
+// Operand packing for the GEMMs the fast kernels cannot take as given (a
+// unit-stride extent or another stride not in whole 16-byte chunks, an
+// unaligned base): the operand, rows mn < MN by depth k < K with any element
+// strides and batch strides, is copied into a dense k-contiguous buffer
+// [batch][MN][K_pad] (K_pad a multiple of 64), zero for k >= K, so the product
+// over K_pad equals the one over K exactly. One 64 x 64 block per work-group;
+// an mn-contiguous source is read along mn and transposed through LDS, any
+// other along k.
+struct PackParams {
+    long long s_mn, s_k;
+    int MN, K, K_pad;
+    int batch_ndim;
+    int batch_shape[ORMI_GEMM_MAX_BATCH_DIMS];
+    long long bs[ORMI_GEMM_MAX_BATCH_DIMS];
+};
+
+template <typename T, bool MN_UNIT>
+__global__ __launch_bounds__(256) void gemm_pack_kernel(T* __restrict__ dst, const T* __restrict__ src, PackParams pp) {
+    const int k0 = blockIdx.x * 64, mn0 = blockIdx.y * 64;
+    long long boff = 0;
+    int rest = blockIdx.z;
+    for (int d = pp.batch_ndim - 1; d >= 0; --d) {
+        boff += (long long)(rest % pp.batch_shape[d]) * pp.bs[d];
+        rest /= pp.batch_shape[d];
+    }
+    const T* s = src + boff;
+    T* o = dst + (long long)blockIdx.z * pp.MN * pp.K_pad;
+    if constexpr (MN_UNIT) {
+        __shared__ T tile[64][65];
+        for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+            const int kk = i >> 6, mm = i & 63, k = k0 + kk, mn = mn0 + mm;
+            tile[kk][mm] = (k < pp.K && mn < pp.MN) ? s[(long long)k * pp.s_k + mn] : T(0);
+        }
+        __syncthreads();
+        for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+            const int mm = i >> 6, kk = i & 63, k = k0 + kk, mn = mn0 + mm;
+            if (mn < pp.MN) o[(long long)mn * pp.K_pad + k] = tile[kk][mm];
+        }
+    } else {
+        for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+            const int mm = i >> 6, kk = i & 63, k = k0 + kk, mn = mn0 + mm;
+            if (mn < pp.MN) o[(long long)mn * pp.K_pad + k] = k < pp.K ? s[(long long)mn * pp.s_mn + (long long)k * pp.s_k] : T(0);
+        }
+    }
+}
+
 // Any strides, any shape: 16x16 output tile per block, fp32 accumulation.
 template <int DT>
 __device__ __forceinline__ float gemm_elem(const void* p, long long i) {
@@ -1381,6 +1427,9 @@ static void launch_finish(const ormi_gemm_desc* d, const float* ws, int splits, 
 namespace ormi_hip {
 // Both GEMM entries: noalloc takes the workspace from `scratch` instead of the
 // grown-on-demand buffer.
+static int gemm_run_locked(const ormi_gemm_desc* d, const Epi& epi, long long batch, bool noalloc, bool packed);
+static int gemm_packed_locked(const ormi_gemm_desc* d, const Epi& epi, long long batch);
+
 static int gemm_run(const ormi_gemm_desc* d, const ormi_gemm_epilogue* epi_in, bool noalloc) {
     if (!d) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_gemm: null descriptor");
     if (d->M < 0 || d->N < 0 || d->K < 0) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_gemm: negative dimension");
@@ -1409,6 +1458,81 @@ static int gemm_run(const ormi_gemm_desc* d, const ormi_gemm_epilogue* epi_in, b
 
     // Held until this call's kernels are enqueued (see g_ws_mu).
     std::lock_guard<std::mutex> ws_lock(g_ws_mu);
+    return gemm_run_locked(d, epi, batch, noalloc, false);
+}
+
+// Packed operands (gemm_pack_kernel), grown on demand and kept, like the
+// split-K workspace; used under g_ws_mu.
+static void* g_pack = nullptr;
+static size_t g_pack_bytes = 0;
+
+static int gemm_packed_locked(const ormi_gemm_desc* d, const Epi& epi, long long batch) {
+    const int es = d->dtype == ORMI_DTYPE_F32 ? 4 : 2;
+    const int k_pad = (int)(((long long)d->K + 63) / 64 * 64);
+    if (k_pad < d->K) return fail(ORMI_HIP_ERR_UNSUPPORTED, "ormi_hip_gemm: K too large to pack");
+    auto round256 = [](size_t v) { return (v + 255) / 256 * 256; };
+    const size_t a_bytes = round256((size_t)batch * d->M * k_pad * es);
+    const size_t b_bytes = round256((size_t)batch * d->N * k_pad * es);
+    if (a_bytes + b_bytes > g_pack_bytes) {
+        if (g_pack) {
+            hipError_t e = hipDeviceSynchronize();
+            if (e == hipSuccess) e = hipFree(g_pack);
+            if (e != hipSuccess) return fail(ORMI_HIP_ERR_RUNTIME, std::string("gemm pack buffer free: ") + hipGetErrorString(e));
+            g_pack = nullptr;
+            g_pack_bytes = 0;
+        }
+        const hipError_t e = hipMalloc(&g_pack, a_bytes + b_bytes);
+        if (e != hipSuccess) return fail(ORMI_HIP_ERR_RUNTIME, std::string("gemm pack buffer: ") + hipGetErrorString(e));
+        g_pack_bytes = a_bytes + b_bytes;
+    }
+    char* const pa = (char*)g_pack;
+    char* const pb = pa + a_bytes;
+    auto pack = [&](void* dst, const void* src, int mn, long long s_mn, long long s_k, const int64_t* bs) {
+        PackParams pp{};
+        pp.s_mn = s_mn;
+        pp.s_k = s_k;
+        pp.MN = mn;
+        pp.K = d->K;
+        pp.K_pad = k_pad;
+        pp.batch_ndim = d->batch_ndim;
+        for (int i = 0; i < d->batch_ndim; ++i) {
+            pp.batch_shape[i] = d->batch_shape[i];
+            pp.bs[i] = bs[i];
+        }
+        const dim3 grid(k_pad / 64, (mn + 63) / 64, (unsigned)batch);
+        const bool mn_unit = s_mn == 1 && s_k != 1;
+        if (es == 4) {
+            if (mn_unit) gemm_pack_kernel<float, true><<<grid, 256>>>((float*)dst, (const float*)src, pp);
+            else gemm_pack_kernel<float, false><<<grid, 256>>>((float*)dst, (const float*)src, pp);
+        } else {
+            if (mn_unit) gemm_pack_kernel<unsigned short, true><<<grid, 256>>>((unsigned short*)dst, (const unsigned short*)src, pp);
+            else gemm_pack_kernel<unsigned short, false><<<grid, 256>>>((unsigned short*)dst, (const unsigned short*)src, pp);
+        }
+    };
+    pack(pa, d->a, d->M, d->a_stride_m, d->a_stride_k, d->a_batch_stride);
+    pack(pb, d->b, d->N, d->b_stride_n, d->b_stride_k, d->b_batch_stride);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(ORMI_HIP_ERR_RUNTIME, std::string("ormi_hip_gemm pack: ") + hipGetErrorString(e));
+    // The packed product: both operands k-contiguous over K_pad, dense batches.
+    ormi_gemm_desc dp = *d;
+    dp.K = k_pad;
+    dp.a = pa;
+    dp.a_stride_m = k_pad;
+    dp.a_stride_k = 1;
+    dp.b = pb;
+    dp.b_stride_n = k_pad;
+    dp.b_stride_k = 1;
+    long long inner = 1;
+    for (int i = d->batch_ndim - 1; i >= 0; --i) {
+        dp.a_batch_stride[i] = inner * d->M * k_pad;
+        dp.b_batch_stride[i] = inner * d->N * k_pad;
+        inner *= d->batch_shape[i];
+    }
+    return gemm_run_locked(&dp, epi, batch, false, true);
+}
+
+static int gemm_run_locked(const ormi_gemm_desc* d, const Epi& epi, long long batch, bool noalloc, bool packed) {
+    int rc = ORMI_HIP_OK;
     auto workspace = [noalloc](size_t bytes, void** out) {
         return noalloc ? scratch_locked(bytes, out) : workspace_locked(bytes, out);
     };
@@ -1465,6 +1589,12 @@ static int gemm_run(const ormi_gemm_desc* d, const ormi_gemm_epilogue* epi_in, b
     }
 
     hipError_t e;
+    // Operands the fast kernels cannot take are packed into dense k-contiguous
+    // buffers first, unless the product is small (the generic kernel is then
+    // at its launch floor anyway) or the caller cannot allocate.
+    if (!fast && !packed && !noalloc && (long long)d->M * d->N * d->K >= (1LL << 24) &&
+        env_cfg("ORMI_GEMM_PACK", 1) != 0)
+        return gemm_packed_locked(d, epi, batch);
     if (!fast) {
         dim3 grid((d->N + 15) / 16, (d->M + 15) / 16, (unsigned)batch);
         if (f32) gemm_generic_kernel<ORMI_DTYPE_F32><<<grid, 256>>>(p);
