@@ -1181,9 +1181,12 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_ilp_kernel(GemmParams p) 
 //                       10: 256x256, 2x4, 4 stages  11: 256x256, 4x2, 4 stages
 //   interleaved with whole-line A loads (A k-contiguous, K % 64 == 0, else 9):
 //                       12: 256x256, 2x2, 3 A pair slots + 4 B slots
-// The defaults: 12 where it applies (NN 4096^3 116.8 -> 112.4 us, NT 121.6 ->
-// 114.3 us on one box, bit-identical), otherwise 9, the fastest of 0-11 on
-// MI355X for NN, NT and TN at 4096^3.
+//   interleaved, BK 32, smaller tiles: 13: 128x128, 2x2, 4 stages (64 KB)
+//                       14: 128x256, 2x2, 4 stages
+// The defaults: 13 when 256x256 tiles do not fill the compute units;
+// otherwise 12 where it applies (NN 4096^3 116.8 -> 112.4 us, NT 121.6 ->
+// 114.3 us on one box, bit-identical), else 9, the fastest of 0-11 on MI355X
+// for NN, NT and TN at 4096^3.
 template <typename Tr, int BM, int BN, int WGM, int WGN>
 struct DmaLauncher {
     static constexpr Cfg cfg{BM, BN, 64};
@@ -1252,6 +1255,8 @@ static Cfg cfg_dma(int id) {
         case 9: return IlLauncher<Tr, 256, 256, 2, 2, 4>::cfg;
         case 10: return IlLauncher<Tr, 256, 256, 2, 4, 4>::cfg;
         case 12: return IlpLauncher<Tr, 256, 256, 2, 2>::cfg;
+        case 13: return IlLauncher<Tr, 128, 128, 2, 2, 4>::cfg;
+        case 14: return IlLauncher<Tr, 128, 256, 2, 2, 4>::cfg;
         default: return IlLauncher<Tr, 256, 256, 4, 2, 4>::cfg;
     }
 }
@@ -1270,6 +1275,8 @@ static void run_dma(int id, const GemmParams& p, dim3 grid, bool a_kc, bool b_kc
         case 9: IlLauncher<Tr, 256, 256, 2, 2, 4>::run(p, grid, a_kc, b_kc); break;
         case 10: IlLauncher<Tr, 256, 256, 2, 4, 4>::run(p, grid, a_kc, b_kc); break;
         case 12: IlpLauncher<Tr, 256, 256, 2, 2>::run(p, grid, a_kc, b_kc); break;
+        case 13: IlLauncher<Tr, 128, 128, 2, 2, 4>::run(p, grid, a_kc, b_kc); break;
+        case 14: IlLauncher<Tr, 128, 256, 2, 2, 4>::run(p, grid, a_kc, b_kc); break;
         default: IlLauncher<Tr, 256, 256, 4, 2, 4>::run(p, grid, a_kc, b_kc); break;
     }
 }
@@ -1612,9 +1619,14 @@ static int gemm_run_locked(const ormi_gemm_desc* d, const Epi& epi, long long ba
     // less than 4 GB.
     const long long a_span = a_kc ? 256LL * d->a_stride_m * 2 : 64LL * d->a_stride_k * 2 + 512;
     const long long b_span = b_kc ? 256LL * d->b_stride_n * 2 : 64LL * d->b_stride_k * 2 + 512;
-    // Default: whole-line A loads (12) when A is k-contiguous and K is in
-    // whole 64-deep pairs, else the interleaved 4-stage kernel (9).
-    const int dma_id = env_cfg("ORMI_GEMM_DMA_CFG", a_kc && d->K % 64 == 0 ? 12 : 9);
+    // Default: 256x256 tiles when they alone fill the compute units, with
+    // whole-line A loads (12) if A is k-contiguous and K is in whole 64-deep
+    // pairs, else the interleaved 4-stage kernel (9); smaller outputs take
+    // 128x128 tiles (13), two work-groups per compute unit (one box: 2048^2 x
+    // 1024 35.4 -> 14.7 us, 3072^3 96.3 -> 76.5 us, 512 x 4096^2 37.8 -> 29.0 us).
+    const long long tiles256 = (long long)((d->M + 255) / 256) * ((d->N + 255) / 256) * batch;
+    const int dma_dflt = tiles256 < compute_units() ? 13 : a_kc && d->K % 64 == 0 ? 12 : 9;
+    const int dma_id = env_cfg("ORMI_GEMM_DMA_CFG", dma_dflt);
     const int dma_bk = f32 ? 64 : cfg_dma<TrBF16>(dma_id).BK;
     const bool dma = !f32 && env_cfg("ORMI_GEMM_DMA", 1) != 0 && d->K % dma_bk == 0 && (a_kc || d->M % 8 == 0) &&
                      (b_kc || d->N % 8 == 0) && a_span < (1LL << 32) && b_span < (1LL << 32);
@@ -1627,6 +1639,16 @@ static int gemm_run_locked(const ormi_gemm_desc* d, const Epi& epi, long long ba
     cfg32_dma(dma32_id, &dma32_bm, &dma32_bn, &dma32_bk);
     const bool dma32 = f32 && env_cfg("ORMI_GEMM_F32_DMA", 1) != 0 && d->K % dma32_bk == 0 && (a_kc || d->M % 4 == 0) &&
                        (b_kc || d->N % 4 == 0) && a_span32 < (1LL << 32) && b_span32 < (1LL << 32);
+    // A large product whose layout the direct-load kernels cannot take (K not
+    // in whole tiles, an mn-contiguous extent not in whole 16-byte chunks) is
+    // packed for them too, rather than run on the register-staged kernels: one
+    // box, fp32 3000^2 x 1000 218.7 -> 203.5 us, 2000 x 4000 x 1000 161.5 ->
+    // 153.8 us. Below 2^32 multiply-adds the packing costs more than it gains
+    // (fp32 1000^3 33.7 -> 47.5 us).
+    const bool direct_on = env_cfg(f32 ? "ORMI_GEMM_F32_DMA" : "ORMI_GEMM_DMA", 1) != 0;
+    if (!packed && !noalloc && direct_on && !(f32 ? dma32 : dma) && (long long)d->M * d->N * d->K >= (1LL << 32) &&
+        env_cfg("ORMI_GEMM_PACK", 1) != 0)
+        return gemm_packed_locked(d, epi, batch);
     int id = dma ? dma_id
              : dma32 ? dma32_id
              : f32 ? env_cfg("ORMI_GEMM_CFG32", -1)

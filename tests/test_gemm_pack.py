@@ -1,9 +1,10 @@
-"""GEMMs whose operands the fast kernels cannot take as given, through the
-C-ABI: a unit-stride extent or another stride not in whole 16-byte chunks
-(odd N, odd K, odd leading dimensions), or no unit stride at all. Such
-operands are packed into dense k-contiguous buffers, zero-padded along K to a
-multiple of 64, and the product runs on the MFMA kernels (ORMI_GEMM_PACK=0
-keeps the generic kernel instead). Each result is checked against the float64
+"""GEMMs whose operands the direct-load kernels cannot take as given, through
+the C-ABI: a unit-stride extent or another stride not in whole 16-byte chunks
+(odd N, odd K, odd leading dimensions), no unit stride at all, or K not in
+whole tiles. Such operands are packed into dense k-contiguous buffers,
+zero-padded along K to a multiple of 64, and the product runs on the
+direct-load MFMA kernels (ORMI_GEMM_PACK=0 keeps the generic or
+register-staged kernel instead). Each result is checked against the float64
 product of the operand values within 2 K eps32 (|A| |B|), on both paths, with
 batches (one operand broadcast) and an epilogue in the finish pass."""
 import ctypes
@@ -138,3 +139,18 @@ def test_packed_batches_with_broadcast_and_epilogue(lib):
     got = run(lib, BF16, a_bits, b_bits, M, N, K, (K, 1), (N, 1), True, batch=(nb, M * K, 0), epi=e, out=c)
     prod = run(lib, BF16, a_bits, b_bits, M, N, K, (K, 1), (N, 1), True, batch=(nb, M * K, 0))
     np.testing.assert_array_equal(got, D - prod * np.float32(0.01))
+
+
+def test_large_product_with_k_not_in_whole_tiles_is_packed(lib):
+    """An fp32 product of 2^32 multiply-adds or more whose K (4100) is not a
+    multiple of the direct-load depth: packed to K 4160 and run on the
+    direct-load kernel instead of the register-staged one."""
+    rng = np.random.default_rng(159)
+    M, N, K = 1024, 1024, 4100
+    assert M * N * K >= 1 << 32
+    a_bits, a64 = host(rng.standard_normal((M, K)) / 8, F32)
+    b_bits, b64 = host(rng.standard_normal((K, N)) / 8, F32)
+    want, bd = a64 @ b64, bound(a64, b64, K)
+    for pack in (True, False):
+        got = run(lib, F32, a_bits, b_bits, M, N, K, (K, 1), (N, 1), pack)
+        assert np.all(np.abs(got - want) <= bd), pack
