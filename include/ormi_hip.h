@@ -132,9 +132,13 @@ int ormi_hip_rtc_cache_size(uint64_t* entries);
  * arrays (reference csrc/backend/cuda/kernels/blas/matmul.cu:19-112,
  * interface cuda_matmul.cuh:6-12). Row-major semantics of the reference:
  *   C[b][m][n] = sum_k A[b][m][k] * B[b][k][n]
- * A[m][k] lives at a + m*a_stride_m + k*a_stride_k (elements); one of the two
- * strides must be 1 (stride_k == 1: "N", stride_m == 1: "T", the reference's
- * trans rule matmul.cu:47-52). Same for B with (stride_k, stride_n).
+ * A[m][k] lives at a + m*a_stride_m + k*a_stride_k (elements); normally one of
+ * the two strides is 1 (stride_k == 1: "N", stride_m == 1: "T", the reference's
+ * trans rule matmul.cu:47-52). Same for B with (stride_k, stride_n). Other
+ * strides are accepted: for a large product such operands (and those whose
+ * unit-stride extent or other strides are not whole 16-byte chunks) are first
+ * copied into a zero-padded, k-contiguous device buffer the library keeps and
+ * grows on demand; small products run a generic kernel.
  * C is written contiguous: C[b][m][n] at c + b*M*N + m*N + n, fp32.
  * dtype: ORMI_DTYPE_F32 (fp32 MFMA), ORMI_DTYPE_BF16 or ORMI_DTYPE_F16
  * (MFMA with fp32 accumulation). Batch index b decomposes row-major over
