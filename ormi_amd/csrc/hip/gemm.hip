@@ -1713,16 +1713,17 @@ static int gemm_run_locked(const ormi_gemm_desc* d, const Epi& epi, long long ba
     }
     dim3 grid(p.tiles_m * p.tiles_n, 1, (unsigned)(batch * splits));
     // fp32 default configuration with more whole tiles than compute units, one
-    // batch, no K split and no epilogue in the store: one persistent
-    // work-group per compute unit walks its tiles as one stream of k-tiles
-    // (ORMI_GEMM_PERSIST=0 turns it off; =2 takes in-store epilogues too,
-    // whose main loop measured 4% slower there).
+    // batch and no K split: one persistent work-group per compute unit walks
+    // its tiles as one stream of k-tiles (ORMI_GEMM_PERSIST=0 turns it off).
+    // An activation epilogue in the store keeps the one-tile kernel (=2 takes
+    // it too): with the activations compiled into the loop's kernel, its main
+    // loop measured 3% slower at K = 4096.
     const int persist_env = env_cfg("ORMI_GEMM_PERSIST", 1);
     const bool persist = dma32 && dma32_id == 1 && even && splits == 1 && batch == 1 && tiles > cus &&
-                         persist_env != 0 && (p.epi.kind == ORMI_GEMM_EPI_NONE || persist_env == 2);
+                         persist_env != 0 && (p.epi.kind != ORMI_GEMM_EPI_UNARY || persist_env == 2);
     if (dma && d->dtype == ORMI_DTYPE_BF16) run_dma<TrBF16>(id, p, grid, a_kc, b_kc);
     else if (dma) run_dma<TrF16>(id, p, grid, a_kc, b_kc);
-    else if (dma32 && persist) run32_dma_persist(p, cus, a_kc, b_kc, p.epi.kind != ORMI_GEMM_EPI_NONE);
+    else if (dma32 && persist) run32_dma_persist(p, cus, a_kc, b_kc);
     else if (dma32) run32_dma(id, p, grid, a_kc, b_kc, p.epi.kind != ORMI_GEMM_EPI_NONE);
     else if (f32 && p.epi.kind != ORMI_GEMM_EPI_NONE) run32_epi(id, p, grid, a_kc, b_kc);
     else if (f32) run32(id, p, grid, even, a_kc, b_kc);

@@ -331,8 +331,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32dma_kernel(GemmParams 
 // flight while the previous tile finishes, and its stores drain while the
 // next tile's MFMAs run. The per-launch fill, the epilogue's latency and the
 // work-group turnover are paid once per work-group instead of once per tile.
-template <int BM, int BN, int BK, int WGM, int WGN, int STAGES, bool A_KC, bool B_KC, bool EPI>
+// EK: the epilogue kind compiled in (ORMI_GEMM_EPI_*; NONE: plain stores).
+template <int BM, int BN, int BK, int WGM, int WGN, int STAGES, bool A_KC, bool B_KC, int EK>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32dma_persist_kernel(GemmParams p) {
+    constexpr bool EPI = EK != ORMI_GEMM_EPI_NONE;
     static_assert(STAGES >= 2 && STAGES <= 5, "2 to 5 stages");
     using St = Il32<BM, BN, BK, WGM, WGN, A_KC, B_KC>;
     constexpr int TM = St::TM, TN = St::TN, WTM = St::WTM, WTN = St::WTN, KS = St::KS;
@@ -445,8 +447,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32dma_persist_kernel(Gem
                 // already loading, run on fresh accumulators.
                 if constexpr (EPI) {
                     float dv[TM][TN][16];
-                    epi_tile<TM, TN, false>(p.epi, sv, c, p.epi.aux, p.epi.d, p.N, cm0 + wm * WTM, cn0 + wn * WTN, acc,
-                                            dv, epi_reads_d(p.epi));
+                    epi_tile<TM, TN, false, EK>(p.epi, sv, c, p.epi.aux, p.epi.d, p.N, cm0 + wm * WTM, cn0 + wn * WTN,
+                                                acc, dv, epi_reads_d(p.epi));
                 } else {
 #pragma unroll
                     for (int i = 0; i < TM; ++i) {
@@ -490,15 +492,27 @@ struct F32DmaLauncher {
         else go<false, false>(p, grid, epi);
     }
     template <bool A_KC, bool B_KC>
-    static void go_persist(const GemmParams& p, int groups, bool epi) {
-        if (epi) gemm_f32dma_persist_kernel<BM, BN, BK, WGM, WGN, STAGES, A_KC, B_KC, true><<<groups, 64 * WGM * WGN>>>(p);
-        else gemm_f32dma_persist_kernel<BM, BN, BK, WGM, WGN, STAGES, A_KC, B_KC, false><<<groups, 64 * WGM * WGN>>>(p);
+    static void go_persist(const GemmParams& p, int groups) {
+        constexpr int NT = 64 * WGM * WGN;
+        switch (p.epi.kind) {
+            case ORMI_GEMM_EPI_ADD:
+                gemm_f32dma_persist_kernel<BM, BN, BK, WGM, WGN, STAGES, A_KC, B_KC, ORMI_GEMM_EPI_ADD><<<groups, NT>>>(p);
+                break;
+            case ORMI_GEMM_EPI_UNARY:
+                gemm_f32dma_persist_kernel<BM, BN, BK, WGM, WGN, STAGES, A_KC, B_KC, ORMI_GEMM_EPI_UNARY><<<groups, NT>>>(p);
+                break;
+            case ORMI_GEMM_EPI_MUL_FN_D:
+                gemm_f32dma_persist_kernel<BM, BN, BK, WGM, WGN, STAGES, A_KC, B_KC, ORMI_GEMM_EPI_MUL_FN_D><<<groups, NT>>>(p);
+                break;
+            default:
+                gemm_f32dma_persist_kernel<BM, BN, BK, WGM, WGN, STAGES, A_KC, B_KC, ORMI_GEMM_EPI_NONE><<<groups, NT>>>(p);
+        }
     }
-    static void run_persist(const GemmParams& p, int groups, bool a_kc, bool b_kc, bool epi) {
-        if (a_kc && b_kc) go_persist<true, true>(p, groups, epi);
-        else if (a_kc) go_persist<true, false>(p, groups, epi);
-        else if (b_kc) go_persist<false, true>(p, groups, epi);
-        else go_persist<false, false>(p, groups, epi);
+    static void run_persist(const GemmParams& p, int groups, bool a_kc, bool b_kc) {
+        if (a_kc && b_kc) go_persist<true, true>(p, groups);
+        else if (a_kc) go_persist<true, false>(p, groups);
+        else if (b_kc) go_persist<false, true>(p, groups);
+        else go_persist<false, false>(p, groups);
     }
 };
 
@@ -519,8 +533,8 @@ void cfg32_dma(int id, int* bm, int* bn, int* bk) {
     *bn = id == 2 ? 256 : 128;
     *bk = id == 4 || id == 5 ? 64 : 32;
 }
-void run32_dma_persist(const GemmParams& p, int groups, bool a_kc, bool b_kc, bool epi) {
-    F32DmaLauncher<128, 128, 32, 2, 4, 4>::run_persist(p, groups, a_kc, b_kc, epi);
+void run32_dma_persist(const GemmParams& p, int groups, bool a_kc, bool b_kc) {
+    F32DmaLauncher<128, 128, 32, 2, 4, 4>::run_persist(p, groups, a_kc, b_kc);
 }
 void run32_dma(int id, const GemmParams& p, dim3 grid, bool a_kc, bool b_kc, bool epi) {
     if (id < 0 || id > 5) id = 1;

@@ -332,7 +332,8 @@ struct TileLoader {
 // element. EARLY_D: dv already holds them (loaded during the last k-tile);
 // otherwise 32x32 block t + 1's are loaded before block t is stored (a lane's
 // blocks are distinct elements, so this holds when D is C itself).
-template <int TM, int TN, bool EARLY_D>
+// ONLY >= 0 compiles in that epilogue kind alone (the caller guarantees e.kind).
+template <int TM, int TN, bool EARLY_D, int ONLY = -1>
 __device__ __forceinline__ void epi_tile(const Epi& e, float sv, float* c, float* aux, const float* dd, int ldc, int row0,
                                          int col0, const f32x16_t (&acc)[TM][TN], float (&dv)[TM][TN][16], bool reads_d) {
     const int lane = threadIdx.x & 63;
@@ -372,19 +373,28 @@ __device__ __forceinline__ void epi_tile(const Epi& e, float sv, float* c, float
             }
         }
     };
-    if (e.kind == ORMI_GEMM_EPI_ADD) {
-        const bool scaled = e.s != nullptr;
-        const int form = e.form;
-        each([&](long long ci, float d, float v) {
-            const float t = scaled ? v * sv : v;
-            c[ci] = form == 0 ? d + t : form == 1 ? d - t : t - d;
-        });
-    } else if (e.kind == ORMI_GEMM_EPI_UNARY) {
-        epi_dispatch_unary(e.fn, [&](auto fn) {
-            if (aux) each([&](long long ci, float, float v) { aux[ci] = v; c[ci] = epi_fn_t<decltype(fn)::value>(v); });
-            else each([&](long long ci, float, float v) { c[ci] = epi_fn_t<decltype(fn)::value>(v); });
-        });
-    } else {
+    const int kind = ONLY >= 0 ? ONLY : e.kind;
+    if constexpr (ONLY < 0 || ONLY == ORMI_GEMM_EPI_ADD) {
+        if (kind == ORMI_GEMM_EPI_ADD) {
+            const bool scaled = e.s != nullptr;
+            const int form = e.form;
+            each([&](long long ci, float d, float v) {
+                const float t = scaled ? v * sv : v;
+                c[ci] = form == 0 ? d + t : form == 1 ? d - t : t - d;
+            });
+            return;
+        }
+    }
+    if constexpr (ONLY < 0 || ONLY == ORMI_GEMM_EPI_UNARY) {
+        if (kind == ORMI_GEMM_EPI_UNARY) {
+            epi_dispatch_unary(e.fn, [&](auto fn) {
+                if (aux) each([&](long long ci, float, float v) { aux[ci] = v; c[ci] = epi_fn_t<decltype(fn)::value>(v); });
+                else each([&](long long ci, float, float v) { c[ci] = epi_fn_t<decltype(fn)::value>(v); });
+            });
+            return;
+        }
+    }
+    if constexpr (ONLY < 0 || ONLY == ORMI_GEMM_EPI_MUL_FN_D) {
         epi_dispatch_grad(e.fn, [&](auto fn) {
             each([&](long long ci, float d, float v) { c[ci] = v * epi_fn_t<decltype(fn)::value>(d); });
         });
@@ -554,7 +564,7 @@ void cfg32_dma(int id, int* bm, int* bn, int* bk);
 void run32_dma(int id, const GemmParams& p, dim3 grid, bool a_kc, bool b_kc, bool epi);
 // The persistent form of the default direct-load configuration (1): `groups`
 // work-groups walk the p.tiles_m x p.tiles_n tiles; whole tiles, one batch,
-// no K split.
-void run32_dma_persist(const GemmParams& p, int groups, bool a_kc, bool b_kc, bool epi);
+// no K split; p.epi (its kind compiled in) applied in the store.
+void run32_dma_persist(const GemmParams& p, int groups, bool a_kc, bool b_kc);
 
 }  // namespace ormi_hip

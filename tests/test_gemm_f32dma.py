@@ -206,7 +206,7 @@ def test_persistent_kernel_epilogues_match_one_tile_kernel(lib, kind):
     outs = []
     try:
         for on in (True, False):
-            # In-store epilogues take the persistent kernel only when asked (2).
+            # Activation epilogues take the persistent kernel only when asked (2).
             os.environ["ORMI_GEMM_PERSIST"] = "2" if on else "0"
             g = GemmDesc(dtype=0, M=M, N=N, K=K, a=lib.dev(A), b=lib.dev(B), c=lib.dev(D.copy()))
             g.a_stride_m, g.a_stride_k, g.b_stride_k, g.b_stride_n = K, 1, N, 1
