@@ -1183,7 +1183,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_ilp_kernel(GemmParams p) 
 //                       12: 256x256, 2x2, 3 A pair slots + 4 B slots
 //   interleaved, BK 32, smaller tiles: 13: 128x128, 2x2, 4 stages (64 KB)
 //                       14: 128x256, 2x2, 4 stages
-// The defaults: 13 when 256x256 tiles do not fill the compute units;
+//   whole-line A loads, 128x128: 15 (3 A pair slots + 4 B slots, 80 KB)
+// The defaults: 15 (or 13) when 256x256 tiles do not fill the compute units;
 // otherwise 12 where it applies (NN 4096^3 116.8 -> 112.4 us, NT 121.6 ->
 // 114.3 us on one box, bit-identical), else 9, the fastest of 0-11 on MI355X
 // for NN, NT and TN at 4096^3.
@@ -1257,6 +1258,7 @@ static Cfg cfg_dma(int id) {
         case 12: return IlpLauncher<Tr, 256, 256, 2, 2>::cfg;
         case 13: return IlLauncher<Tr, 128, 128, 2, 2, 4>::cfg;
         case 14: return IlLauncher<Tr, 128, 256, 2, 2, 4>::cfg;
+        case 15: return IlpLauncher<Tr, 128, 128, 2, 2>::cfg;
         default: return IlLauncher<Tr, 256, 256, 4, 2, 4>::cfg;
     }
 }
@@ -1277,6 +1279,7 @@ static void run_dma(int id, const GemmParams& p, dim3 grid, bool a_kc, bool b_kc
         case 12: IlpLauncher<Tr, 256, 256, 2, 2>::run(p, grid, a_kc, b_kc); break;
         case 13: IlLauncher<Tr, 128, 128, 2, 2, 4>::run(p, grid, a_kc, b_kc); break;
         case 14: IlLauncher<Tr, 128, 256, 2, 2, 4>::run(p, grid, a_kc, b_kc); break;
+        case 15: IlpLauncher<Tr, 128, 128, 2, 2>::run(p, grid, a_kc, b_kc); break;
         default: IlLauncher<Tr, 256, 256, 4, 2, 4>::run(p, grid, a_kc, b_kc); break;
     }
 }
@@ -1619,13 +1622,14 @@ static int gemm_run_locked(const ormi_gemm_desc* d, const Epi& epi, long long ba
     // less than 4 GB.
     const long long a_span = a_kc ? 256LL * d->a_stride_m * 2 : 64LL * d->a_stride_k * 2 + 512;
     const long long b_span = b_kc ? 256LL * d->b_stride_n * 2 : 64LL * d->b_stride_k * 2 + 512;
-    // Default: 256x256 tiles when they alone fill the compute units, with
-    // whole-line A loads (12) if A is k-contiguous and K is in whole 64-deep
-    // pairs, else the interleaved 4-stage kernel (9); smaller outputs take
-    // 128x128 tiles (13), two work-groups per compute unit (one box: 2048^2 x
-    // 1024 35.4 -> 14.7 us, 3072^3 96.3 -> 76.5 us, 512 x 4096^2 37.8 -> 29.0 us).
+    // Default: 256x256 tiles when they alone fill the compute units, else
+    // 128x128 tiles with two work-groups per compute unit (one box: 2048^2 x
+    // 1024 35.4 -> 14.0 us, 3072^3 96.3 -> 66.7 us, 512 x 4096^2 37.8 -> 26.9
+    // us); either with whole-line A loads (12, 15) if A is k-contiguous and K
+    // is in whole 64-deep pairs, else the interleaved 4-stage kernel (9, 13).
     const long long tiles256 = (long long)((d->M + 255) / 256) * ((d->N + 255) / 256) * batch;
-    const int dma_dflt = tiles256 < compute_units() ? 13 : a_kc && d->K % 64 == 0 ? 12 : 9;
+    const bool whole_line = a_kc && d->K % 64 == 0;
+    const int dma_dflt = tiles256 < compute_units() ? (whole_line ? 15 : 13) : (whole_line ? 12 : 9);
     const int dma_id = env_cfg("ORMI_GEMM_DMA_CFG", dma_dflt);
     const int dma_bk = f32 ? 64 : cfg_dma<TrBF16>(dma_id).BK;
     const bool dma = !f32 && env_cfg("ORMI_GEMM_DMA", 1) != 0 && d->K % dma_bk == 0 && (a_kc || d->M % 8 == 0) &&

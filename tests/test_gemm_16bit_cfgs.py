@@ -1,7 +1,7 @@
 """16-bit GEMM configurations through the C-ABI (ORMI_GEMM_DMA_CFG, read per
-call): the whole-line kernel for a k-contiguous A (configuration 12, the
-default for NN and NT with K a multiple of 64) against the interleaved
-half-line kernel (configuration 9). Both run the same MFMAs in the same order,
+call): the whole-line kernel for a k-contiguous A (configurations 12 and 15,
+256x256 and 128x128 tiles, the defaults for NN and NT with K a multiple of 64)
+against the interleaved half-line kernel of the same tile (9 and 13). Both run the same MFMAs in the same order,
 so with the same K split (none: ORMI_GEMM_MAX_SPLITS=1; the two kernels'
 depths, 64 and 32, would otherwise choose different splits for some shapes)
 their outputs must be bit-identical. Each result, the default's with its own K
@@ -100,11 +100,13 @@ def test_whole_line_kernel_matches_interleaved_bit_for_bit(lib, dt, layout):
         b_store = b_bits if layout[1] == "N" else np.ascontiguousarray(b_bits.T)
         want = a64 @ b64
         bound = 2 * K * np.finfo(np.float32).eps * (np.abs(a64) @ np.abs(b64))
-        got9 = gemm(lib, 9, dt, a_store, b_store, M, N, K, layout, split=False)
-        got12 = gemm(lib, 12, dt, a_store, b_store, M, N, K, layout, split=False)
+        # (interleaved, whole-line) pairs: 256x256 tiles (9, 12), 128x128 (13, 15).
+        for half, whole in ((9, 12), (13, 15)):
+            got_h = gemm(lib, half, dt, a_store, b_store, M, N, K, layout, split=False)
+            got_w = gemm(lib, whole, dt, a_store, b_store, M, N, K, layout, split=False)
+            assert np.all(np.abs(got_h - want) <= bound), (half, layout, M, N, K)
+            assert np.array_equal(got_w, got_h), (whole, layout, M, N, K)
         got = gemm(lib, None, dt, a_store, b_store, M, N, K, layout)
-        assert np.all(np.abs(got9 - want) <= bound), (layout, M, N, K)
-        assert np.array_equal(got12, got9), (layout, M, N, K)
         assert np.all(np.abs(got - want) <= bound), (layout, M, N, K)
 
 
@@ -116,9 +118,10 @@ def test_whole_line_kernel_batches_with_broadcast_b(lib, layout):
     b_bits, b64 = to_16(rng.standard_normal((K, N)) / 8, BF16)
     a_store = a_bits if layout[0] == "N" else None
     b_store = b_bits if layout[1] == "N" else np.ascontiguousarray(b_bits.T)
-    got12 = gemm(lib, 12, BF16, a_store, b_store, M, N, K, layout, batch=batch, split=False)
-    got9 = gemm(lib, 9, BF16, a_store, b_store, M, N, K, layout, batch=batch, split=False)
     want = a64 @ b64
     bound = 2 * K * np.finfo(np.float32).eps * (np.abs(a64) @ np.abs(b64))
-    assert np.all(np.abs(got12 - want) <= bound)
-    assert np.array_equal(got12, got9)
+    for half, whole in ((9, 12), (13, 15)):
+        got_w = gemm(lib, whole, BF16, a_store, b_store, M, N, K, layout, batch=batch, split=False)
+        got_h = gemm(lib, half, BF16, a_store, b_store, M, N, K, layout, batch=batch, split=False)
+        assert np.all(np.abs(got_w - want) <= bound), whole
+        assert np.array_equal(got_w, got_h), whole
