@@ -1221,6 +1221,7 @@ namespace ormi::hip {
     namespace {
         struct KeyBuf {
             std::string s;
+            KeyBuf() { s.reserve(512); }
             void i64(long long v) { s.append(reinterpret_cast<const char*>(&v), sizeof v); }
         };
         void key_expr(KeyBuf& kb, const Expr& e) {
@@ -1262,10 +1263,29 @@ namespace ormi::hip {
             for (const auto& [slot, src] : k.ptr_slots)
                 k.args[slot] = (uint64_t)(uintptr_t)(src >= 0 ? e.leaves[src].ptr : outs[-1 - src]);
         }
+        // The cached launch c for this request's buffers: with launch_only and a
+        // compiled kernel, only what launch() reads.
+        KernelLaunch instantiate(const KernelLaunch& c, const Expr& e, const void* const* outs, bool launch_only) {
+            if (!launch_only || !c.handle) {
+                KernelLaunch k = c;
+                patch(k, e, outs);
+                return k;
+            }
+            KernelLaunch k;
+            k.handle = c.handle;
+            for (int i = 0; i < 3; ++i) {
+                k.grid[i] = c.grid[i];
+                k.block[i] = c.block[i];
+            }
+            k.args = c.args;
+            for (const auto& [slot, src] : c.ptr_slots)
+                k.args[slot] = (uint64_t)(uintptr_t)(src >= 0 ? e.leaves[src].ptr : outs[-1 - src]);
+            return k;
+        }
     }  // namespace
 
     KernelLaunch plan_map_multi(const Expr& expr, const std::vector<int>& shape, const std::vector<void*>& outs,
-                                const std::vector<DType>& out_dtypes, int cu) {
+                                const std::vector<DType>& out_dtypes, int cu, bool launch_only) {
         if (outs.size() != expr.roots.size() || outs.size() != out_dtypes.size() || outs.empty())
             throw std::runtime_error("HIP codegen: one output buffer and dtype per root.");
         KeyBuf kb;
@@ -1281,9 +1301,7 @@ namespace ormi::hip {
             auto it = rc.maps.find(kb.s);
             if (it != rc.maps.end()) {
                 refresh_handle(it->second);
-                KernelLaunch k = it->second;
-                patch(k, expr, outs.data());
-                return k;
+                return instantiate(it->second, expr, outs.data(), launch_only);
             }
         }
         KernelLaunch k = plan_map_multi_uncached(expr, shape, outs, out_dtypes, cu);
@@ -1293,12 +1311,13 @@ namespace ormi::hip {
         return k;
     }
 
-    KernelLaunch plan_map(const Expr& expr, const std::vector<int>& shape, void* out, DType out_dtype, int cu) {
-        return plan_map_multi(expr, shape, {out}, {out_dtype}, cu);
+    KernelLaunch plan_map(const Expr& expr, const std::vector<int>& shape, void* out, DType out_dtype, int cu,
+                          bool launch_only) {
+        return plan_map_multi(expr, shape, {out}, {out_dtype}, cu, launch_only);
     }
 
     ReducePlan plan_reduce(const Expr& expr, const std::vector<int>& in_shape, const std::vector<int>& axes, ReduceOp op,
-                           void* out, int cu) {
+                           void* out, int cu, bool launch_only) {
         KeyBuf kb;
         kb.i64('R');
         kb.i64(cu);
@@ -1316,9 +1335,11 @@ namespace ormi::hip {
             if (it != rc.reduces.end()) {
                 refresh_handle(it->second.first);
                 if (it->second.two_pass) refresh_handle(it->second.second);
-                ReducePlan plan = it->second;
-                patch(plan.first, expr, outs);
-                if (plan.two_pass) patch(plan.second, expr, outs);
+                ReducePlan plan;
+                plan.two_pass = it->second.two_pass;
+                plan.workspace_bytes = it->second.workspace_bytes;
+                plan.first = instantiate(it->second.first, expr, outs, launch_only);
+                if (plan.two_pass) plan.second = instantiate(it->second.second, expr, outs, launch_only);
                 return plan;
             }
         }

@@ -10,6 +10,7 @@
 #include <unordered_set>
 
 #include "backend/hip/hip_backend.h"
+#include "backend/hip/small_containers.h"
 #include "runtime/runtime.h"
 
 namespace ormi::hip {
@@ -20,11 +21,22 @@ namespace ormi::hip {
         return t;
     }
 
-    void HIPLoweringRegistry::register_func(OpEnum op, LoweringFunc f) { lowering_table()[op] = std::move(f); }
-    bool HIPLoweringRegistry::has(OpEnum op) { return lowering_table().count(op) > 0; }
+    // The registered function per op, indexed by the op's value: the graph
+    // walks ask for every node they visit. unordered_map elements keep their
+    // addresses across inserts, so the pointers stay valid.
+    constexpr size_t kOpSlots = 64;
+    static_assert((size_t)OpEnum::CAST < kOpSlots, "op table too small");
+    static const LoweringFunc* lowering_slots[kOpSlots] = {};
+
+    void HIPLoweringRegistry::register_func(OpEnum op, LoweringFunc f) {
+        LoweringFunc& slot = lowering_table()[op];
+        slot = std::move(f);
+        lowering_slots[(size_t)op] = &slot;
+    }
+    bool HIPLoweringRegistry::has(OpEnum op) { return find(op) != nullptr; }
     const LoweringFunc* HIPLoweringRegistry::find(OpEnum op) {
-        auto it = lowering_table().find(op);
-        return it == lowering_table().end() ? nullptr : &it->second;
+        const size_t i = (size_t)op;
+        return i < kOpSlots ? lowering_slots[i] : nullptr;
     }
     LoweringFunc HIPLoweringRegistry::get(OpEnum op) {
         auto it = lowering_table().find(op);
@@ -64,19 +76,21 @@ namespace ormi::hip {
 
     std::vector<NodePtr> region_frontier(const NodePtr& root) {
         std::vector<NodePtr> frontier;
-        std::unordered_set<Node*> seen{root.get()};
-        std::vector<NodePtr> stack{root};
+        SmallSet<Node> seen;
+        seen.insert(root.get());
+        SmallVec<Node*, 64> stack;
+        stack.push_back(root.get());
         size_t interior = 1;
         while (!stack.empty()) {
-            NodePtr n = stack.back();
+            Node* n = stack.back();
             stack.pop_back();
             for (const auto& p : n->parents) {
-                if (!seen.insert(p.get()).second) continue;
+                if (!seen.insert(p.get())) continue;
                 if (p->is_realized()) continue;
                 // Past kMaxRegion interior nodes, element-wise nodes become frontier:
                 // they are realized first, as regions of their own.
                 if (fusible_interior(*p) && interior < kMaxRegion) {
-                    stack.push_back(p);
+                    stack.push_back(p.get());
                     ++interior;
                 } else {
                     frontier.push_back(p);
@@ -88,15 +102,17 @@ namespace ormi::hip {
 
     size_t region_size(const NodePtr& root, size_t limit) {
         if (root->is_realized() || !fusible_root(*root)) return 0;
-        std::unordered_set<Node*> seen{root.get()};
-        std::vector<NodePtr> stack{root};
+        SmallSet<Node> seen;
+        seen.insert(root.get());
+        SmallVec<Node*, 64> stack;
+        stack.push_back(root.get());
         size_t interior = 1;
         while (!stack.empty() && interior <= limit) {
-            NodePtr n = stack.back();
+            Node* n = stack.back();
             stack.pop_back();
             for (const auto& p : n->parents) {
-                if (!seen.insert(p.get()).second || p->is_realized() || !fusible_interior(*p)) continue;
-                stack.push_back(p);
+                if (!seen.insert(p.get()) || p->is_realized() || !fusible_interior(*p)) continue;
+                stack.push_back(p.get());
                 ++interior;
             }
         }
@@ -136,23 +152,25 @@ namespace ormi::hip {
 
     Expr build_expr_multi(const std::vector<NodePtr>& roots, const std::vector<int>& shape, bool plan_only) {
         Expr e;
-        std::unordered_map<Node*, int> value_of;
-        std::unordered_set<Node*> root_set;
+        e.leaves.reserve(8);
+        e.roots.reserve(roots.size());
+        SmallMap<Node, int> value_of;
+        SmallSet<Node, 8> root_set;
         for (const auto& r : roots) root_set.insert(r.get());
         // Post-order DFS over the union of the roots' regions: leaves get ids as
         // first seen, interior nodes after all their operands. A node shared by
         // several roots (or a root inside another root's region) is one value.
-        struct Frame { NodePtr n; size_t next; };
-        std::vector<Frame> stack;
-        auto is_interior = [&](const NodePtr& n) {
-            return root_set.count(n.get()) ? fusible_root(*n) : fusible_interior(*n);
+        struct Frame { Node* n; size_t next; };
+        SmallVec<Frame, 64> stack;
+        auto is_interior = [&](const Node* n) {
+            return root_set.contains(n) ? fusible_root(*n) : fusible_interior(*n);
         };
         auto visit_leaf = [&](const NodePtr& n) {
             const int id = (int)e.leaves.size();
             e.leaves.push_back(make_leaf(n, shape, plan_only));
-            value_of[n.get()] = id;
+            value_of.insert(n.get(), id);
         };
-        if (roots.size() == 1 && !is_interior(roots[0])) {
+        if (roots.size() == 1 && !is_interior(roots[0].get())) {
             // A realized node (or a reduction input that is already a buffer):
             // the tape is the identity on one leaf.
             visit_leaf(roots[0]);
@@ -160,45 +178,53 @@ namespace ormi::hip {
             e.roots = {0};
             return e;
         }
-        std::vector<NodePtr> interior_post;
-        std::unordered_set<Node*> on_stack;
+        SmallVec<Node*, 64> interior_post;
+        SmallSet<Node> on_stack;
         for (const auto& root : roots) {
-            if (!is_interior(root)) throw std::runtime_error("HIP codegen: a grouped root is not an element-wise node.");
-            if (value_of.count(root.get())) continue;  // inside an earlier root's region
+            if (!is_interior(root.get())) throw std::runtime_error("HIP codegen: a grouped root is not an element-wise node.");
+            if (value_of.find(root.get())) continue;  // inside an earlier root's region
             on_stack.insert(root.get());
-            stack.push_back({root, 0});
+            stack.push_back({root.get(), 0});
             while (!stack.empty()) {
                 Frame& f = stack.back();
                 if (f.next < f.n->parents.size()) {
-                    NodePtr p = f.n->parents[f.next++];
-                    if (value_of.count(p.get()) || on_stack.count(p.get())) continue;
-                    if (!p->is_realized() && is_interior(p)) {
+                    const NodePtr& p = f.n->parents[f.next++];
+                    if (value_of.find(p.get()) || on_stack.contains(p.get())) continue;
+                    if (!p->is_realized() && is_interior(p.get())) {
                         on_stack.insert(p.get());
-                        stack.push_back({p, 0});
+                        stack.push_back({p.get(), 0});
                     } else {
                         if (!p->is_realized()) throw std::runtime_error("HIP codegen: region input was not realized first.");
                         visit_leaf(p);
                     }
                 } else {
-                    interior_post.push_back(f.n);
-                    value_of[f.n.get()] = -1;  // assigned below
-                    on_stack.erase(f.n.get());
+                    Node* n = f.n;
+                    interior_post.push_back(n);
+                    value_of.insert(n, -1);  // assigned below
+                    on_stack.erase(n);
                     stack.pop_back();
                 }
             }
         }
         const int nleaves = (int)e.leaves.size();
-        for (size_t k = 0; k < interior_post.size(); ++k) value_of[interior_post[k].get()] = nleaves + (int)k;
-        for (const auto& n : interior_post) {
+        for (size_t k = 0; k < interior_post.size(); ++k) value_of.set(interior_post[k], nleaves + (int)k);
+        auto id_of = [&](const Node* n) {
+            const int* v = value_of.find(n);
+            if (!v) throw std::runtime_error("HIP codegen: operand without a value.");
+            return *v;
+        };
+        e.insts.reserve(interior_post.size());
+        for (size_t k = 0; k < interior_post.size(); ++k) {
+            const Node* n = interior_post[k];
             Inst in;
             in.op = n->op;
-            in.a = value_of.at(n->parents[0].get());
-            if (ops::op_arity(n->op) == 2) in.b = value_of.at(n->parents[1].get());
+            in.a = id_of(n->parents[0].get());
+            if (ops::op_arity(n->op) == 2) in.b = id_of(n->parents[1].get());
             if (n->op == OpEnum::CAST) in.cast = std::get<CastAttrs>(n->attrs).dtype;
             else in.lower = HIPLoweringRegistry::find(n->op);
             e.insts.push_back(in);
         }
-        for (const auto& r : roots) e.roots.push_back(value_of.at(r.get()));
+        for (const auto& r : roots) e.roots.push_back(id_of(r.get()));
         e.root = e.roots[0];
         return e;
     }

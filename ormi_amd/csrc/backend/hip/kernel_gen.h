@@ -112,10 +112,14 @@ namespace ormi::hip {
     const Tuning& tuning();
 
     // Element-wise map of expr over `shape` into out (contiguous, out_dtype).
-    KernelLaunch plan_map(const Expr& expr, const std::vector<int>& shape, void* out, DType out_dtype, int compute_units);
+    // launch_only: the caller only launches the result, so a repeat request
+    // whose kernel is compiled returns just the handle, launch shape and
+    // arguments (no name, signature or plan text to copy).
+    KernelLaunch plan_map(const Expr& expr, const std::vector<int>& shape, void* out, DType out_dtype, int compute_units,
+                          bool launch_only = false);
     // The same with one contiguous output per expr.roots entry (multi-output fusion).
     KernelLaunch plan_map_multi(const Expr& expr, const std::vector<int>& shape, const std::vector<void*>& outs,
-                                const std::vector<DType>& out_dtypes, int compute_units);
+                                const std::vector<DType>& out_dtypes, int compute_units, bool launch_only = false);
 
     // Reduction of expr (evaluated over in_shape) over `axes` (sorted; empty =
     // all). out holds prod(kept dims) values, fp32 (Sum/Max) or int64 (Argmax).
@@ -129,7 +133,7 @@ namespace ormi::hip {
         size_t workspace_bytes = 0;
     };
     ReducePlan plan_reduce(const Expr& expr, const std::vector<int>& in_shape, const std::vector<int>& axes, ReduceOp op,
-                           void* out, int compute_units);
+                           void* out, int compute_units, bool launch_only = false);
     void bind_workspace(ReducePlan& plan, void* workspace);
 
     // Source text of a planned kernel: a plan that hit the kernel cache after

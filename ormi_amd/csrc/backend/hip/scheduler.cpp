@@ -23,6 +23,7 @@
 #include <vector>
 
 #include "backend/hip/hip_backend.h"
+#include "backend/hip/small_containers.h"
 #include "core/allocator.h"
 #include "core/memory.h"
 #include "runtime/graph_breakers.h"
@@ -73,7 +74,7 @@ namespace ormi::hip {
             return;
         }
         const Expr e = build_expr(x, in_shape);
-        ReducePlan plan = plan_reduce(e, in_shape, attrs.axes, op, out->ptr, device_compute_units());
+        ReducePlan plan = plan_reduce(e, in_shape, attrs.axes, op, out->ptr, device_compute_units(), true);
         std::shared_ptr<Buffer> ws;
         if (plan.two_pass) {
             ws = empty({(int)((plan.workspace_bytes + 3) / 4)}, DeviceEnum::HIP, DType::Float32);
@@ -368,7 +369,8 @@ namespace ormi::hip {
     // activation f(p) the same graph holds, which stores p and f(p) from one
     // GEMM (identical values either way).
     struct RealizeScope {
-        std::vector<NodePtr> roots;
+        const NodePtr* roots = nullptr;  // the outermost call's roots, alive for the scope
+        size_t nroots = 0;
         bool indexed = false;
         std::unordered_map<Node*, NodePtr> act;  // product -> f(product)
     };
@@ -377,10 +379,11 @@ namespace ormi::hip {
     struct ScopeGuard {
         RealizeScope scope;
         bool owner;
-        // Roots are copied only by the owner: nested realizes allocate nothing.
+        // The roots belong to the outermost caller, which outlives the scope.
         ScopeGuard(const NodePtr* roots, size_t n) : owner(t_scope == nullptr) {
             if (!owner) return;
-            scope.roots.assign(roots, roots + n);
+            scope.roots = roots;
+            scope.nroots = n;
             t_scope = &scope;
         }
         ~ScopeGuard() {
@@ -398,8 +401,10 @@ namespace ormi::hip {
             sc.indexed = true;
             std::vector<NodePtr> stack;
             std::unordered_set<Node*> seen;
-            for (const auto& r : sc.roots)
+            for (size_t i = 0; i < sc.nroots; ++i) {
+                const NodePtr& r = sc.roots[i];
                 if (r && !r->is_realized() && seen.insert(r.get()).second) stack.push_back(r);
+            }
             while (!stack.empty()) {
                 const NodePtr n = stack.back();
                 stack.pop_back();
@@ -426,7 +431,7 @@ namespace ormi::hip {
         root->data = out;
         root->view.strides = calc_contiguous_strides(root->view.shape);
         if (out->numel() == 0) return;
-        launch(plan_map(e, root->view.shape, out->ptr, root->dtype, device_compute_units()));
+        launch(plan_map(e, root->view.shape, out->ptr, root->dtype, device_compute_units(), true));
     }
 
     // Nodes that must hold buffers before `n` can run as one step: a view's
@@ -482,15 +487,16 @@ namespace ormi::hip {
     void realize(const NodePtr& root) {
         if (!root || root->is_realized()) return;
         ScopeGuard guard(&root, 1);
-        std::vector<NodePtr> stack{root};
-        std::unordered_set<Node*> expanded;
+        SmallVec<NodePtr, 16> stack;
+        stack.push_back(root);
+        SmallSet<Node> expanded;
         while (!stack.empty()) {
             const NodePtr n = stack.back();
             if (n->is_realized()) {
                 stack.pop_back();
                 continue;
             }
-            if (expanded.insert(n.get()).second) {
+            if (expanded.insert(n.get())) {
                 bool pushed = false;
                 for (const auto& d : dependencies(n)) {
                     if (d->is_realized()) continue;
@@ -545,7 +551,7 @@ namespace ormi::hip {
                 outs.push_back(bufs.back()->ptr);
                 dts.push_back(m->dtype);
             }
-            if (shape_numel(shape) > 0) launch(plan_map_multi(e, shape, outs, dts, device_compute_units()));
+            if (shape_numel(shape) > 0) launch(plan_map_multi(e, shape, outs, dts, device_compute_units(), true));
             for (size_t i = 0; i < live.size(); ++i) {
                 live[i]->data = bufs[i];
                 live[i]->view.strides = calc_contiguous_strides(live[i]->view.shape);

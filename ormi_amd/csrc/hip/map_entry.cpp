@@ -136,7 +136,7 @@ ORMI_EXPORT int ormi_hip_map(const ormi_map_desc* d) {
     rc = ormi_hip::ensure_init();
     if (rc != ORMI_HIP_OK) return rc;
     try {
-        launch(plan_map_multi(r.expr, r.shape, r.outs, r.out_dtypes, ormi_hip::compute_units()));
+        launch(plan_map_multi(r.expr, r.shape, r.outs, r.out_dtypes, ormi_hip::compute_units(), true));
     } catch (const std::exception& e) {
         return fail(ORMI_HIP_ERR_RUNTIME, std::string("ormi_hip_map: ") + e.what());
     }

@@ -142,7 +142,7 @@ ORMI_EXPORT int ormi_hip_reduce(const ormi_reduce_desc* d) {
         return ormi_hip_fill(d->out, &zero, 4, (size_t)r.out_numel);
     }
     try {
-        ReducePlan plan = plan_reduce(input_expr(d, r), r.shape, r.axes, r.op, d->out, ormi_hip::compute_units());
+        ReducePlan plan = plan_reduce(input_expr(d, r), r.shape, r.axes, r.op, d->out, ormi_hip::compute_units(), true);
         std::unique_lock<std::mutex> lock(g_mu, std::defer_lock);
         if (plan.two_pass) {
             void* ws = d->workspace;
