@@ -4,6 +4,7 @@
 #include <hip/hiprtc.h>
 
 #include <atomic>
+#include <chrono>
 #include <condition_variable>
 #include <cstdlib>
 #include <cstring>
@@ -286,11 +287,19 @@ struct LaunchQueue {
             const uint64_t t = tail.load(std::memory_order_relaxed);
             if (head.load(std::memory_order_acquire) == t) {
                 if (stop.load()) return;
-                // Spin for a while (launches tend to come in bursts), then sleep.
+                // Spin (yielding) for kSpin after the last launch, then sleep:
+                // launches come in bursts separated by host work (building the
+                // next graph, a training step's Python), and a launch that has
+                // to wake a sleeping worker waits tens of microseconds for it.
+                constexpr auto kSpin = std::chrono::microseconds(2000);
+                const auto spin_end = std::chrono::steady_clock::now() + kSpin;
                 bool got = false;
-                for (int i = 0; i < 20000 && !got; ++i) {
+                for (int i = 0; !got; ++i) {
                     if (head.load(std::memory_order_acquire) != t) got = true;
-                    else if ((i & 63) == 63) std::this_thread::yield();
+                    else if ((i & 63) == 63) {
+                        if (std::chrono::steady_clock::now() >= spin_end) break;
+                        std::this_thread::yield();
+                    }
                 }
                 if (!got) {
                     std::unique_lock<std::mutex> lock(sleep_mu);
