@@ -320,6 +320,30 @@ typedef struct ormi_map_desc {
 } ormi_map_desc;
 int ormi_hip_map(const ormi_map_desc* desc);
 
+/* ------------------------------------------------------ fused reduction --
+ * ormi_hip_reduce over the values of an element-wise tape instead of a stored
+ * input. Where the reference realizes the producer into a buffer and then
+ * sums that buffer (csrc/backend/runtime.cpp:16-18 realizes every parent
+ * first; cuda::sum, csrc/backend/cuda/kernels/reduce/cuda_sum.cuh:5-11), the
+ * tape here runs as the reduction kernel's prologue and its values are never
+ * stored: the fusion scheduler's reduction with a fused producer, for callers
+ * that hold only this library. prologue is an ormi_map_desc whose shape is the
+ * reduction's input shape; num_outputs must be 1 and output_values[0] names
+ * the reduced value (its buffer and dtype fields are not read and may be
+ * NULL). op, axes (over prologue->shape; naxes 0 = all), out and the
+ * optional workspace are as in ormi_reduce_desc. */
+typedef struct ormi_reduce_map_desc {
+    const ormi_map_desc* prologue;
+    int                  op;                       /* ORMI_REDUCE_*                    */
+    int                  naxes;
+    int                  axes[ORMI_REDUCE_MAX_DIMS];
+    void*                out;
+    void*                workspace;                /* optional (NULL: library-owned)   */
+    size_t               workspace_bytes;
+} ormi_reduce_map_desc;
+int ormi_hip_reduce_map_workspace_size(const ormi_reduce_map_desc* desc, size_t* bytes);
+int ormi_hip_reduce_map(const ormi_reduce_map_desc* desc);
+
 /* ---------------------------------------------------------------- timing --
  * HIP events on the library's stream, for measuring kernel time from
  * outside (benchmarks). */

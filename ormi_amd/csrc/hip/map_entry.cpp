@@ -16,6 +16,7 @@
 #include <vector>
 
 #include "backend/hip/kernel_gen.h"
+#include "map_tape.h"
 #include "ormi_hip_internal.h"
 
 #define ORMI_EXPORT extern "C" __attribute__((visibility("default")))
@@ -50,39 +51,46 @@ namespace {
         return true;
     }
 
-    struct Request {
-        Expr expr;
-        std::vector<int> shape;
-        std::vector<void*> outs;
-        std::vector<DType> out_dtypes;
-        long long numel = 1;
-    };
+}  // namespace
 
-    int check(const ormi_map_desc* d, Request* r) {
-        if (!d) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_map: null descriptor");
-        if (d->ndim < 0 || d->ndim > ORMI_MAP_MAX_DIMS) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_map: ndim must be 0..8");
-        r->shape.assign(d->shape, d->shape + d->ndim);
-        for (int e : r->shape) {
-            if (e < 0) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_map: negative extent");
-            if (e > 0 && r->numel > (1LL << 62) / e) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_map: more than 2^62 elements");
-            r->numel *= e;
+namespace ormi_hip {
+    using ormi::DType;
+    using ormi::ops::OpEnum;
+    using ormi::hip::Expr;
+    using ormi::hip::Inst;
+    using ormi::hip::Leaf;
+    using ormi::hip::builtin_lowering;
+
+    int parse_map_tape(const ormi_map_desc* d, const char* who_c, bool with_buffers, MapTape* t) {
+        const std::string who(who_c);
+        if (!d) return fail(ORMI_HIP_ERR_INVALID, who + ": null descriptor");
+        if (d->ndim < 0 || d->ndim > ORMI_MAP_MAX_DIMS) return fail(ORMI_HIP_ERR_INVALID, who + ": ndim must be 0..8");
+        t->shape.assign(d->shape, d->shape + d->ndim);
+        for (int e : t->shape) {
+            if (e < 0) return fail(ORMI_HIP_ERR_INVALID, who + ": negative extent");
+            if (e > 0 && t->numel > (1LL << 62) / e) return fail(ORMI_HIP_ERR_INVALID, who + ": more than 2^62 elements");
+            t->numel *= e;
         }
         if (d->num_leaves < 0 || (d->num_leaves > 0 && !d->leaves))
-            return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_map: num_leaves must be >= 0, with a leaves array");
+            return fail(ORMI_HIP_ERR_INVALID, who + ": num_leaves must be >= 0, with a leaves array");
         if (d->num_insts < 0 || (d->num_insts > 0 && !d->insts))
-            return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_map: num_insts must be >= 0, with an insts array");
-        if (d->num_outputs < 1 || d->num_outputs > ORMI_MAP_MAX_OUTPUTS || !d->output_values || !d->outputs ||
-            !d->output_dtypes)
-            return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_map: num_outputs must be 1..16, with values, buffers and dtypes");
+            return fail(ORMI_HIP_ERR_INVALID, who + ": num_insts must be >= 0, with an insts array");
+        if (with_buffers) {
+            if (d->num_outputs < 1 || d->num_outputs > ORMI_MAP_MAX_OUTPUTS || !d->output_values || !d->outputs ||
+                !d->output_dtypes)
+                return fail(ORMI_HIP_ERR_INVALID, who + ": num_outputs must be 1..16, with values, buffers and dtypes");
+        } else if (d->num_outputs != 1 || !d->output_values) {
+            return fail(ORMI_HIP_ERR_INVALID, who + ": the prologue has exactly one output value (num_outputs = 1)");
+        }
         const int nval = d->num_leaves + d->num_insts;
-        Expr& e = r->expr;
+        Expr& e = t->expr;
         for (int i = 0; i < d->num_leaves; ++i) {
             const ormi_map_leaf& s = d->leaves[i];
             Leaf L;
-            if (!to_dtype(s.dtype, &L.dtype)) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_map: leaf " + std::to_string(i) + " has an unknown dtype");
-            if (!s.ptr && r->numel > 0) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_map: leaf " + std::to_string(i) + " is null");
+            if (!to_dtype(s.dtype, &L.dtype)) return fail(ORMI_HIP_ERR_INVALID, who + ": leaf " + std::to_string(i) + " has an unknown dtype");
+            if (!s.ptr && t->numel > 0) return fail(ORMI_HIP_ERR_INVALID, who + ": leaf " + std::to_string(i) + " is null");
             if ((uintptr_t)s.ptr % ormi::dtype_size(L.dtype) != 0)
-                return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_map: leaf " + std::to_string(i) + " is not aligned to its element size");
+                return fail(ORMI_HIP_ERR_INVALID, who + ": leaf " + std::to_string(i) + " is not aligned to its element size");
             L.ptr = s.ptr;
             L.scalar = s.scalar != 0;
             L.st.assign(d->ndim, 0);
@@ -92,7 +100,7 @@ namespace {
         }
         for (int k = 0; k < d->num_insts; ++k) {
             const ormi_map_inst& s = d->insts[k];
-            const std::string where = "ormi_hip_map: instruction " + std::to_string(k);
+            const std::string where = who + ": instruction " + std::to_string(k);
             Inst in;
             if (!to_op(s.op, &in.op)) return fail(ORMI_HIP_ERR_INVALID, where + " has an unknown op");
             const int self = d->num_leaves + k;
@@ -113,15 +121,16 @@ namespace {
         }
         for (int o = 0; o < d->num_outputs; ++o) {
             const int v = d->output_values[o];
-            if (v < 0 || v >= nval) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_map: output " + std::to_string(o) + " names no value");
-            DType dt;
-            if (!to_dtype(d->output_dtypes[o], &dt)) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_map: output " + std::to_string(o) + " has an unknown dtype");
-            if (!d->outputs[o] && r->numel > 0) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_map: output " + std::to_string(o) + " is null");
-            if ((uintptr_t)d->outputs[o] % ormi::dtype_size(dt) != 0)
-                return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_map: output " + std::to_string(o) + " is not aligned to its element size");
+            if (v < 0 || v >= nval) return fail(ORMI_HIP_ERR_INVALID, who + ": output " + std::to_string(o) + " names no value");
             e.roots.push_back(v);
-            r->outs.push_back(d->outputs[o]);
-            r->out_dtypes.push_back(dt);
+            if (!with_buffers) continue;
+            DType dt;
+            if (!to_dtype(d->output_dtypes[o], &dt)) return fail(ORMI_HIP_ERR_INVALID, who + ": output " + std::to_string(o) + " has an unknown dtype");
+            if (!d->outputs[o] && t->numel > 0) return fail(ORMI_HIP_ERR_INVALID, who + ": output " + std::to_string(o) + " is null");
+            if ((uintptr_t)d->outputs[o] % ormi::dtype_size(dt) != 0)
+                return fail(ORMI_HIP_ERR_INVALID, who + ": output " + std::to_string(o) + " is not aligned to its element size");
+            t->outs.push_back(d->outputs[o]);
+            t->out_dtypes.push_back(dt);
         }
         e.root = e.roots[0];
         return ORMI_HIP_OK;
@@ -129,8 +138,8 @@ namespace {
 }
 
 ORMI_EXPORT int ormi_hip_map(const ormi_map_desc* d) {
-    Request r;
-    int rc = check(d, &r);
+    ormi_hip::MapTape r;
+    int rc = ormi_hip::parse_map_tape(d, "ormi_hip_map", true, &r);
     if (rc != ORMI_HIP_OK) return rc;
     if (r.numel == 0) return ORMI_HIP_OK;
     rc = ormi_hip::ensure_init();
