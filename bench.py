@@ -383,6 +383,11 @@ def bench_c1(ev: Events, n: int) -> dict:
         loss.backward()
         return loss, [A.grad, B.grad, C.grad]
 
+    # Sets of 200 realizes, as the step loop below: a C1 kernel runs 3-4 us, so
+    # a set of 30 lasts about 100 us, and the start of a set (the launch
+    # thread's first launch after the start event) adds about 0.2 us per
+    # realize to it (one box: 3.3 us per realize in sets of 50, 3.1 in 400).
+    n = max(n, 200)
     ms_f = timed_launches(ev, fwd, n)
     ms_b = timed_launches(ev, lambda i: _Grads(*grads(i), grouped=False), n)
     ms_g = timed_launches(ev, lambda i: _Grads(*grads(i), grouped=True), n)
@@ -408,7 +413,8 @@ def bench_c1(ev: Events, n: int) -> dict:
             "bwd_separate_us": round(ms_b * 1e3, 2), "bwd_separate_GB/s": round(bb / ms_b / 1e6, 1),
             "bwd_grouped_us": round(ms_g * 1e3, 2), "bwd_grouped_GB/s": round(gb / ms_g / 1e6, 1),
             "bwd_step_wall_us": round(step_ms * 1e3, 1),
-            "note": "fwd: one fused reduce kernel (12,587,008 B); bwd_separate: one fused kernel per gradient root "
+            "note": "per realize, HIP events over sets of 200 pre-built graphs; "
+                    "fwd: one fused reduce kernel (12,587,008 B); bwd_separate: one fused kernel per gradient root "
                     "(3 x 16,777,216 B); bwd_grouped: realize_all, one multi-output kernel (25,165,824 B); "
                     "bwd_step_wall_us: host-inclusive loop (graph build + backward + realize_all + zero_grad_graph)"}
 
