@@ -11,7 +11,9 @@ within the fp32 sum bound of the tape's values (n eps32 sum|v|), max and argmax
 exactly. Cases: the C1 forward (relu(a*b + c) * 0.5 summed over each row), a
 column sum and a global sum of a broadcast-bias map, max and argmax of a scaled
 and shifted input, a bf16 leaf, a two-pass reduction with the caller's
-workspace and with the library's, and empty inputs.
+workspace and with the library's, empty inputs, and 24 random tapes (every op,
+broadcast / transposed / scalar / 16-bit leaves) under random reductions,
+bit for bit against the graph path.
 CPU: descriptor validation (no compute)."""
 import ctypes
 
@@ -228,5 +230,69 @@ def test_reduce_map_empty_inputs(lib, hip):
         d = rdesc(pro, ARGMAX, (0,), out)
         assert lib.ormi_hip_reduce_map(ctypes.byref(d)) == 3
         assert b"no identity" in lib.ormi_hip_last_error()
+    finally:
+        dev.free()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(24))
+def test_random_tapes_reduce_as_the_graph_path(ob, lib, hip, seed):
+    """Random tapes (every op, broadcast / transposed / scalar / 16-bit leaves,
+    the generator of test_map_cabi) plus a full-shape leaf added to the last
+    value, reduced by a random op over random axes: the C-ABI result equals
+    the graph path's (a reduction of the same unrealized region) bit for bit,
+    NaN and infinities included."""
+    from ormi_amd import Tensor
+    from test_map_cabi import BINARY, DT_NAME, random_case
+
+    rng = np.random.default_rng(1000 + seed)
+    shape, leaves, insts, _ = random_case(seed)
+    nl = len(leaves)
+    full = rng.uniform(-2, 2, shape).astype(np.float32)
+    leaves = leaves + [dict(kind="plain", dtype=F32, data=full)]
+    bump = lambda v: v + 1 if v >= nl else v  # instruction values move up past the new leaf
+    insts = [(name, bump(a), bump(b) if b >= 0 else b, dt) for name, a, b, dt in insts]
+    last = nl + len(insts)                    # the old last value, renumbered
+    insts.append(("ADD", last, nl, F32))
+    value = nl + len(insts)
+    op = int(rng.integers(0, 3))
+    nd = len(shape)
+    if op == ARGMAX:
+        axes = [int(rng.integers(0, nd))]
+    else:
+        axes = sorted(set(int(a) for a in rng.integers(0, nd, int(rng.integers(1, nd + 1)))))
+        if rng.random() < 0.3:
+            axes = []
+    dev = Dev(lib)
+    try:
+        nodes, cleaves = [], []
+        for L in leaves:
+            t = Tensor(L["data"] if L["kind"] != "T" else np.ascontiguousarray(L["data"].T), hip,
+                       dtype=DT_NAME[L["dtype"]])
+            if L["kind"] == "T":
+                t = t.transpose().realize()
+            n = t._node
+            nodes.append(n)
+            if L["kind"] == "scalar":
+                cleaves.append((n.data.ptr, L["dtype"], True, [0] * nd))
+                continue
+            lshape, lst = list(n.view.shape), list(n.view.strides)
+            off = nd - len(lshape)
+            cleaves.append((n.data.ptr, L["dtype"], False, [0] * off + [0 if e == 1 else s for e, s in zip(lshape, lst)]))
+        opc = ob.OpEnum
+        for name, a, b, dt in insts:
+            if name == "CAST":
+                nodes.append(ob.cast(nodes[a], DT_NAME[dt]))
+            elif name in BINARY:
+                nodes.append(ob._binary(getattr(opc, name), nodes[a], nodes[b]))
+            else:
+                nodes.append(ob._unary(getattr(opc, name), nodes[a]))
+        fn = {SUM: ob.sum, MAX: ob.max, ARGMAX: ob.argmax}[op]
+        g = fn(nodes[value], axes if axes else list(range(nd)), False)
+        ob.execute_graph(g)
+        want = np.asarray(ob.buffer_to_numpy(g.data)).reshape(-1)
+        got, _ = run(lib, dev, tuple(shape), cleaves, insts, value, op, tuple(axes))
+        got = got.reshape(-1)
+        assert got.dtype == want.dtype and np.array_equal(bits(got), bits(want)), (seed, shape, insts, op, axes)
     finally:
         dev.free()
