@@ -2,34 +2,34 @@
 // accumulate) or fp32 inputs (fp32 MFMA). Replaces the reference's
 // cublasSgemmBatched call (csrc/backend/cuda/kernels/blas/matmul.cu:98-105).
 //
-// Design
-//   * Block tile BM x BN x BK, WGM x WGN wave64s; each wave owns a
-//     (BM/WGM) x (BN/WGN) sub-tile of 32x32 MFMA tiles
-//     (v_mfma_f32_32x32x16_{bf16,f16}, or v_mfma_f32_32x32x2_f32).
-//   * Operands sit in LDS as [mn][k] rows of BK elements plus 16 bytes of
-//     padding (144-byte rows), so every MFMA operand fragment is one
-//     conflict-free 16-byte ds_read per lane (fp32 mn-contiguous operands:
-//     [k][mn] rows, below). LDS is double-buffered: the next
-//     k-tile is fetched from HBM into registers while the current one feeds the
-//     MFMAs, and fragments for the next k-step are read from LDS while the
-//     current k-step's MFMAs issue.
-//   * An operand whose k index is contiguous in memory ("N" for A, "T" for B)
-//     is copied 16 bytes at a time. One whose m/n index is contiguous is
-//     fetched as VE x MC blocks (VE = elements per 16 bytes); 16-bit blocks
-//     are transposed in registers before the LDS store, 32-bit ones stay
-//     k-major in LDS and form fragments from dword reads. NN, NT and TN (the
-//     forward and the two backward GEMMs autograd issues) all run the same
-//     MFMA loop.
+// Kernels, in the order the dispatch (gemm_run_locked) prefers them
+//   * 16-bit direct-load kernels (this file): HBM -> LDS with
+//     global_load_lds_dwordx4 into XOR-swizzled multi-stage rings, 4 waves of
+//     128x128 (256x256 tiles) or 64x64 (128x128 tiles), 32x32x16 MFMAs. A
+//     k-contiguous A with K a multiple of 64 takes whole 128-byte lines per
+//     row (gemm_ilp_kernel, 64-deep A slots); otherwise the interleaved kernel
+//     (gemm_il_kernel). 256x256 tiles when there are at least as many as
+//     compute units, else 128x128.
+//   * fp32 direct-load kernels (gemm_f32dma.hip): 8 waves of 64x32 on
+//     128x128x32 tiles and 32x32x2 fp32 MFMAs; a persistent form walks several
+//     tiles per work-group through one ring when the output has more tiles
+//     than compute units.
+//   * Operands those kernels cannot take as given (a unit-stride extent or
+//     another stride not in whole 16-byte chunks, no unit stride, K not in
+//     whole tiles) are packed into zero-padded k-contiguous buffers first for
+//     large products (gemm_packed_locked).
+//   * Register-staged kernels (gemm_mfma_kernel, gemm_mfma.h) and a plain tiled
+//     kernel cover what remains (small products, the allocation-free entry's
+//     unpackable layouts).
+// Shared by all
 //   * An element-wise epilogue (ormi_hip_gemm_ex) is applied in the store of
-//     the fp32 default configurations (gemm_epi.hip), otherwise in the pass
-//     that finishes a K split.
+//     the fp32 direct-load kernels (gemm_f32dma.hip, gemm_epi.hip), otherwise
+//     in the pass that finishes a K split.
 //   * The tile index is remapped so the 8 XCDs (round-robin block dispatch)
 //     each own a compact group of tiles, sharing operand panels in their L2.
 //   * When the output has too few tiles to occupy the 256 CUs, K is split
 //     across blocks; partial products go to a workspace and a second kernel
 //     adds them in split order (deterministic).
-//   * Shapes or strides the fast path cannot take (alignment, ragged 16-byte
-//     chunks) run a plain tiled kernel instead.
 #include <hip/hip_runtime.h>
 #include <algorithm>
 #include <cstdint>
