@@ -360,3 +360,24 @@ def test_kernel_cache_tells_bf16_from_f16(ob, cpu):
     assert o16["name"] != obf["name"]
     assert "ormi_f32_to_bf16(" in obf["source"].split("extern")[1]
     assert "ormi_f32_to_bf16(" not in o16["source"].split("extern")[1]
+
+
+def test_planner_walks_large_regions(ob, cpu):
+    """A region wider and deeper than the planner's inline walk storage (32
+    visited nodes, 64 stack entries before they move to the heap): a chain
+    v[k+1] = v[k] * v[k-1] + leaf[k] over 150 distinct leaves, so every value
+    is shared by two consumers. The tape holds each leaf and each node once,
+    and a second root inside the first one's region adds nothing."""
+    n = 150
+    leaves = [_cpu(np.full((4, 8), 1.0 + k / n)) for k in range(n + 2)]
+    v = [leaves[0], leaves[1]]
+    for k in range(n):
+        v.append(v[-1] * v[-2] + leaves[k + 2])
+    root = v[-1]._node
+    d = ob._plan_group([root])
+    assert d["num_leaves"] == n + 2
+    assert d["num_insts"] == 2 * n
+    both = ob._plan_group([root, v[n // 2]._node])
+    assert both["num_leaves"] == n + 2 and both["num_insts"] == 2 * n
+    single = ob._plan_kernel(root)
+    assert single["num_args"] > n + 2  # every leaf's pointer is an argument
