@@ -5,8 +5,10 @@ Outputs
   ormi_amd/lib/libormi_core.so     graph, autograd, runtime, HIP backend host code (g++)
   ormi_amd/ormi_backend*.so        pybind11 module (g++)
   oracle/_build/libormi_cpu_oracle.so  CPU oracle, test infrastructure only (g++)
-  oracle/_ref/libormi_ref.so       the reference's own CPU path, a second checker (make -f
-                                   oracle/Makefile.ref; only where /root/reference exists)
+  oracle/_ref/libormi_ref.so       the reference's own CPU path, a second checker, and
+  oracle/_ref/libormi_ref_hip.so   the reference's core with the HIP device plugged in over
+                                   libormi_hip.so (make -f oracle/Makefile.ref; built where
+                                   /root/reference exists, and shipped prebuilt elsewhere)
 
 Run `python -m ormi_amd._build` (or __graft_entry__.build()). Every call
 recompiles everything; objects go to ormi_amd/_build/.
@@ -163,7 +165,7 @@ def build(verbose: bool = False, incremental: bool = False) -> None:
     # The reference's own CPU path, a second checker for the oracle, where its
     # sources are (this container; other machines use the prebuilt file).
     if REF_CSRC.is_dir():
-        _run(["make", "-s", "-f", "oracle/Makefile.ref", f"REF={REF_CSRC}"] + ([] if incremental else ["-B"]), cwd=ROOT)
+        _run(["make", "-s", "-j2", "-f", "oracle/Makefile.ref", f"REF={REF_CSRC}"] + ([] if incremental else ["-B"]), cwd=ROOT)
 
 
 def built() -> bool:

@@ -58,6 +58,10 @@ class V:
     def __truediv__(self, o):
         return self._bin(o, lambda a, b: a / b, lambda a, b, y, g: (g / b, -g * a / (b * b)))
 
+    def __pow__(self, o):
+        return self._bin(o, lambda a, b: a ** b,
+                         lambda a, b, y, g: (g * b * a ** (b - 1.0), g * y * np.log(np.where(a > 0, a, 1.0))))
+
     def _un(self, f, df):
         out = f(self.data)
         return V(out, (self,), lambda g: [g * df(self.data, out)])
@@ -150,3 +154,40 @@ class V:
                 continue
             for p, g in zip(v.parents, v.back(v.grad)):
                 p.grad = g if p.grad is None else p.grad + g
+
+
+def run_program(leaves, ops, outputs, grad_root=-1):
+    """A driver program (oracle.ref_call's format: leaves [(array,
+    requires_grad)], ops [(name, a, b, attr, keepdims)], outputs as value ids or
+    -1 - leaf for a leaf's gradient) evaluated in float64. Returns one float64
+    array per output (None for a leaf the gradient does not reach)."""
+    vals = [V(np.asarray(a, np.float64)) for a, *_ in leaves]
+    un = {"NEG": V.__neg__, "EXP": V.exp, "LOG": V.log, "SIN": V.sin, "COS": V.cos}
+    bi = {"ADD": V.__add__, "SUB": V.__sub__, "MUL": V.__mul__, "DIV": V.__truediv__, "POW": V.__pow__,
+          "MATMUL": V.__matmul__}
+    for name, a, b, attr, keepdims in ops:
+        x = vals[a]
+        if name in un:
+            vals.append(un[name](x))
+        elif name in bi:
+            vals.append(bi[name](x, vals[b]))
+        elif name == "SUM":
+            vals.append(x.sum(axis=tuple(attr) if attr else None, keepdims=bool(keepdims)))
+        elif name == "TRANSPOSE":
+            vals.append(x.transpose(attr))
+        elif name == "RESHAPE":
+            vals.append(x.reshape(attr))
+        elif name == "EXPAND":
+            vals.append(x.expand(attr))
+        else:
+            raise ValueError(name)
+    if grad_root >= 0:
+        vals[grad_root].backward()
+    res = []
+    for o in outputs:
+        if o >= 0:
+            res.append(vals[o].data)
+        else:
+            g = vals[-1 - o].grad
+            res.append(None if g is None or not leaves[-1 - o][1] else g)
+    return res

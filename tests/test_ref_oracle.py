@@ -20,8 +20,9 @@ divides by zero on an expanded (stride-0) view and misreads a transposed one.
 Autograd feeds such views to that sum whenever a broadcast ADD/SUB receives an
 expanded or transposed gradient, so every broadcast ADD/SUB here is followed by
 a unary op (whose adjoint yields a contiguous product) and every transpose or
-sum block is entered through one. Skipped where the reference sources are
-absent (the GPU box)."""
+sum block is entered through one. The library is built where the reference
+sources are (this container) and travels prebuilt with the tree, so these tests
+also run on the GPU box; they skip only when it was never built."""
 import math
 
 import numpy as np
@@ -29,7 +30,7 @@ import pytest
 
 import oracle
 
-pytestmark = pytest.mark.skipif(not oracle.ref_available(), reason="reference CPU path not built (no /root/reference here)")
+pytestmark = pytest.mark.skipif(not oracle.ref_available(), reason="reference CPU path not built (oracle/_ref)")
 
 UNARY = ["NEG", "SIN", "COS"]
 
