@@ -73,7 +73,7 @@ int ormi_hip_free(void* ptr);                                        /* cuMemFre
 int ormi_hip_memset_d8(void* dst, unsigned char value, size_t count);/* cuMemsetD8   allocator.cu:58,81 */
 int ormi_hip_memset_d32(void* dst, uint32_t value, size_t count);    /* cuMemsetD32  allocator.cu:76 */
 /* Fill count elements of elem_bytes (1, 2, 4 or 8) with the pattern at value
- * (a kernel, so it is safe inside stream capture). fill_n for every dtype. */
+ * (a small kernel, not hipMemset). fill_n for every dtype. */
 int ormi_hip_fill(void* dst, const void* value, size_t elem_bytes, size_t count);
 /* cuMemcpyHtoD allocator.cu:94, stream-ordered: src is copied into pinned
  * staging before the call returns (the caller may reuse it at once) and the
@@ -211,17 +211,18 @@ typedef struct ormi_gemm_epilogue {
 int ormi_hip_gemm_ex(const ormi_gemm_desc* desc, const ormi_gemm_epilogue* epi);
 
 /* ormi_hip_gemm_ex without any device allocation. No counterpart in the
- * reference: it is for callers that cannot allocate device memory (code under
- * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
- * Same kernels, same results bit for bit; the split-K partials and the finish
- * pass's input live in a static device array of ORMI_GEMM_NOALLOC_SCRATCH_BYTES
- * that the library's code object carries (held by each GPU until the process
- * ends) instead of the grown-on-demand workspace. A shape whose workspace
- * (batch * M * N * splits * 4 bytes, when the K split or the epilogue needs one)
- * exceeds it returns ORMI_HIP_ERR_INVALID and launches nothing. All calls in a
- * process share the array: the library enqueues each call's kernels under one
- * lock on one stream, so calls through this ABI never overlap; work the caller
- * captures from them and replays concurrently on other streams would race. */
+ * reference: it is for callers that cannot allocate device memory (tight
+ * serving loops, harnesses that forbid hipMalloc). Same kernels, same results
+ * bit for bit; the split-K partials and the finish pass's input live in a
+ * static device array of ORMI_GEMM_NOALLOC_SCRATCH_BYTES that the library's
+ * code object carries (held by each GPU until the process ends) instead of the
+ * grown-on-demand workspace. A shape whose workspace (batch * M * N * splits *
+ * 4 bytes, when the K split or the epilogue needs one) exceeds it returns
+ * ORMI_HIP_ERR_INVALID and launches nothing. Like every entry point it
+ * launches on the null stream, so it cannot be recorded into a HIP graph (the
+ * null stream cannot be captured). All calls in a process share the array:
+ * the library enqueues each call's kernels under one lock on that one stream,
+ * so calls through this ABI never overlap. */
 #define ORMI_GEMM_NOALLOC_SCRATCH_BYTES (32u << 20)
 int ormi_hip_gemm_ex_noalloc(const ormi_gemm_desc* desc, const ormi_gemm_epilogue* epi);
 

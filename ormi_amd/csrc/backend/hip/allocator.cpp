@@ -12,6 +12,8 @@
 // synchronize) and the allocation retried once.
 #include <map>
 #include <mutex>
+#include <stdexcept>
+#include <string>
 #include <unordered_map>
 
 #include "backend/hip/hip_backend.h"
@@ -70,8 +72,12 @@ namespace ormi {
             cached_.emplace(sz, ptr);
         }
 
+        // Returns every cached block to the device. A launch error that the
+        // library still holds (a queued launch that failed) is thrown after
+        // the blocks are freed, so it is reported, not lost.
         void release_cached() {
-            ormi_hip_synchronize();
+            const int rc = ormi_hip_synchronize();
+            const std::string msg = rc != ORMI_HIP_OK ? ormi_hip_last_error() : "";
             std::lock_guard<std::mutex> lock(mu_);
             for (auto& kv : cached_) {
                 ormi_hip_free(kv.second);
@@ -80,6 +86,7 @@ namespace ormi {
             }
             stats_.cached_bytes = 0;
             cached_.clear();
+            if (rc != ORMI_HIP_OK) throw std::runtime_error("HIP Error: " + msg);
         }
 
         hip::AllocatorStats stats() {

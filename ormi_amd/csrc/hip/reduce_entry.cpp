@@ -14,6 +14,7 @@
 //
 // Built with -fvisibility=hidden: only the extern "C" functions are exported.
 #include <algorithm>
+#include <cstdint>
 #include <exception>
 #include <mutex>
 #include <string>
@@ -69,6 +70,9 @@ namespace {
             else r->out_numel *= r->shape[a];
         }
         if (r->out_numel > 0 && !out) return fail(ORMI_HIP_ERR_INVALID, who + ": null output");
+        // fp32 values, or int64 indices for ARGMAX
+        if ((uintptr_t)out % (r->op == ReduceOp::Argmax ? 8 : 4) != 0)
+            return fail(ORMI_HIP_ERR_INVALID, who + ": output is not aligned to its element size");
         return ORMI_HIP_OK;
     }
 
@@ -88,6 +92,8 @@ namespace {
         const int rc = check_reduction("ormi_hip_reduce", d->op, d->ndim, d->shape, d->naxes, d->axes, d->out, r);
         if (rc != ORMI_HIP_OK) return rc;
         if (r->in_numel > 0 && !d->in) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_reduce: null input");
+        if ((uintptr_t)d->in % ormi::dtype_size(r->dtype) != 0)
+            return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_reduce: input is not aligned to its element size");
         return ORMI_HIP_OK;
     }
 
@@ -145,6 +151,8 @@ namespace {
     // Plan, bind a workspace (the caller's, else the library's) and launch.
     int run(const std::string& who, const Expr& expr, const Request& r, void* out, void* workspace,
             size_t workspace_bytes) {
+        // the partials are fp32 values and int32 positions
+        if ((uintptr_t)workspace % 4 != 0) return fail(ORMI_HIP_ERR_INVALID, who + ": workspace is not 4-byte aligned");
         if (r.out_numel == 0) return ORMI_HIP_OK;
         int rc = ormi_hip::ensure_init();
         if (rc != ORMI_HIP_OK) return rc;

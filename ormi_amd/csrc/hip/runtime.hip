@@ -467,10 +467,14 @@ int ormi_hip_malloc(void** ptr, size_t bytes) {
     return ORMI_HIP_OK;
 }
 
+// The block is freed even when a queued launch failed (the error of that
+// launch is returned afterwards), so the failure does not leak it.
 int ormi_hip_free(void* ptr) {
     if (!ptr) return ORMI_HIP_OK;
-    ORMI_HIP_DRAIN();
+    const int queued = drain_queue();
+    const std::string queued_msg = queued != ORMI_HIP_OK ? g_last_error : std::string();
     ORMI_HIP_TRY(hipFree(ptr));
+    if (queued != ORMI_HIP_OK) return fail(queued, queued_msg);
     return ORMI_HIP_OK;
 }
 
@@ -636,6 +640,15 @@ int ormi_hip_launch_queued(uint64_t handle, const uint32_t grid[3], const uint32
     if (block[0] * block[1] * block[2] == 0 || block[0] * block[1] * block[2] > 1024)
         return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_launch_queued: block size must be 1..1024 threads");
     return submit_launch(fn, grid, block, lds_bytes, args, num_args);
+}
+
+// Test hook, outside the C ABI of include/ormi_hip.h: records msg as the error
+// of a queued launch, exactly as the launch thread records a launch the runtime
+// refused, so a test can check that the next call reports it without making a
+// launch fail on the device. Touches no device state.
+__attribute__((visibility("default"))) int ormi_hip_test_fail_queued_launch(const char* msg) {
+    launch_queue().record_error(std::string("queued kernel launch: ") + (msg ? msg : ""));
+    return ORMI_HIP_OK;
 }
 
 int ormi_hip_event_create(void** event) {

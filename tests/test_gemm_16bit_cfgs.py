@@ -125,3 +125,31 @@ def test_whole_line_kernel_batches_with_broadcast_b(lib, layout):
         got_h = gemm(lib, half, BF16, a_store, b_store, M, N, K, layout, batch=batch, split=False)
         assert np.all(np.abs(got_w - want) <= bound), whole
         assert np.array_equal(got_w, got_h), whole
+
+
+# Tile counts T = tiles_m * tiles_n (256x256 tiles) that are multiples of 8, so
+# the XCD remap (t -> (t & 7) * T/8 + t/8) runs, with tiles_m not a multiple of
+# the 4-row tile group, so the last group is ragged: 4x8 = 32 (no ragged group),
+# 6x4 = 24 with a ragged M, 5x8 = 40 with a ragged N and an odd number of k-tile
+# pairs, 3x8 = 24 with one pair.
+REMAP_SHAPES = [(1024, 2048, 128), (1400, 1024, 128), (1280, 1896, 192), (700, 2048, 64)]
+
+
+@pytest.mark.parametrize("layout", ["NN", "NT"])
+def test_whole_line_kernel_xcd_remap_and_ragged_groups(lib, layout):
+    """Configuration 12 (the default for 256 or more 256x256 tiles, C4 4096^3
+    included) against 9 where the tile remap and a ragged tile group apply:
+    bit for bit, and within 2 K eps32 (|A| |B|) of the float64 product."""
+    rng = np.random.default_rng(139)
+    for M, N, K in REMAP_SHAPES:
+        tiles = ((M + 255) // 256) * ((N + 255) // 256)
+        assert tiles % 8 == 0
+        a_bits, a64 = to_16(rng.standard_normal((M, K)) / 8, BF16)
+        b_bits, b64 = to_16(rng.standard_normal((K, N)) / 8, BF16)
+        b_store = b_bits if layout[1] == "N" else np.ascontiguousarray(b_bits.T)
+        want = a64 @ b64
+        bound = 2 * K * np.finfo(np.float32).eps * (np.abs(a64) @ np.abs(b64))
+        got_h = gemm(lib, 9, BF16, a_bits, b_store, M, N, K, layout, split=False)
+        got_w = gemm(lib, 12, BF16, a_bits, b_store, M, N, K, layout, split=False)
+        assert np.all(np.abs(got_w - want) <= bound), (layout, M, N, K)
+        assert np.array_equal(got_w, got_h), (layout, M, N, K)

@@ -105,3 +105,29 @@ def test_kernel_with_more_arguments_than_the_queue_holds(ob, hip):
     after = (total * 1.0).realize()           # the big kernel, then a queued map over it
     assert np.array_equal(after.numpy(), np.sum(arrs, axis=0, dtype=np.float32))
     assert np.array_equal(before.numpy(), arrs[0] * 2)
+
+
+def test_failed_queued_launch_is_reported_not_lost(ob, cabi, hip):
+    """A queued launch that failed (recorded through the library's test hook,
+    as the launch thread records a launch the runtime refuses; no kernel runs)
+    is reported by the next call that waits for the queue: empty_cache raises
+    it after returning the cached blocks, and ormi_hip_free returns it after
+    freeing its block. Each report clears it, so the call after succeeds."""
+    cabi.ormi_hip_test_fail_queued_launch.argtypes = [ctypes.c_char_p]
+    X = T(np.ones(1 << 16, np.float32), hip)
+    del X  # one block in the cache
+    assert ob.allocator_stats()["cached_bytes"] > 0
+    assert cabi.ormi_hip_test_fail_queued_launch(b"refused") == 0
+    with pytest.raises(RuntimeError, match="queued kernel launch: refused"):
+        ob.empty_cache()
+    assert ob.allocator_stats()["cached_bytes"] == 0
+    assert cabi.ormi_hip_synchronize() == 0
+
+    p = ctypes.c_void_p()
+    assert cabi.ormi_hip_malloc(ctypes.byref(p), 1 << 20) == 0
+    assert cabi.ormi_hip_test_fail_queued_launch(b"refused again") == 0
+    assert cabi.ormi_hip_free(p) == 1  # ORMI_HIP_ERR_RUNTIME, after the hipFree
+    assert b"queued kernel launch: refused again" in cabi.ormi_hip_last_error()
+    assert cabi.ormi_hip_synchronize() == 0
+    x = np.arange(1024, dtype=np.float32)
+    assert np.array_equal((T(x, hip) * 2.0).numpy(), x * 2)

@@ -49,12 +49,18 @@ def desc(op, dtype, ptr, shape, strides, axes, out, ws=None, ws_bytes=0):
     (dict(axes=(1, 1)), b"repeated axis"),
     (dict(shape=(4, -1)), b"negative extent"),
     (dict(shape=(1 << 30, 1 << 30, 1 << 30)), b"more than 2^62 elements"),
+    (dict(in_=0x1002), b"input is not aligned to its element size"),
+    (dict(in_dtype=BF16, in_=0x1001), b"input is not aligned to its element size"),
+    (dict(out=0x2002), b"output is not aligned to its element size"),
+    (dict(op=ARGMAX, out=0x2004), b"output is not aligned to its element size"),  # int64 indices
+    (dict(ws=0x3002), b"workspace is not 4-byte aligned"),
 ])
 def test_reduce_descriptor_validation(cabi, fields, msg):
-    base = dict(op=SUM, in_dtype=F32, shape=(4, 6), axes=(1,))
+    base = dict(op=SUM, in_dtype=F32, shape=(4, 6), axes=(1,), in_=0x1000, out=0x2000, ws=None)
     base.update(fields)
     shape = base["shape"]
-    d = desc(base["op"], base["in_dtype"], 0x1000, shape, [6] * (len(shape) - 1) + [1], base["axes"], 0x2000)
+    d = desc(base["op"], base["in_dtype"], base["in_"], shape, [6] * (len(shape) - 1) + [1], base["axes"], base["out"],
+             base["ws"], 1 << 20 if base["ws"] else 0)
     if "ndim" in fields:
         d.ndim = fields["ndim"]
     if "naxes" in fields:

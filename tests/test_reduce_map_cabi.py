@@ -61,6 +61,8 @@ def lib(cabi):
     (dict(a=3), b"ormi_hip_reduce_map: instruction 0: operand a must be an earlier value"),
     (dict(value=9), b"output 0 names no value"),
     (dict(out=None), b"null output"),
+    (dict(out=0x2002), b"output is not aligned to its element size"),
+    (dict(op=ARGMAX, out=0x2004), b"output is not aligned to its element size"),  # int64 indices
 ])
 def test_reduce_map_rejects_bad_descriptors(lib, case, msg):
     pro, keep = make_desc((4, 8), [(0x1000, case.get("leaf_dtype", F32), False, (8, 1))],
