@@ -83,8 +83,12 @@ int ormi_hip_memcpy_d2h(void* dst, const void* src, size_t bytes);   /* cuMemcpy
 int ormi_hip_memcpy_d2d(void* dst, const void* src, size_t bytes);   /* cuMemcpyDtoD allocator.cu:62 */
 int ormi_hip_synchronize(void);
 
-/* Contiguous element-type conversion dst[i] = (dst_dtype) src[i]. Float to
- * bf16/fp16 rounds to nearest even. Used for bf16 leaves and casts. */
+/* Contiguous element-type conversion dst[i] = (dst_dtype) src[i]. To a float
+ * type it rounds to nearest even (int64 and int32 values past 2^24 included).
+ * From a float type to an integer type it truncates toward zero, NaN gives 0
+ * and out-of-range values saturate; to bool it is x != 0 (NaN gives true).
+ * Between integer types (bool included) it is exact, an int64 outside the
+ * int32 range saturating. */
 int ormi_hip_convert(void* dst, int dst_dtype, const void* src, int src_dtype, size_t count);
 
 /* ------------------------------------------------------------- hipRTC JIT --

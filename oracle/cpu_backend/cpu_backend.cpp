@@ -125,6 +125,15 @@ namespace ormi::oracle {
         return (long long)f;
     }
 
+    // float -> int32: truncation toward zero, NaN gives 0, values outside
+    // [-2^31, 2^31 - 1] saturate (the int64 rule at 32 bits).
+    static int f32_to_i32(float f) {
+        if (f != f) return 0;
+        if (f >= 2147483648.0f) return 2147483647;
+        if (f <= -2147483648.0f) return (int)0x80000000u;
+        return (int)f;
+    }
+
     static float load_f32(const void* p, DType dt, long long i) {
         switch (dt) {
             case DType::Float32: return ((const float*)p)[i];
@@ -142,7 +151,7 @@ namespace ormi::oracle {
             case DType::BFloat16: ((uint16_t*)p)[i] = f32_to_bf16(v); break;
             case DType::Float16: ((uint16_t*)p)[i] = f32_to_f16(v); break;
             case DType::Int64: ((long long*)p)[i] = f32_to_i64(v); break;
-            case DType::Int32: ((int*)p)[i] = (int)f32_to_i64(v); break;
+            case DType::Int32: ((int*)p)[i] = f32_to_i32(v); break;
             case DType::Bool: ((unsigned char*)p)[i] = v != 0.0f; break;
         }
     }

@@ -140,7 +140,7 @@ namespace ormi::hip {
                 case DType::BFloat16: return "ormi_f32_to_bf16(" + v + ")";
                 case DType::Float16: return "ormi_f32_to_f16(" + v + ")";
                 case DType::Int64: return "ormi_f32_to_i64(" + v + ")";
-                case DType::Int32: return "((int)ormi_f32_to_i64(" + v + "))";
+                case DType::Int32: return "ormi_f32_to_i32(" + v + ")";
                 case DType::Bool: return "((unsigned char)((" + v + ") != 0.0f))";
             }
             return v;

@@ -1,5 +1,7 @@
 // CAST (additive): element type conversion, materialized contiguously.
-// Float -> bf16/fp16 rounds to nearest even.
+// Float -> bf16/fp16 rounds to nearest even. Integer targets (int64, int32,
+// bool) convert the float32 value on store: truncation toward zero with NaN
+// giving 0 and saturation at the type's range, or x != 0 for bool.
 #include <stdexcept>
 #include "core/ops/api.h"
 #include "core/shape.h"
@@ -12,7 +14,6 @@ namespace ormi {
 
     namespace ops {
         NodePtr cast(NodePtr x, DType dtype) {
-            if (dtype == DType::Bool || dtype == DType::Int32) throw std::runtime_error("CAST supports float32, bfloat16, float16 and int64 targets.");
             // A cast to the operand's own type is the operand: nodes are never
             // written after they are realized, so aliasing is invisible, and an
             // int64 value above 2^24 must not round through the fp32 registers

@@ -50,6 +50,14 @@ __device__ __forceinline__ long long ormi_f32_to_i64(float f) {
     if (f <= -9.2233720368547758e18f) return (long long)0x8000000000000000ULL;
     return (long long)f;
 }
+// float -> int32 the same way: truncation toward zero, NaN gives 0, values
+// outside [-2^31, 2^31 - 1] saturate.
+__device__ __forceinline__ int ormi_f32_to_i32(float f) {
+    if (f != f) return 0;
+    if (f >= 2147483648.0f) return 2147483647;
+    if (f <= -2147483648.0f) return (int)0x80000000u;
+    return (int)f;
+}
 
 // ------------------------------------------------------- element-wise ops --
 __device__ __forceinline__ float ormi_relu(float a) { return a > 0.0f ? a : 0.0f; }

@@ -69,11 +69,34 @@ __device__ __forceinline__ float load_as_f32(const void* p, int dt, size_t i) {
     }
 }
 
+__device__ __forceinline__ bool is_int_dtype(int dt) {
+    return dt == ORMI_DTYPE_I32 || dt == ORMI_DTYPE_I64 || dt == ORMI_DTYPE_BOOL;
+}
+
+__device__ __forceinline__ long long load_as_i64(const void* p, int dt, size_t i) {
+    switch (dt) {
+        case ORMI_DTYPE_I32: return ((const int*)p)[i];
+        case ORMI_DTYPE_I64: return ((const long long*)p)[i];
+        default: return ((const unsigned char*)p)[i] ? 1 : 0;
+    }
+}
+
+// dst[i] = src[i] as dst's dtype. Between integer types (bool included) the
+// value converts exactly, an int64 outside the int32 range saturating and a
+// nonzero value giving true; from a float type it goes through float32 (the
+// ormi_f32_to_* rules: truncation, NaN to 0, saturation); to a float type it
+// rounds to nearest even.
 __global__ void convert_kernel(void* __restrict__ dst, int dst_dt, const void* __restrict__ src, int src_dt, size_t count) {
     const size_t stride = (size_t)gridDim.x * blockDim.x;
+    const bool int_to_int = is_int_dtype(src_dt) && is_int_dtype(dst_dt);
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
-        if (src_dt == ORMI_DTYPE_I64 && dst_dt == ORMI_DTYPE_I64) {
-            ((long long*)dst)[i] = ((const long long*)src)[i];
+        if (int_to_int) {
+            const long long v = load_as_i64(src, src_dt, i);
+            switch (dst_dt) {
+                case ORMI_DTYPE_I64: ((long long*)dst)[i] = v; break;
+                case ORMI_DTYPE_I32: ((int*)dst)[i] = v > 2147483647LL ? 2147483647 : v < -2147483648LL ? (int)0x80000000u : (int)v; break;
+                default: ((unsigned char*)dst)[i] = v != 0; break;
+            }
             continue;
         }
         const float v = load_as_f32(src, src_dt, i);
@@ -81,7 +104,7 @@ __global__ void convert_kernel(void* __restrict__ dst, int dst_dt, const void* _
             case ORMI_DTYPE_F32: ((float*)dst)[i] = v; break;
             case ORMI_DTYPE_BF16: ((unsigned short*)dst)[i] = ormi_f32_to_bf16(v); break;
             case ORMI_DTYPE_F16: ((unsigned short*)dst)[i] = ormi_f32_to_f16(v); break;
-            case ORMI_DTYPE_I32: ((int*)dst)[i] = (int)ormi_f32_to_i64(v); break;
+            case ORMI_DTYPE_I32: ((int*)dst)[i] = ormi_f32_to_i32(v); break;
             case ORMI_DTYPE_I64: ((long long*)dst)[i] = ormi_f32_to_i64(v); break;
             default: ((unsigned char*)dst)[i] = v != 0.0f; break;
         }
