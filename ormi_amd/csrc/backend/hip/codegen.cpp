@@ -25,6 +25,7 @@
 // partial results go to a workspace, and a second kernel combines them in part
 // order (two-pass; deterministic, no atomics).
 #include <algorithm>
+#include <atomic>
 #include <charconv>
 #include <memory>
 #include <cstdlib>
@@ -221,6 +222,9 @@ namespace ormi::hip {
                 vals.push_back((uint64_t)v);
             }
         };
+
+        // ptr_slots source of a store epilogue's leaf i (see resolve).
+        constexpr int kEpilogueLeaf = 1 << 20;
 
         // Appends without stream machinery (the signature is built per launch).
         void append_int(std::string& s, long long v) {
@@ -507,6 +511,88 @@ namespace ormi::hip {
             return op == ReduceOp::Sum ? "sum" : op == ReduceOp::Max ? "max" : "argmax";
         }
 
+        // ------------------------------------------------ store epilogue --
+        // Kernel arguments of a store epilogue: its output (epo) and its
+        // scalar operands (E<leaf>), read once per stored element.
+        void declare_epilogue(Gen& g, const StoreEpilogue* ep) {
+            if (!ep) return;
+            g.args.ptr(false, storage_type(ep->out_dtype), "epo", ep->out);
+            for (size_t L = 0; L < ep->expr.leaves.size(); ++L)
+                if ((int)L != ep->value)
+                    g.args.ptr(true, storage_type(ep->expr.leaves[L].dtype), "E", ep->expr.leaves[L].ptr, (int)L);
+        }
+
+        // Statements that evaluate the epilogue of the reduced value `v` and
+        // store it at element `at` of epo. The tape is lowered exactly as a
+        // map kernel lowers it, so the stored bits equal those of the
+        // element-wise kernel it replaces.
+        void emit_epilogue(std::ostringstream& b, const std::string& ind, const StoreEpilogue* ep, const std::string& v,
+                           const std::string& at) {
+            if (!ep) return;
+            const Expr& e = ep->expr;
+            std::vector<std::string> name(e.leaves.size() + e.insts.size());
+            b << ind << "{\n";
+            for (size_t L = 0; L < e.leaves.size(); ++L) {
+                name[L] = "ev" + std::to_string(L);
+                const std::string src = (int)L == ep->value ? v : to_f32(e.leaves[L].dtype, "E" + std::to_string(L) + "[0]");
+                b << ind << "  const float " << name[L] << " = " << src << ";\n";
+            }
+            for (size_t i = 0; i < e.insts.size(); ++i) {
+                const Inst& in = e.insts[i];
+                std::string expr;
+                if (in.op == OpEnum::CAST) {
+                    if (in.cast == DType::BFloat16) expr = "ormi_round_bf16(" + name[in.a] + ")";
+                    else if (in.cast == DType::Float16) expr = "ormi_round_f16(" + name[in.a] + ")";
+                    else expr = name[in.a];
+                } else {
+                    std::vector<std::string> operands{name[in.a]};
+                    if (in.b >= 0) operands.push_back(name[in.b]);
+                    if (!in.lower) throw std::runtime_error(std::string("HIP JIT Compiler Error: No lowering rule registered for ") +
+                                                            ops::op_name(in.op));
+                    expr = (*in.lower)(operands);
+                }
+                name[e.leaves.size() + i] = "et" + std::to_string(i);
+                b << ind << "  const float et" << i << " = " << expr << ";\n";
+            }
+            b << ind << "  epo[" << at << "] = " << from_f32(ep->out_dtype, name[e.root]) << ";\n" << ind << "}\n";
+        }
+
+        // Signature part of a store epilogue (its arguments are in the
+        // declarations already).
+        std::string epilogue_layout(const StoreEpilogue* ep) {
+            if (!ep) return std::string();
+            std::string s = "|ep";
+            append_int(s, ep->value);
+            s += ',';
+            s += char('a' + (int)ep->out_dtype);
+            for (const Leaf& L : ep->expr.leaves) s += char('a' + (int)L.dtype);
+            for (const Inst& in : ep->expr.insts) {
+                s += ';';
+                append_int(s, (int)in.op);
+                s += ',';
+                append_int(s, in.a);
+                s += ',';
+                append_int(s, in.b);
+                s += ',';
+                append_int(s, (int)in.cast);
+            }
+            s += ';';
+            append_int(s, ep->expr.root);
+            return s;
+        }
+
+        void check_epilogue(const StoreEpilogue* ep, ReduceOp op) {
+            if (!ep) return;
+            if (op == ReduceOp::Argmax) throw std::runtime_error("HIP reduce: no store epilogue on an argmax.");
+            const Expr& e = ep->expr;
+            if (ep->value < 0 || ep->value >= (int)e.leaves.size() || e.root < 0 ||
+                e.root >= (int)(e.leaves.size() + e.insts.size()) || !ep->out)
+                throw std::runtime_error("HIP reduce: malformed store epilogue.");
+            for (size_t L = 0; L < e.leaves.size(); ++L)
+                if ((int)L != ep->value && !e.leaves[L].scalar)
+                    throw std::runtime_error("HIP reduce: store epilogue operands must be scalars.");
+        }
+
         // Everything a generated source depends on, without sizes, strides or
         // pointers: kernel kind, parameter list, which strides are 0 / 1 /
         // general, group layout, vector width, index width, tuning and the tape.
@@ -629,6 +715,8 @@ namespace ormi::hip {
                 if (name == "L") k.ptr_slots.push_back({(int)i, d.i});
                 else if (name == "out") k.ptr_slots.push_back({(int)i, -1 - std::max(d.i, 0)});
                 else if (name == "outp" && g.args.vals[i] != 0) k.ptr_slots.push_back({(int)i, -1});
+                else if (name == "epo") k.ptr_slots.push_back({(int)i, -2});
+                else if (name == "E") k.ptr_slots.push_back({(int)i, kEpilogueLeaf + d.i});
             }
             std::string sig = signature(g, kind);
             sig += "|b";
@@ -871,7 +959,9 @@ namespace ormi::hip {
 
     // ------------------------------------------------------------- reduce --
     static ReducePlan plan_reduce_uncached(const Expr& expr, const std::vector<int>& in_shape, const std::vector<int>& axes_in,
-                                           ReduceOp op, void* out, int cu) {
+                                           ReduceOp op, void* out, int cu, const StoreEpilogue* ep) {
+        check_epilogue(ep, op);
+        const std::string ep_layout = epilogue_layout(ep);
         const Tuning& tn = tuning();
         const int n = (int)in_shape.size();
         std::vector<bool> red(n, axes_in.empty());
@@ -919,9 +1009,11 @@ namespace ormi::hip {
             P = RG == 0 ? 1 : (RG + CH - 1) / CH;  // drop empty parts
             g.choose_idx(O * P * 64 + RG * V + 64 * V * RU);
             plan.two_pass = P > 1;
+            const StoreEpilogue* ep1 = plan.two_pass ? nullptr : ep;  // the finishing kernel stores a split result
             g.args.ptr(false, "void", "outp", plan.two_pass ? nullptr : out);  // workspace bound later
             g.args.ptr(false, "int", "outi", nullptr);
             g.declare_leaves();
+            declare_epilogue(g, ep1);
             g.args.i64("NO", O);
             g.args.i64("NP", P);
             g.args.i64("RG", RG);
@@ -988,7 +1080,9 @@ namespace ormi::hip {
                 if (is_sum) {
                     b << "  float s = " << (V > 1 ? "(acc[0] + acc[1]) + (acc[2] + acc[3])" : "acc[0]") << ";\n";
                     b << "  s = ormi_wave_sum(s);\n";
-                    b << "  if (lane == 0) ((float*)outp)[wid] = s;\n";
+                    b << "  if (lane == 0) {\n    ((float*)outp)[wid] = s;\n";
+                    emit_epilogue(b, "    ", ep1, "s", "wid");
+                    b << "  }\n";
                 } else {
                     // A non-empty chain of only -inf still holds the empty marker: its first
                     // element is the first maximum. An empty chain keeps the marker, an
@@ -1001,9 +1095,10 @@ namespace ormi::hip {
                     b << "  if (lane == 0) {\n";
                     if (is_arg) b << "    if (NP == 1) ((long long*)outp)[wid] = (long long)bi; else { ((float*)outp)[wid] = bv; outi[wid] = bi; }\n";
                     else b << "    ((float*)outp)[wid] = bv; if (NP > 1) outi[wid] = bi;\n";
+                    emit_epilogue(b, "    ", ep1, "bv", "wid");
                     b << "  }\n";
                 }
-            });
+            }, ep1 ? ep_layout : std::string());
             if (plan.two_pass) {
                 plan.workspace_bytes = (size_t)(O * P) * (sizeof(float) + sizeof(int));
                 // Second pass: one wave per output row over its P partials, in part order.
@@ -1012,6 +1107,7 @@ namespace ormi::hip {
                 g2.args.ptr(false, "void", "outp", out);
                 g2.args.ptr(true, "float", "pvals", nullptr);
                 g2.args.ptr(true, "int", "pidx", nullptr);
+                declare_epilogue(g2, ep);
                 g2.args.i64("NO", O);
                 g2.args.i64("NP", P);
                 s2.grid[0] = (uint32_t)std::max(1LL, (O + 3) / 4);
@@ -1033,7 +1129,9 @@ namespace ormi::hip {
                               "    for (int u = 0; u < 8; ++u) v[u] = pv[q + 64 * u];\n#pragma unroll\n"
                               "    for (int u = 0; u < 8; ++u) s += v[u];\n  }\n";
                         sb << "  for (; q < NP; q += 64) s += pv[q];\n";
-                        sb << "  s = ormi_wave_sum(s);\n  if (lane == 0) ((float*)outp)[o] = s;\n";
+                        sb << "  s = ormi_wave_sum(s);\n  if (lane == 0) {\n    ((float*)outp)[o] = s;\n";
+                        emit_epilogue(sb, "    ", ep, "s", "o");
+                        sb << "  }\n";
                     } else {
                         sb << "  float bv = -__builtin_inff(); int bi = 0x7fffffff;\n";
                         sb << "  for (; q + 448 < NP; q += 512) {\n    float v[8]; int ix[8];\n#pragma unroll\n"
@@ -1042,9 +1140,13 @@ namespace ormi::hip {
                         sb << "  for (; q < NP; q += 64) ormi_am_take(bv, bi, pv[q], pi[q]);\n";
                         sb << "  ormi_wave_argmax(bv, bi);\n";
                         if (is_arg) sb << "  if (lane == 0) ((long long*)outp)[o] = (long long)bi;\n";
-                        else sb << "  if (lane == 0) ((float*)outp)[o] = bv;\n";
+                        else {
+                            sb << "  if (lane == 0) {\n    ((float*)outp)[o] = bv;\n";
+                            emit_epilogue(sb, "    ", ep, "bv", "o");
+                            sb << "  }\n";
+                        }
                     }
-                });
+                }, ep_layout);
             }
             return plan;
         }
@@ -1071,9 +1173,11 @@ namespace ormi::hip {
         P = R == 0 ? 1 : (R + CH - 1) / CH;
         g.choose_idx(O * I * P + R + 4LL * W * 4);
         plan.two_pass = P > 1;
+        const StoreEpilogue* ep1 = plan.two_pass ? nullptr : ep;
         g.args.ptr(false, "void", "outp", plan.two_pass ? nullptr : out);
         g.args.ptr(false, "int", "outi", nullptr);
         g.declare_leaves();
+        declare_epilogue(g, ep1);
         g.args.i64("NO", O);
         g.args.i64("NI", I);
         g.args.i64("NIG", IG);
@@ -1159,14 +1263,16 @@ namespace ormi::hip {
                 b << "      float s = sv[0][cl][k];\n";
                 b << "#pragma unroll\n      for (int q = 1; q < " << WR << "; ++q) s += sv[q][cl][k];\n";
                 b << "      ((float*)outp)[e0 + k] = s;\n";
+                emit_epilogue(b, "      ", ep1, "s", "e0 + k");
             } else {
                 b << "      float v = sv[0][cl][k]; int x = si[0][cl][k];\n";
                 b << "#pragma unroll\n      for (int q = 1; q < " << WR << "; ++q) ormi_am_take(v, x, sv[q][cl][k], si[q][cl][k]);\n";
                 if (is_arg) b << "      if (outi == nullptr) ((long long*)outp)[e0 + k] = (long long)x; else { ((float*)outp)[e0 + k] = v; outi[e0 + k] = x; }\n";
                 else b << "      ((float*)outp)[e0 + k] = v; if (outi != nullptr) outi[e0 + k] = x;\n";
+                if (!is_arg) emit_epilogue(b, "      ", ep1, "v", "e0 + k");
             }
             b << "    }\n  }\n";
-        }, "|cw" + std::to_string(WC));
+        }, "|cw" + std::to_string(WC) + (ep1 ? ep_layout : std::string()));
         if (plan.two_pass) {
             // Partials are laid out [P][O*I]; the second pass walks them in part order.
             plan.workspace_bytes = (size_t)(P * O * I) * (sizeof(float) + sizeof(int));
@@ -1175,6 +1281,7 @@ namespace ormi::hip {
             g2.args.ptr(false, "void", "outp", out);
             g2.args.ptr(true, "float", "pvals", nullptr);
             g2.args.ptr(true, "int", "pidx", nullptr);
+            declare_epilogue(g2, ep);
             g2.args.i64("NE", O * I);
             g2.args.i64("NP", P);
             s2.grid[0] = (uint32_t)std::max(1LL, (O * I + 255) / 256);
@@ -1194,6 +1301,7 @@ namespace ormi::hip {
                     sb << "#pragma unroll\n    for (int j = 0; j < " << FIN << "; ++j) v[j] = q0 + j < NP ? pvals[(q0 + j) * NE + e] : 0.0f;\n";
                     sb << "#pragma unroll\n    for (int j = 0; j < " << FIN << "; ++j) if (q0 + j < NP) s += v[j];\n  }\n";
                     sb << "  ((float*)outp)[e] = s;\n";
+                    emit_epilogue(sb, "  ", ep, "s", "e");
                 } else {
                     sb << "  float bv = -__builtin_inff(); int bi = 0x7fffffff;\n";
                     sb << "  for (long long q0 = 0; q0 < NP; q0 += " << FIN << ") {\n";
@@ -1201,9 +1309,12 @@ namespace ormi::hip {
                     sb << "#pragma unroll\n    for (int j = 0; j < " << FIN << "; ++j) if (q0 + j < NP) { v[j] = pvals[(q0 + j) * NE + e]; x[j] = pidx[(q0 + j) * NE + e]; }\n";
                     sb << "#pragma unroll\n    for (int j = 0; j < " << FIN << "; ++j) if (q0 + j < NP) ormi_am_take(bv, bi, v[j], x[j]);\n  }\n";
                     if (is_arg) sb << "  ((long long*)outp)[e] = (long long)bi;\n";
-                    else sb << "  ((float*)outp)[e] = bv;\n";
+                    else {
+                        sb << "  ((float*)outp)[e] = bv;\n";
+                        emit_epilogue(sb, "  ", ep, "bv", "e");
+                    }
                 }
-            });
+            }, ep_layout);
         }
         return plan;
     }
@@ -1259,27 +1370,28 @@ namespace ormi::hip {
                 k.source.shrink_to_fit();
             }
         }
-        void patch(KernelLaunch& k, const Expr& e, const void* const* outs) {
-            for (const auto& [slot, src] : k.ptr_slots)
-                k.args[slot] = (uint64_t)(uintptr_t)(src >= 0 ? e.leaves[src].ptr : outs[-1 - src]);
+        // The buffer address a ptr_slots source names: a leaf of the kernel's
+        // expression, an output, or a store epilogue's operand.
+        uint64_t slot_value(int src, const Expr& e, const void* const* outs, const Expr* ep) {
+            if (src >= kEpilogueLeaf) return (uint64_t)(uintptr_t)ep->leaves[src - kEpilogueLeaf].ptr;
+            return (uint64_t)(uintptr_t)(src >= 0 ? e.leaves[src].ptr : outs[-1 - src]);
         }
         // The cached launch c for this request's buffers: with launch_only and a
         // compiled kernel, only what launch() reads.
-        KernelLaunch instantiate(const KernelLaunch& c, const Expr& e, const void* const* outs, bool launch_only) {
-            if (!launch_only || !c.handle) {
-                KernelLaunch k = c;
-                patch(k, e, outs);
-                return k;
-            }
+        KernelLaunch instantiate(const KernelLaunch& c, const Expr& e, const void* const* outs, bool launch_only,
+                                 const Expr* ep = nullptr) {
             KernelLaunch k;
-            k.handle = c.handle;
-            for (int i = 0; i < 3; ++i) {
-                k.grid[i] = c.grid[i];
-                k.block[i] = c.block[i];
+            if (!launch_only || !c.handle) {
+                k = c;
+            } else {
+                k.handle = c.handle;
+                for (int i = 0; i < 3; ++i) {
+                    k.grid[i] = c.grid[i];
+                    k.block[i] = c.block[i];
+                }
+                k.args = c.args;
             }
-            k.args = c.args;
-            for (const auto& [slot, src] : c.ptr_slots)
-                k.args[slot] = (uint64_t)(uintptr_t)(src >= 0 ? e.leaves[src].ptr : outs[-1 - src]);
+            for (const auto& [slot, src] : c.ptr_slots) k.args[slot] = slot_value(src, e, outs, ep);
             return k;
         }
     }  // namespace
@@ -1317,7 +1429,7 @@ namespace ormi::hip {
     }
 
     ReducePlan plan_reduce(const Expr& expr, const std::vector<int>& in_shape, const std::vector<int>& axes, ReduceOp op,
-                           void* out, int cu, bool launch_only) {
+                           void* out, int cu, bool launch_only, const StoreEpilogue* ep) {
         KeyBuf kb;
         kb.i64('R');
         kb.i64(cu);
@@ -1327,7 +1439,13 @@ namespace ormi::hip {
         kb.i64((long long)axes.size());
         for (int a : axes) kb.i64(a);
         key_expr(kb, expr);
-        const void* outs[1] = {out};
+        if (ep) {
+            kb.i64('E');
+            kb.i64((long long)ep->value | ((long long)ep->out_dtype << 32) | ((long long)((uintptr_t)ep->out & 255) << 40));
+            key_expr(kb, ep->expr);
+        }
+        const void* outs[2] = {out, ep ? ep->out : nullptr};
+        const Expr* epx = ep ? &ep->expr : nullptr;
         RequestCache& rc = request_cache();
         {
             std::lock_guard<std::mutex> lock(rc.mu);
@@ -1338,12 +1456,12 @@ namespace ormi::hip {
                 ReducePlan plan;
                 plan.two_pass = it->second.two_pass;
                 plan.workspace_bytes = it->second.workspace_bytes;
-                plan.first = instantiate(it->second.first, expr, outs, launch_only);
-                if (plan.two_pass) plan.second = instantiate(it->second.second, expr, outs, launch_only);
+                plan.first = instantiate(it->second.first, expr, outs, launch_only, epx);
+                if (plan.two_pass) plan.second = instantiate(it->second.second, expr, outs, launch_only, epx);
                 return plan;
             }
         }
-        ReducePlan plan = plan_reduce_uncached(expr, in_shape, axes, op, out, cu);
+        ReducePlan plan = plan_reduce_uncached(expr, in_shape, axes, op, out, cu, ep);
         std::lock_guard<std::mutex> lock(rc.mu);
         if (rc.reduces.size() >= kMaxRequests) rc.reduces.clear();
         rc.reduces.emplace(std::move(kb.s), plan);
@@ -1362,7 +1480,11 @@ namespace ormi::hip {
         plan.second.args[2] = idx;
     }
 
+    static std::atomic<unsigned long long> g_launches{0};
+    unsigned long long kernel_launches() { return g_launches.load(); }
+
     void launch(const KernelLaunch& k) {
+        g_launches.fetch_add(1, std::memory_order_relaxed);
         uint64_t handle = k.handle;
         if (!handle) {
             if (k.source.empty()) throw std::runtime_error("HIP codegen: kernel " + k.name + " has no source");

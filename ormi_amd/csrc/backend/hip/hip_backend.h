@@ -48,6 +48,10 @@ namespace ormi::hip {
     // One tape for several element-wise roots of the same shape: shared leaves
     // and interior nodes are evaluated once, each root is one output.
     Expr build_expr_multi(const std::vector<NodePtr>& roots, const std::vector<int>& shape, bool plan_only = false);
+    // The unrealized SUM or MAX whose store epilogue the element-wise region of
+    // n can be (n's region reads only it and realized scalars, and it has n's
+    // shape), else nullptr. The scheduler then realizes both with one kernel.
+    NodePtr epilogue_reduction(const NodePtr& n);
 
     // ------------------------------------------------------- scheduler --
     // Realize root on the HIP device: pointwise regions become one fused

@@ -132,8 +132,22 @@ namespace ormi::hip {
         KernelLaunch second;
         size_t workspace_bytes = 0;
     };
+    // An element-wise consumer of a Sum or Max result, applied as the result
+    // is stored (the mean's 1/N, a scaled or shifted sum), so it needs no
+    // kernel of its own: expr's leaf `value` stands for the reduced value and
+    // every other leaf is a scalar (1-element) operand. The kernel that writes
+    // the result (the finishing kernel of a split reduction) also writes
+    // expr.root, converted to out_dtype, to out, at the same position.
+    struct StoreEpilogue {
+        Expr expr;
+        int value = -1;
+        void* out = nullptr;
+        DType out_dtype = DType::Float32;
+    };
     ReducePlan plan_reduce(const Expr& expr, const std::vector<int>& in_shape, const std::vector<int>& axes, ReduceOp op,
-                           void* out, int compute_units, bool launch_only = false);
+                           void* out, int compute_units, bool launch_only = false, const StoreEpilogue* epilogue = nullptr);
+    // Generated kernels launched by this process so far (tests count fusions).
+    unsigned long long kernel_launches();
     void bind_workspace(ReducePlan& plan, void* workspace);
 
     // Source text of a planned kernel: a plan that hit the kernel cache after

@@ -56,7 +56,54 @@ namespace ormi::hip {
         }
     }
 
-    static void reduce_handler(const NodePtr& root, ReduceOp op) {
+    static void run_map(const NodePtr& root);
+
+    // Element-wise regions of at most this many ops run as a reduction's store
+    // epilogue (the mean is one multiply).
+    constexpr size_t kMaxStoreEpilogue = 16;
+
+    // The reduction whose store epilogue region `n` can be: n is an unrealized
+    // fp32 element-wise root whose region reads exactly one unrealized node,
+    // a SUM or MAX with n's own shape, besides realized scalars (1-element
+    // buffers, such as the mean's 1/N). The region then costs no kernel and no
+    // pass over the reduction's result. nullptr when the region is not of that
+    // form.
+    NodePtr epilogue_reduction(const NodePtr& n) {
+        if (n->is_realized() || n->dtype != DType::Float32 || !fusible_root(*n)) return nullptr;
+        NodePtr red;
+        SmallSet<Node> seen;
+        seen.insert(n.get());
+        SmallVec<Node*, 16> stack;
+        stack.push_back(n.get());
+        size_t interior = 1;
+        while (!stack.empty()) {
+            Node* m = stack.back();
+            stack.pop_back();
+            for (const auto& p : m->parents) {
+                if (!seen.insert(p.get())) continue;
+                if (p->is_realized()) {
+                    if (p->data->numel() != 1) return nullptr;
+                    continue;
+                }
+                if (fusible_interior(*p)) {
+                    if (++interior > kMaxStoreEpilogue) return nullptr;
+                    stack.push_back(p.get());
+                    continue;
+                }
+                if (red || (p->op != OpEnum::SUM && p->op != OpEnum::MAX) || p->dtype != DType::Float32 ||
+                    p->view.shape != n->view.shape)
+                    return nullptr;
+                red = p;
+            }
+        }
+        return red;
+    }
+
+    // The reduction `root`. With `epi`, an element-wise consumer of root's
+    // result (epilogue_reduction(epi) == root) is realized by the same kernel:
+    // it runs as the reduction's store epilogue and root's own result is
+    // stored as well, so both nodes hold buffers afterwards.
+    static void reduce_handler(const NodePtr& root, ReduceOp op, const NodePtr& epi = nullptr) {
         const NodePtr& x = root->parents[0];
         prepare_input(x);
         const auto& attrs = std::get<ReduceAttrs>(root->attrs);
@@ -66,15 +113,32 @@ namespace ormi::hip {
         auto out = empty(root->view.shape, DeviceEnum::HIP, out_dtype);
         root->data = out;
         root->view.strides = calc_contiguous_strides(root->view.shape);
-        if (out->numel() == 0) return;
-        if (in_numel == 0) {
-            if (op != ReduceOp::Sum) throw std::runtime_error("zero-size array to reduction operation maximum which has no identity");
-            const float zero = 0.0f;
-            ORMI_HIP_CHECK(ormi_hip_fill(out->ptr, &zero, 4, out->numel()));
+        if (out->numel() == 0 || in_numel == 0) {
+            if (out->numel() > 0) {
+                if (op != ReduceOp::Sum) throw std::runtime_error("zero-size array to reduction operation maximum which has no identity");
+                const float zero = 0.0f;
+                ORMI_HIP_CHECK(ormi_hip_fill(out->ptr, &zero, 4, out->numel()));
+            }
+            if (epi) run_map(epi);  // root holds its buffer now: a plain element-wise kernel
             return;
         }
         const Expr e = build_expr(x, in_shape);
-        ReducePlan plan = plan_reduce(e, in_shape, attrs.axes, op, out->ptr, device_compute_units(), true);
+        StoreEpilogue ep;
+        std::shared_ptr<Buffer> epi_out;
+        if (epi) {
+            // root is realized now, so the consumer's tape reads it as a leaf.
+            ep.expr = build_expr(epi, epi->view.shape);
+            for (size_t L = 0; L < ep.expr.leaves.size(); ++L)
+                if (ep.expr.leaves[L].ptr == out->ptr) ep.value = (int)L;
+            epi_out = empty(epi->view.shape, DeviceEnum::HIP, epi->dtype);
+            ep.out = epi_out->ptr;
+            ep.out_dtype = epi->dtype;
+        }
+        ReducePlan plan = plan_reduce(e, in_shape, attrs.axes, op, out->ptr, device_compute_units(), true, epi ? &ep : nullptr);
+        if (epi) {
+            epi->data = epi_out;
+            epi->view.strides = calc_contiguous_strides(epi->view.shape);
+        }
         std::shared_ptr<Buffer> ws;
         if (plan.two_pass) {
             ws = empty({(int)((plan.workspace_bytes + 3) / 4)}, DeviceEnum::HIP, DType::Float32);
@@ -419,11 +483,16 @@ namespace ormi::hip {
         return it == sc.act.end() || it->second->is_realized() ? nullptr : it->second;
     }
 
-    // An element-wise region: a matched GEMM epilogue, else one fused kernel.
+    // An element-wise region: a matched GEMM epilogue, a reduction's store
+    // epilogue, else one fused kernel.
     static void run_map(const NodePtr& root) {
         {
             EpilogueMatch m;
             if (match_epilogue(root, m) && run_gemm_epilogue(root, m)) return;
+        }
+        if (const NodePtr r = epilogue_reduction(root)) {
+            reduce_handler(r, r->op == OpEnum::SUM ? ReduceOp::Sum : ReduceOp::Max, root);
+            return;
         }
         for (const auto& f : region_frontier(root)) realize(f);
         const Expr e = build_expr(root, root->view.shape);
@@ -447,6 +516,7 @@ namespace ormi::hip {
                 if (m.s) deps.push_back(m.s);
                 return deps;
             }
+            if (const NodePtr r = epilogue_reduction(n)) return dependencies(r);
             return region_frontier(n);
         }
         if (ops::is_reduction(n->op)) {
@@ -521,7 +591,7 @@ namespace ormi::hip {
             if (!r || r->is_realized() || !seen.insert(r.get()).second) continue;
             if (r->device.type != DeviceEnum::HIP) throw std::runtime_error("HIP scheduler: node belongs to another device.");
             EpilogueMatch m;
-            if (!fusible_interior(*r) || match_epilogue(r, m)) {
+            if (!fusible_interior(*r) || match_epilogue(r, m) || epilogue_reduction(r)) {
                 rest.push_back(r);
                 continue;
             }

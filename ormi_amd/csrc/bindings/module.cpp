@@ -150,7 +150,36 @@ namespace {
         hip::KernelLaunch k;
         hip::ReducePlan rp;
         const int cu = 256;
-        if (ops::is_reduction(root->op)) {
+        const std::shared_ptr<Node> red = ops::is_reduction(root->op) ? nullptr : hip::epilogue_reduction(root);
+        if (red) {
+            // An element-wise root that runs as a reduction's store epilogue:
+            // the reduction's plan with the root's tape at its store. The
+            // epilogue reads the reduction as a leaf, so it gets a host
+            // stand-in buffer while the tape is built.
+            const auto& x = red->parents[0];
+            const hip::Expr e = hip::build_expr(x, x->view.shape, true);
+            const auto& a = std::get<ReduceAttrs>(red->attrs);
+            hip::StoreEpilogue ep;
+            red->data = empty(red->view.shape, DeviceEnum::CPU, DType::Float32);
+            try {
+                ep.expr = hip::build_expr(root, root->view.shape, true);
+            } catch (...) {
+                red->data = nullptr;
+                throw;
+            }
+            for (size_t L = 0; L < ep.expr.leaves.size(); ++L)
+                if (ep.expr.leaves[L].ptr == red->data->ptr) ep.value = (int)L;
+            red->data = nullptr;
+            ep.out = (void*)(uintptr_t)0x200000;
+            const hip::ReduceOp op = red->op == ops::OpEnum::SUM ? hip::ReduceOp::Sum : hip::ReduceOp::Max;
+            rp = hip::plan_reduce(e, x->view.shape, a.axes, op, (void*)(uintptr_t)0x100000, cu, false, &ep);
+            k = rp.first;
+            d["two_pass"] = rp.two_pass;
+            d["second_source"] = hip::kernel_source(rp.second);
+            d["second_name"] = rp.second.name;
+            d["workspace_bytes"] = rp.workspace_bytes;
+            d["store_epilogue"] = true;
+        } else if (ops::is_reduction(root->op)) {
             const auto& x = root->parents[0];
             const hip::Expr e = hip::build_expr(x, x->view.shape, true);
             const auto& a = std::get<ReduceAttrs>(root->attrs);
@@ -358,4 +387,8 @@ PYBIND11_MODULE(ormi_backend, m) {
         return py::make_tuple(f.m, f.s);
     });
     m.def("_rtc_options", [] { return hip::rtc_options(); });
+    m.def("_is_store_epilogue", [](const std::shared_ptr<Node>& n) { return hip::epilogue_reduction(n) != nullptr; },
+          "Whether the element-wise region of n would run as a reduction's store epilogue.");
+    m.def("_kernel_launches", [] { return hip::kernel_launches(); },
+          "Generated (hipRTC) kernels launched by this process so far.");
 }
