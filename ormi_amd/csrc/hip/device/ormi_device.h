@@ -67,7 +67,8 @@ __device__ __forceinline__ float ormi_tanh_grad(float y) { return 1.0f - y * y; 
 // tanh in about 15 VALU instructions (the device library's tanhf takes about 27
 // and branches), branch-free, within 3 ulp of the exact value:
 //   |y| <  0.625: y + y^3 P(y^2), P of degree 4 fitted here by Remez exchange on
-//                 the relative error of tanh over [0, 0.625] (fit error 4.4e-9);
+//                 the relative error of tanh over [0, 0.625] (fit error 4.4e-9;
+//                 tests/test_tanh_fit.py re-derives the fit on the host);
 //   |y| >= 0.625: 1 - 2 / (1 + 2^(2|y| log2 e)) with the hardware V_EXP_F32
 //                 (2^x) and V_RCP_F32; at |y| >= 0.625 the subtraction loses at
 //                 most one bit.
