@@ -1638,7 +1638,17 @@ static int gemm_run_locked(const ormi_gemm_desc* d, const Epi& epi, long long ba
     // in whole 16-byte chunks, per-lane tile offsets in 32 bits.
     const long long a_span32 = a_kc ? 256LL * d->a_stride_m * 4 : 64LL * d->a_stride_k * 4 + 1024;
     const long long b_span32 = b_kc ? 256LL * d->b_stride_n * 4 : 64LL * d->b_stride_k * 4 + 1024;
-    const int dma32_id = env_cfg("ORMI_GEMM_F32_DMA_CFG", 1);
+    // Default fp32 configuration: 128x128 tiles (1), or 128x64 tiles (9; 6
+    // when K is not in whole 64-deep tiles) when 128x128 tiles would leave
+    // compute units idle. Twice the tiles then need half the K split or none:
+    // one box, interleaved, warm clocks: 2048x1024x4096 NT (C4's dA) 128.6 ->
+    // 124.9 us, 1024^2 x 4096 NN 69.3 -> 67.9, 1024x2048x2048 TN 69.6 ->
+    // 63.3, 2048x1024x1024 NT 40.3 -> 34.9, 512^2 x 4096 30.9 -> 26.9.
+    int dma32_id = env_cfg("ORMI_GEMM_F32_DMA_CFG", -1);
+    if (dma32_id < 0 || dma32_id > 9) {
+        const long long t128 = (long long)((d->M + 127) / 128) * ((d->N + 127) / 128) * batch;
+        dma32_id = t128 >= compute_units() ? 1 : d->K % 64 == 0 ? 9 : 6;
+    }
     int dma32_bm = 0, dma32_bn = 0, dma32_bk = 0;
     cfg32_dma(dma32_id, &dma32_bm, &dma32_bn, &dma32_bk);
     const bool dma32 = f32 && env_cfg("ORMI_GEMM_F32_DMA", 1) != 0 && d->K % dma32_bk == 0 && (a_kc || d->M % 4 == 0) &&

@@ -525,25 +525,33 @@ struct F32DmaLauncher {
 //   3: 128x128, 2x2 waves, BK 32, 2 stages (64 KB: two work-groups per CU)
 //   4: 128x128, 2x2 waves, BK 64, 2 stages (128 KB)
 //   5: 128x128, 2x4 waves, BK 64, 2 stages (128 KB)
+//   6: 128x64,  2x2 waves (64x32 per wave), BK 32, 4 stages (96 KB)
+//   7: 64x128,  2x2 waves (32x64 per wave), BK 32, 4 stages (96 KB)
+//   8: 128x64,  2x2 waves, BK 32, 5 stages (120 KB)
+//   9: 128x64,  2x2 waves, BK 64, 3 stages (144 KB)
 // Configuration 1 is the default (ORMI_GEMM_F32_DMA_CFG selects another;
 // out-of-range ids select it too).
 void cfg32_dma(int id, int* bm, int* bn, int* bk) {
-    if (id < 0 || id > 5) id = 1;
-    *bm = 128;
-    *bn = id == 2 ? 256 : 128;
-    *bk = id == 4 || id == 5 ? 64 : 32;
+    if (id < 0 || id > 9) id = 1;
+    *bm = id == 7 ? 64 : 128;
+    *bn = id == 2 ? 256 : id == 6 || id == 8 || id == 9 ? 64 : 128;
+    *bk = id == 4 || id == 5 || id == 9 ? 64 : 32;
 }
 void run32_dma_persist(const GemmParams& p, int groups, bool a_kc, bool b_kc) {
     F32DmaLauncher<128, 128, 32, 2, 4, 4>::run_persist(p, groups, a_kc, b_kc);
 }
 void run32_dma(int id, const GemmParams& p, dim3 grid, bool a_kc, bool b_kc, bool epi) {
-    if (id < 0 || id > 5) id = 1;
+    if (id < 0 || id > 9) id = 1;
     switch (id) {
         case 0: F32DmaLauncher<128, 128, 32, 2, 2, 4>::run(p, grid, a_kc, b_kc, epi); break;
         case 2: F32DmaLauncher<128, 256, 32, 2, 2, 3>::run(p, grid, a_kc, b_kc, epi); break;
         case 3: F32DmaLauncher<128, 128, 32, 2, 2, 2>::run(p, grid, a_kc, b_kc, epi); break;
         case 4: F32DmaLauncher<128, 128, 64, 2, 2, 2>::run(p, grid, a_kc, b_kc, epi); break;
         case 5: F32DmaLauncher<128, 128, 64, 2, 4, 2>::run(p, grid, a_kc, b_kc, epi); break;
+        case 6: F32DmaLauncher<128, 64, 32, 2, 2, 4>::run(p, grid, a_kc, b_kc, epi); break;
+        case 7: F32DmaLauncher<64, 128, 32, 2, 2, 4>::run(p, grid, a_kc, b_kc, epi); break;
+        case 8: F32DmaLauncher<128, 64, 32, 2, 2, 5>::run(p, grid, a_kc, b_kc, epi); break;
+        case 9: F32DmaLauncher<128, 64, 64, 2, 2, 3>::run(p, grid, a_kc, b_kc, epi); break;
         default: F32DmaLauncher<128, 128, 32, 2, 4, 4>::run(p, grid, a_kc, b_kc, epi); break;
     }
 }

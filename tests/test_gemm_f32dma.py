@@ -99,7 +99,7 @@ def run(lib, A, B, layout, batch_b_broadcast=False):
 SHAPES = [(256, 256, 128), (300, 520, 128), (96, 200, 192), (256, 512, 96), (4, 8, 64)]
 
 
-@pytest.mark.parametrize("cfg", [0, 1, 2, 3, 4, 5, None])
+@pytest.mark.parametrize("cfg", [0, 1, 2, 3, 4, 5, 6, 7, 8, 9, None])
 @pytest.mark.parametrize("layout", ["NN", "NT", "TN", "TT"])
 def test_direct_load_layouts_and_ragged_tiles(lib, cfg, layout):
     use(cfg)
@@ -111,7 +111,7 @@ def test_direct_load_layouts_and_ragged_tiles(lib, cfg, layout):
         assert np.all(err <= bound(A, B)), (cfg, layout, M, N, K, float(np.max(err / bound(A, B))))
 
 
-@pytest.mark.parametrize("cfg", [1, 2, 4, None])
+@pytest.mark.parametrize("cfg", [1, 2, 4, 6, 7, 8, 9, None])
 def test_direct_load_k_split_and_batches(lib, cfg):
     """One 128x128 tile over K = 4096 is split over the CUs (a finish pass sums
     the partials in split order); three batches against one broadcast B."""
@@ -131,7 +131,7 @@ def test_direct_load_k_split_and_batches(lib, cfg):
         assert np.all(np.abs(got - want) <= bound(A3, B3)), (cfg, layout)
 
 
-@pytest.mark.parametrize("cfg", [0, 1, 2, 3, 4, 5])
+@pytest.mark.parametrize("cfg", [0, 1, 2, 3, 4, 5, 6, 7, 8, 9])
 def test_direct_load_epilogue_in_kernel(lib, cfg):
     """C = D - s * (A @ B) (the SGD form) and C = relu(A @ B) with the product
     in aux, on a shape in whole tiles with no K split, so the epilogue runs in
