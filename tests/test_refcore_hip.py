@@ -21,8 +21,10 @@ The checks:
     CPU device; each of exp/log/sin/cos/pow within rtol 1e-6; seeded programs
     with sums and gradients (tests/test_ref_oracle.py's generator) within the
     summation-order tolerance; GEMMs forward and backward, the C4 fp32 config
-    included, within 2K eps32 |A||B| of a float64 product; and a config-size
-    row and column sum within the float64 sum's order bound.
+    included, within 2K eps32 |A||B| of a float64 product; a config-size
+    row and column sum within the float64 sum's order bound; C1's shape and
+    data in the reference's op set with its gradients; and a two-layer
+    training step at C5's batch and widths (GEMMs, autograd, SGD update).
 """
 import ctypes
 import json
@@ -353,3 +355,74 @@ def test_row_and_column_sums_at_config_width(refhip):
     assert rows.shape == (4096,) and cols.shape == (1, 8192)
     assert np.all(np.abs(rows - x64.sum(1)) <= 8192 * EPS32 * ax.sum(1))
     assert np.all(np.abs(cols[0] - x64.sum(0)) <= 4096 * EPS32 * ax.sum(0))
+
+
+@pytest.mark.gpu
+def test_c1_shaped_program_through_the_reference_core(refhip, refcpu):
+    """C1's shape and data (1024x1024, seed 0, U(-1,1)) in the reference's op set
+    (it has no relu): y = sum((a*b + c) * 0.5, axis 1), loss = sum(y), and the
+    gradients of loss w.r.t. a, b, c. The reference realizes each op as its own
+    kernel here. The gradients are element-wise products of the seed (0.5 * b,
+    0.5 * a, 0.5), bit-exact against the reference's CPU device; the row sums
+    within n eps sum|v| of float64."""
+    rng = np.random.default_rng(0)
+    a, b, c = (rng.uniform(-1, 1, (1024, 1024)).astype(np.float32) for _ in range(3))
+    half = np.float32(0.5).reshape(())
+    leaves = [(a, True), (b, True), (c, True), (half, False)]
+    ops = [("MUL", 0, 1, [], 0), ("ADD", 4, 2, [], 0), ("MUL", 5, 3, [], 0), ("SUM", 6, -1, [1], 0),
+           ("SUM", 7, -1, [0], 0)]
+    outputs = [7, 8, -1, -2, -3]
+    want = run(refcpu, "cpu", leaves, ops, outputs, 8)
+    got = run(refhip, "hip", leaves, ops, outputs, 8)
+    for k in (2, 3, 4):
+        assert same(got[k], want[k]), k
+    v = ((a * b + c) * np.float32(0.5)).astype(np.float64)
+    bound = 1024 * EPS32 * np.abs(v).sum(1)
+    assert np.all(np.abs(got[0] - v.sum(1)) <= bound)
+    assert abs(float(got[1].reshape(-1)[0]) - v.sum()) <= 1024 * 1024 * EPS32 * np.abs(v).sum()
+
+
+@pytest.mark.gpu
+def test_two_layer_training_step_through_the_reference_core(refhip):
+    """C5's batch and widths without the activations the reference lacks:
+    Y = (X W1) W2 with X (1024,1024), W1 (1024,4096), W2 (4096,1024), loss =
+    sum((Y - T)^2) * 2^-20, the reference's autograd for dW1 and dW2 (two NT and
+    two TN GEMMs over transposed views), then the SGD update W - lr dW, all on
+    DeviceEnum::HIP. Checked against float64 normwise: the forward within
+    2 K eps32 |A||B| per product, the updates and gradients within 1e-4."""
+    rng = np.random.default_rng(4)
+    X = rng.normal(0, 1, (1024, 1024)).astype(np.float32)
+    T_ = rng.normal(0, 1, (1024, 1024)).astype(np.float32)
+    W1 = rng.uniform(-np.sqrt(6 / 1024), np.sqrt(6 / 1024), (1024, 4096)).astype(np.float32)
+    W2 = rng.uniform(-np.sqrt(6 / 4096), np.sqrt(6 / 4096), (4096, 1024)).astype(np.float32)
+    scale = np.float32(2.0 ** -20).reshape(())
+    lr = np.float32(1e-3).reshape(())
+    leaves = [(X, False), (W1, True), (W2, True), (T_, False), (scale, False), (lr, False)]
+    ops = [("MATMUL", 0, 1, [], 0),    # 6  H = X W1
+           ("MATMUL", 6, 2, [], 0),    # 7  Y = H W2
+           ("SUB", 7, 3, [], 0),       # 8  D = Y - T
+           ("MUL", 8, 8, [], 0),       # 9  D*D
+           ("SUM", 9, -1, [0, 1], 0),  # 10
+           ("MUL", 10, 4, [], 0)]      # 11 loss
+    outputs = [6, 7, 11, -2, -3]
+    H, Y, loss, dW1, dW2 = run(refhip, "hip", leaves, ops, outputs, 11, capacity=4096 * 1024)
+    x64, w1, w2, t64 = (v.astype(np.float64) for v in (X, W1, W2, T_))
+    h64 = x64 @ w1
+    assert np.all(np.abs(H - h64) <= 2 * 1024 * EPS32 * (np.abs(x64) @ np.abs(w1)))
+    y64 = H.astype(np.float64) @ w2
+    assert np.all(np.abs(Y - y64) <= 2 * 4096 * EPS32 * (np.abs(H.astype(np.float64)) @ np.abs(w2)))
+    d64 = (x64 @ w1) @ w2 - t64
+    np.testing.assert_allclose(float(loss.reshape(-1)[0]), (d64 * d64).sum() * 2.0 ** -20, rtol=1e-5)
+    g = 2 * d64 * 2.0 ** -20
+    dw2 = h64.T @ g
+    dw1 = x64.T @ (g @ w2.T)
+
+    def normwise(got, want):
+        return np.linalg.norm(got - want) / np.linalg.norm(want)
+
+    assert normwise(dW2, dw2) < 1e-4 and normwise(dW1, dw1) < 1e-4
+    # the SGD update W - lr * dW as reference ops over the realized gradients
+    upd_leaves = [(W1, False), (dW1, False), (W2, False), (dW2, False), (lr, False)]
+    upd_ops = [("MUL", 1, 4, [], 0), ("SUB", 0, 5, [], 0), ("MUL", 3, 4, [], 0), ("SUB", 2, 7, [], 0)]
+    nW1, nW2 = run(refhip, "hip", upd_leaves, upd_ops, [6, 8], capacity=4096 * 1024)
+    assert same(nW1, W1 - dW1 * np.float32(1e-3)) and same(nW2, W2 - dW2 * np.float32(1e-3))
