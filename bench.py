@@ -828,13 +828,12 @@ def _pmc_plan():
         "copy": [("copy y = -x", (2 ** 27, 2 ** 27))],
         "c2": [("C2 fused map", (c2_bytes() - 2 ** 27, 2 ** 27))],
         "c3": [("C3 row max", (inb, rows * 4)), ("C3 row sum(exp(x - max))", (inb + rows * 4, rows * 4)),
-               ("C3 row mean (sum)", (inb, rows * 4)), ("C3 row mean (scale by 2^-13)", (rows * 4, rows * 4)),
+               ("C3 row mean (sum, its 2^-13 scale at the store)", (inb, rows * 4)),
                ("C3 row argmax", (inb, rows * 8)),
                ("C3 column sum, main", (inb, None)), ("C3 column sum, finish", (None, cols * 4))],
         "c4": [("C4 bf16 4096^3", (2 * 4096 * 4096 * 2, 4096 * 4096 * 4)),
                ("C4 fp32 NN 2048x1024x4096", ((2048 * 1024 + 1024 * 4096) * 4, 2048 * 4096 * 4)),
-               ("C4 fp32 NT dA (K split)", ((2048 * 4096 + 4096 * 1024) * 4, None)),
-               ("C4 fp32 NT dA, finish", (None, 2048 * 1024 * 4)),
+               ("C4 fp32 NT dA (128x64 tiles)", ((2048 * 4096 + 4096 * 1024) * 4, 2048 * 1024 * 4)),
                ("C4 fp32 TN dB", ((1024 * 2048 + 2048 * 4096) * 4, 1024 * 4096 * 4))],
     }
 
