@@ -602,6 +602,140 @@ def vendor_gemm(out_md: Path, cmd: str, rounds: int = 3, n: int = 20) -> None:
     print(out_md.read_text())
 
 
+# Register-only MFMA loops: the matrix cores' sustained rate with no memory
+# work. Each wave keeps 4 independent accumulators and cycles through 8
+# operand fragments loaded once from `vals` (vary = 0: all 8 hold the same
+# values; 1: 8 different sets, so the operands change every instruction).
+# Each lane stores one sum of its accumulators, so nothing is dead code.
+MFMA_PROBE_SRC = r"""
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+extern "C" __global__ __launch_bounds__(256) void ormi_mfma_probe_bf16(float* out, const unsigned* vals, long long iters,
+                                                                       long long vary) {
+    const int lane = threadIdx.x & 63;
+    u32x4 a[8], b[8];
+    for (int s = 0; s < 8; ++s) {
+        const int k = (vary ? s : 0) * 512 + lane * 4;
+        a[s] = u32x4{vals[k], vals[k + 1], vals[k + 2], vals[k + 3]};
+        b[s] = u32x4{vals[k + 256], vals[k + 257], vals[k + 258], vals[k + 259]};
+    }
+    f32x16 acc[4];
+    for (int q = 0; q < 4; ++q) acc[q] = f32x16{};
+    for (long long it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+            acc[s & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a[s]),
+                                                                 __builtin_bit_cast(bf16x8, b[s]), acc[s & 3], 0, 0, 0);
+    }
+    float t = 0.0f;
+    for (int q = 0; q < 4; ++q)
+        for (int r = 0; r < 16; ++r) t += acc[q][r];
+    out[blockIdx.x * blockDim.x + threadIdx.x] = t;
+}
+extern "C" __global__ __launch_bounds__(256) void ormi_mfma_probe_f32(float* out, const unsigned* vals, long long iters,
+                                                                      long long vary) {
+    const int lane = threadIdx.x & 63;
+    float a[8], b[8];
+    for (int s = 0; s < 8; ++s) {
+        const int k = (vary ? s : 0) * 512 + lane;
+        a[s] = __uint_as_float(vals[k]);
+        b[s] = __uint_as_float(vals[k + 256]);
+    }
+    f32x16 acc[4];
+    for (int q = 0; q < 4; ++q) acc[q] = f32x16{};
+    for (long long it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int s = 0; s < 8; ++s) acc[s & 3] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], b[s], acc[s & 3], 0, 0, 0);
+    }
+    float t = 0.0f;
+    for (int q = 0; q < 4; ++q)
+        for (int r = 0; r < 16; ++r) t += acc[q][r];
+    out[blockIdx.x * blockDim.x + threadIdx.x] = t;
+}
+"""
+
+
+def mfma_probe_values(seed: int = 7) -> np.ndarray:
+    """8 x 512 operand words, each two bf16 of N(0, 1/64) values (the statistics
+    of the C4 inputs); read as fp32, a word is about its upper value."""
+    rng = np.random.default_rng(seed)
+    x = rng.normal(0, 1 / 64, 2 * 8 * 512).astype(np.float32)
+    bf = (x.view(np.uint32) >> 16).astype(np.uint32)
+    return (bf[0::2] | (bf[1::2] << 16)).astype(np.uint32)
+
+
+class _Props(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 64), ("compute_units", ctypes.c_int), ("clock_khz", ctypes.c_int),
+                ("lds_bytes_per_block", ctypes.c_int), ("total_mem_bytes", ctypes.c_size_t)]
+
+
+def mfma_ceiling(out_md: Path, cmd: str) -> None:
+    """Sustained matrix-core rate of v_mfma_f32_32x32x16_bf16 and
+    v_mfma_f32_32x32x2_f32 in register-only loops (one and two 4-wave blocks
+    per compute unit; constant and changing operands), compiled and launched
+    through libormi_hip's hipRTC entry points; best of 3 launches after a warm-up.
+    Writes a markdown table to out_md."""
+    ev = Events()
+    lib = ev.lib
+    lib.ormi_hip_last_error.restype = ctypes.c_char_p
+    lib.ormi_hip_rtc_compile.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p), ctypes.c_int,
+                                         ctypes.POINTER(ctypes.c_uint64)]
+    lib.ormi_hip_launch.argtypes = [ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint32),
+                                    ctypes.c_uint32, ctypes.POINTER(ctypes.c_void_p)]
+    lib.ormi_hip_malloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
+    lib.ormi_hip_memcpy_h2d.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]
+    assert lib.ormi_hip_init(0) == 0
+    props = _Props()
+    assert lib.ormi_hip_get_props(ctypes.byref(props)) == 0
+    cus = props.compute_units
+    vals = mfma_probe_values()
+    dv, dout = ctypes.c_void_p(), ctypes.c_void_p()
+    assert lib.ormi_hip_malloc(ctypes.byref(dv), vals.nbytes) == 0
+    assert lib.ormi_hip_memcpy_h2d(dv, vals.ctypes.data, vals.nbytes) == 0
+    assert lib.ormi_hip_malloc(ctypes.byref(dout), 2 * cus * 256 * 4) == 0
+    rows = []
+    for name, inst, flops_per, iters in (("ormi_mfma_probe_bf16", "`v_mfma_f32_32x32x16_bf16`", 32 * 32 * 16 * 2, 60000),
+                                         ("ormi_mfma_probe_f32", "`v_mfma_f32_32x32x2_f32`", 32 * 32 * 2 * 2, 45000)):
+        h = ctypes.c_uint64()
+        if lib.ormi_hip_rtc_compile(MFMA_PROBE_SRC.encode(), name.encode(), None, 0, ctypes.byref(h)) != 0:
+            raise SystemExit("mfma probe: " + lib.ormi_hip_last_error().decode())
+        for bpc in (1, 2):
+            for vary in (0, 1):
+                grid = (ctypes.c_uint32 * 3)(cus * bpc, 1, 1)
+                block = (ctypes.c_uint32 * 3)(256, 1, 1)
+                a_out, a_vals = ctypes.c_void_p(dout.value), ctypes.c_void_p(dv.value)
+                a_it, a_vary = ctypes.c_longlong(iters * bpc), ctypes.c_longlong(vary)
+                argv = (ctypes.c_void_p * 4)(ctypes.addressof(a_out), ctypes.addressof(a_vals), ctypes.addressof(a_it),
+                                             ctypes.addressof(a_vary))
+                assert lib.ormi_hip_launch(h.value, grid, block, 0, argv) == 0, lib.ormi_hip_last_error()
+                ev.sync()
+                best = 1e9
+                for _ in range(3):
+                    e0, e1 = ev.new(), ev.new()
+                    ev.record(e0)
+                    assert lib.ormi_hip_launch(h.value, grid, block, 0, argv) == 0
+                    ev.record(e1)
+                    ev.sync()
+                    best = min(best, ev.elapsed_ms(e0, e1))
+                waves = cus * bpc * 4
+                tf = waves * iters * bpc * 8 * flops_per / (best * 1e-3) / 1e12
+                peak = BF16_PEAK_TFLOPS if "bf16" in name else FP32_PEAK_TFLOPS
+                rows.append(f"| {inst} | {'random N(0,1/64)' if vary else 'constant'} | {bpc} | {best:.3f} | "
+                            f"{tf:.1f} | {100 * tf / peak:.1f}% |")
+                log(rows[-1])
+    lines = ["# Matrix-core ceilings (register-only MFMA loops)", "", f"Command (from the repo root): `{cmd}`", "",
+             "4 independent accumulators per wave, 4 waves per 256-thread block, one or two blocks per compute unit "
+             "(1 or 2 waves per SIMD); the kernel (`MFMA_PROBE_SRC` in bench.py) is compiled and launched through "
+             "libormi_hip's hipRTC entry points and timed with HIP events, best of 3 launches after one untimed. "
+             "Operands are loaded once into 8 fragment registers and cycled: either all 8 hold the same N(0, 1/64) "
+             "values (constant) or 8 different sets (random, changing every instruction).", "",
+             "| instruction | operands | waves/SIMD | ms | TFLOP/s | of datasheet dense peak |",
+             "|---|---|---|---|---|---|"] + rows
+    out_md.write_text("\n".join(lines) + "\n")
+    print(out_md.read_text())
+
+
 def gemm_k_sweep(out_md: Path, cmd: str, rounds: int = 3, n: int = 10) -> None:
     """Time of the fp32 GEMM against K at the C5 output shapes (1024x4096: one
     128x128 tile per compute unit; 4096x4096: four), per epilogue, through
@@ -1058,6 +1192,8 @@ def main():
                     help="summarize a rocprofv3 --kernel-trace run into per-kernel durations (no GPU needed); "
                          "--trace-cmd gives the command that made the run")
     ap.add_argument("--trace-cmd", default="", help="the rocprofv3 command recorded by --trace-report")
+    ap.add_argument("--mfma-ceiling", metavar="OUT_MD",
+                    help="register-only MFMA loops: the matrix cores' sustained bf16 and fp32 rates (markdown)")
     ap.add_argument("--vendor-gemm", metavar="OUT_MD",
                     help="time the C4/C5 GEMM shapes against torch.matmul (hipBLASLt) and write a markdown summary")
     args = ap.parse_args()
@@ -1069,6 +1205,9 @@ def main():
         return
     if args.vendor_gemm:
         vendor_gemm(Path(args.vendor_gemm), "python3 bench.py --vendor-gemm profiles/gemm_vs_hipblaslt.md")
+        return
+    if args.mfma_ceiling:
+        mfma_ceiling(Path(args.mfma_ceiling), f"python3 bench.py --mfma-ceiling {args.mfma_ceiling}")
         return
     if args.mfma_report:
         only = args.only or "c4"
