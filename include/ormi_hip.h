@@ -230,6 +230,31 @@ int ormi_hip_gemm_ex(const ormi_gemm_desc* desc, const ormi_gemm_epilogue* epi);
 #define ORMI_GEMM_NOALLOC_SCRATCH_BYTES (32u << 20)
 int ormi_hip_gemm_ex_noalloc(const ormi_gemm_desc* desc, const ormi_gemm_epilogue* epi);
 
+/* Two products as one call: the result is that of ormi_hip_gemm_ex(d0, e0)
+ * followed by ormi_hip_gemm_ex(d1, e1), bit for bit. Replaces the two
+ * independent cuda::matmul calls (csrc/backend/cuda/kernels/blas/matmul.cu:
+ * 19-122) the reference's MATMUL backward issues on one dZ: dX = dZ Y^T and
+ * dY = X^T dZ (csrc/core/ops/blas/matmul.cpp:84-124), one after the other.
+ * When neither product writes what the other reads or writes and each would
+ * run alone as the fp32 128x128-tile kernel (one batch, M and N multiples of
+ * 128, K of 32, at least one tile per compute unit, no K split, its epilogue
+ * NONE or in the store), and their layouts and epilogues are the pair the
+ * kernel is built for (one product with both operands k-contiguous, NONE or
+ * MUL_FN_D, the other with both mn-contiguous, NONE or ADD: dZ W^T with the
+ * activation's derivative and X^T dZ with the SGD update), both run as ONE
+ * persistent launch whose work-groups take the first product's tiles, then the
+ * second's, through one pipeline: the fill, the epilogue latency and the
+ * last-wave tail are paid once instead of twice. That pays for shallow pairs
+ * and costs for deep ones (a long persistent stream runs each k-tile slower),
+ * so by default only pairs of at most 48 k-tiles (of 32) per work-group are
+ * grouped. Otherwise the two run in order as their own calls would. *grouped
+ * (if not NULL) is set to 1 when they ran as one launch, else 0. Both
+ * descriptors are checked before anything is launched: an invalid one returns
+ * its error and launches nothing. ORMI_GEMM_PAIR=0 turns grouping off, =2
+ * groups every eligible pair whatever its depth. */
+int ormi_hip_gemm_pair(const ormi_gemm_desc* d0, const ormi_gemm_epilogue* e0, const ormi_gemm_desc* d1,
+                       const ormi_gemm_epilogue* e1, int* grouped);
+
 /* ------------------------------------------------------------- reduction --
  * Replaces the reference's reduction kernel entry
  *   cuda::sum(in_buf, in_view, axes, out_view, keepdims)

@@ -65,6 +65,9 @@ namespace ormi::hip {
     // the switch for that matching (on unless ORMI_GEMM_EPILOGUE=0).
     uint64_t gemm_epilogue_count();
     void set_gemm_epilogue(bool on);
+    // Pairs of products the scheduler launched as one grouped GEMM
+    // (ormi_hip_gemm_pair) so far.
+    uint64_t gemm_pair_count();
 
     // ------------------------------------------------------- allocator --
     struct AllocatorStats {

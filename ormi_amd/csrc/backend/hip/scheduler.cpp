@@ -161,10 +161,12 @@ namespace ormi::hip {
         return c;
     }
 
-    // The product of MATMUL node `root` into `out` (contiguous fp32, root's
-    // shape), with an optional epilogue: same shape rule as the reference,
-    // trans/ld derived from strides, batch dims broadcast with stride 0.
-    static void gemm_into(const NodePtr& root, float* out, const ormi_gemm_epilogue* epi) {
+    // The descriptor of MATMUL node `root`'s product into `out` (contiguous
+    // fp32, root's shape): same shape rule as the reference, trans/ld derived
+    // from strides, batch dims broadcast with stride 0. Realizes the operands
+    // (converting other dtypes); `hold` keeps the nodes whose buffers the
+    // descriptor points at.
+    static ormi_gemm_desc gemm_desc(const NodePtr& root, float* out, std::vector<NodePtr>& hold) {
         NodePtr A = root->parents[0], B = root->parents[1];
         realize(A);
         realize(B);
@@ -225,19 +227,42 @@ namespace ormi::hip {
             d.a_batch_stride[i] = abs[i];
             d.b_batch_stride[i] = bbs[i];
         }
-        ORMI_HIP_CHECK(ormi_hip_gemm_ex(&d, epi));
+        hold.push_back(A);
+        hold.push_back(B);
+        return d;
     }
+
+    // A GEMM ready to launch: node n gets `out` once it has run (and the
+    // product node g gets `aux`, for an activation epilogue). n is the MATMUL
+    // itself for a plain product, else the element-wise node its epilogue
+    // computes.
+    struct PreparedGemm {
+        NodePtr n, g;
+        ormi_gemm_desc d{};
+        ormi_gemm_epilogue e{};
+        std::shared_ptr<Buffer> out, aux;
+        std::vector<NodePtr> hold;
+        bool empty = false;  // no elements: nothing to launch
+    };
+
+    static void commit(PreparedGemm& p);
+    static bool launch_paired(PreparedGemm& self);
 
     // MATMUL on the HIP device (replaces cuda::matmul, csrc/backend/cuda/kernels/blas/
     // matmul.cu:19-122).
-    static void matmul_handler(const NodePtr& root) {
+    static void prepare_matmul(const NodePtr& root, PreparedGemm& pg) {
         realize(root->parents[0]);
         realize(root->parents[1]);
-        auto out = empty(root->view.shape, DeviceEnum::HIP, DType::Float32);
-        root->data = out;
-        root->view.strides = calc_contiguous_strides(root->view.shape);
-        if (out->numel() == 0) return;
-        gemm_into(root, (float*)out->ptr, nullptr);
+        pg.n = root;
+        pg.out = empty(root->view.shape, DeviceEnum::HIP, DType::Float32);
+        pg.empty = pg.out->numel() == 0;
+        if (!pg.empty) pg.d = gemm_desc(root, (float*)pg.out->ptr, pg.hold);
+    }
+    static void matmul_handler(const NodePtr& root) {
+        PreparedGemm pg;
+        prepare_matmul(root, pg);
+        if (!pg.empty && !launch_paired(pg)) ORMI_HIP_CHECK(ormi_hip_gemm_ex(&pg.d, nullptr));
+        commit(pg);
     }
 
     // ------------------------------------------------ GEMM epilogue fusion --
@@ -384,13 +409,13 @@ namespace ormi::hip {
         return false;
     }
 
-    // Run n as its matched GEMM; false (nothing launched) when a realized
+    // Prepare n as its matched GEMM; false (nothing prepared) when a realized
     // operand turns out not to be fp32.
-    static bool run_gemm_epilogue(const NodePtr& n, const EpilogueMatch& m) {
+    static bool prepare_epilogue(const NodePtr& n, const EpilogueMatch& m, PreparedGemm& pg) {
         if (m.d) realize(m.d);
         if (m.s) realize(m.s);
         if ((m.d && m.d->data->dtype != DType::Float32) || (m.s && m.s->data->dtype != DType::Float32)) return false;
-        ormi_gemm_epilogue e{};
+        ormi_gemm_epilogue& e = pg.e;
         e.kind = m.kind;
         e.fn = m.fn;
         e.form = m.form;
@@ -408,20 +433,36 @@ namespace ormi::hip {
             e.d_stride_m = st[0];
             e.d_stride_n = st[1];
         }
-        auto out = empty(n->view.shape, DeviceEnum::HIP, DType::Float32);
-        std::shared_ptr<Buffer> aux;
+        pg.n = n;
+        pg.g = m.g;
+        pg.hold = {m.d, m.s};
+        pg.out = empty(n->view.shape, DeviceEnum::HIP, DType::Float32);
         if (m.kind == ORMI_GEMM_EPI_UNARY) {
-            aux = empty(m.g->view.shape, DeviceEnum::HIP, DType::Float32);
-            e.aux = (float*)aux->ptr;
+            pg.aux = empty(m.g->view.shape, DeviceEnum::HIP, DType::Float32);
+            e.aux = (float*)pg.aux->ptr;
         }
-        if (out->numel() > 0) gemm_into(m.g, (float*)out->ptr, &e);
-        n->data = out;
-        n->view.strides = calc_contiguous_strides(n->view.shape);
-        if (aux) {
-            m.g->data = aux;
-            m.g->view.strides = calc_contiguous_strides(m.g->view.shape);
+        pg.empty = pg.out->numel() == 0;
+        if (!pg.empty) pg.d = gemm_desc(m.g, (float*)pg.out->ptr, pg.hold);
+        return true;
+    }
+
+    static void commit(PreparedGemm& pg) {
+        pg.n->data = pg.out;
+        pg.n->view.strides = calc_contiguous_strides(pg.n->view.shape);
+        if (pg.aux) {
+            pg.g->data = pg.aux;
+            pg.g->view.strides = calc_contiguous_strides(pg.g->view.shape);
         }
-        g_epilogue_gemms.fetch_add(1);
+        if (pg.g) g_epilogue_gemms.fetch_add(1);
+    }
+
+    // Run n as its matched GEMM; false (nothing launched) when a realized
+    // operand turns out not to be fp32.
+    static bool run_gemm_epilogue(const NodePtr& n, const EpilogueMatch& m) {
+        PreparedGemm pg;
+        if (!prepare_epilogue(n, m, pg)) return false;
+        if (!pg.empty && !launch_paired(pg)) ORMI_HIP_CHECK(ormi_hip_gemm_ex(&pg.d, &pg.e));
+        commit(pg);
         return true;
     }
 
@@ -437,6 +478,8 @@ namespace ormi::hip {
         size_t nroots = 0;
         bool indexed = false;
         std::unordered_map<Node*, NodePtr> act;  // product -> f(product)
+        bool gemms_indexed = false;
+        std::vector<NodePtr> gemms;  // products the scope will realize (pairing candidates)
     };
     static thread_local RealizeScope* t_scope = nullptr;
     // The outermost realize owns the scope; nested realizes share it.
@@ -481,6 +524,116 @@ namespace ormi::hip {
         }
         const auto it = sc.act.find(p.get());
         return it == sc.act.end() || it->second->is_realized() ? nullptr : it->second;
+    }
+
+    // ------------------------------------------------------ GEMM pairing --
+    // The backward of a MATMUL builds two products on one dZ, dX = dZ Y^T and
+    // dY = X^T dZ (reference csrc/core/ops/blas/matmul.cpp:84-124); in a
+    // training step dX (often with an activation's derivative, a MUL_FN_D
+    // epilogue) feeds the layer below while dY feeds the weight update (an ADD
+    // epilogue). The two are independent, so when the scheduler is about to
+    // launch one, another product of the same realize scope whose inputs are
+    // all realized runs with it through ormi_hip_gemm_pair: one persistent
+    // launch when the library can group them, else two calls in order. The
+    // results are the same bits either way; only when the partner's buffer is
+    // filled changes. ORMI_GEMM_PAIR=0 (read by the library on each call) keeps
+    // the launches separate.
+    static std::atomic<uint64_t> g_gemm_pairs{0};
+    uint64_t gemm_pair_count() { return g_gemm_pairs.load(); }
+
+    // Whether a product of this 2-D shape, depth and epilogue kind is one the
+    // library can group: fp32, whole 128x128 tiles, K in whole 32-deep tiles,
+    // at least one tile per compute unit, no activation epilogue. The library
+    // checks the rest (layouts, strides, independence).
+    static bool pair_shape(long long M, long long N, long long K, int kind) {
+        return M > 0 && N > 0 && K > 0 && M % 128 == 0 && N % 128 == 0 && K % 32 == 0 &&
+               (M / 128) * (N / 128) >= device_compute_units() && kind != ORMI_GEMM_EPI_UNARY;
+    }
+    static bool pair_candidate_shape(const NodePtr& g, int kind) {
+        const auto& a = g->parents[0];
+        const auto& b = g->parents[1];
+        if (g->view.shape.size() != 2 || a->dtype != DType::Float32 || b->dtype != DType::Float32) return false;
+        return pair_shape(g->view.shape[0], g->view.shape[1], a->view.shape.back(), kind);
+    }
+
+    // x holds a buffer, or is a chain of views over one that does.
+    static bool realized_through_views(NodePtr x) {
+        while (!x->is_realized() && is_view_op(x->op)) x = x->parents[0];
+        return x->is_realized();
+    }
+
+    static const std::vector<NodePtr>& scope_gemms(RealizeScope& sc) {
+        if (sc.gemms_indexed) return sc.gemms;
+        sc.gemms_indexed = true;
+        // The roots and every operand of a MATMUL below them: nodes the scope
+        // realizes whatever the order.
+        std::vector<NodePtr> stack, found;
+        std::unordered_set<Node*> seen, taken;
+        auto take = [&](const NodePtr& c) {
+            if (!c->is_realized() && taken.insert(c.get()).second) found.push_back(c);
+        };
+        for (size_t i = 0; i < sc.nroots; ++i) {
+            const NodePtr& r = sc.roots[i];
+            if (!r || r->is_realized()) continue;
+            take(r);
+            if (seen.insert(r.get()).second) stack.push_back(r);
+        }
+        while (!stack.empty()) {
+            const NodePtr n = stack.back();
+            stack.pop_back();
+            if (n->op == OpEnum::MATMUL)
+                for (const auto& q : n->parents) take(q);
+            for (const auto& q : n->parents)
+                if (!q->is_realized() && seen.insert(q.get()).second) stack.push_back(q);
+        }
+        for (const auto& c : found) {
+            EpilogueMatch m;
+            const bool gemm = c->op == OpEnum::MATMUL || (c->device.type == DeviceEnum::HIP && match_epilogue(c, m));
+            if (gemm && c->device.type == DeviceEnum::HIP) sc.gemms.push_back(c);
+        }
+        return sc.gemms;
+    }
+
+    static std::vector<NodePtr> dependencies(const NodePtr& n);
+
+    // Launch self together with a ready partner from the scope; false (nothing
+    // launched) when there is none.
+    static bool launch_paired(PreparedGemm& self) {
+        if (!t_scope || self.empty) return false;
+        const ormi_gemm_desc& d = self.d;
+        if (d.dtype != ORMI_DTYPE_F32 || d.batch_ndim != 0 || !pair_shape(d.M, d.N, d.K, self.e.kind)) return false;
+        const Node* self_product = self.g ? self.g.get() : self.n.get();
+        for (const NodePtr& c : scope_gemms(*t_scope)) {
+            if (c->is_realized() || c == self.n) continue;
+            EpilogueMatch m;
+            const bool epi = c->op != OpEnum::MATMUL;
+            if (epi && !match_epilogue(c, m)) continue;
+            const NodePtr& g = epi ? m.g : c;
+            if (g.get() == self_product || g->is_realized()) continue;
+            // A product whose activation the scope holds runs as that
+            // activation's epilogue (it stores both), not as a plain GEMM.
+            if (!epi && activation_consumer(c)) continue;
+            if (!pair_candidate_shape(g, epi ? m.kind : ORMI_GEMM_EPI_NONE)) continue;
+            bool ready = true;
+            for (const auto& dep : dependencies(c)) ready = ready && realized_through_views(dep);
+            if (!ready) continue;
+            PreparedGemm other;
+            if (epi) {
+                if (!prepare_epilogue(c, m, other)) continue;
+            } else {
+                prepare_matmul(c, other);
+            }
+            if (other.empty) {
+                commit(other);
+                continue;
+            }
+            int grouped = 0;
+            ORMI_HIP_CHECK(ormi_hip_gemm_pair(&self.d, &self.e, &other.d, epi ? &other.e : nullptr, &grouped));
+            if (grouped) g_gemm_pairs.fetch_add(1);
+            commit(other);
+            return true;
+        }
+        return false;
     }
 
     // An element-wise region: a matched GEMM epilogue, a reduction's store

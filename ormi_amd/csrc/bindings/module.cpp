@@ -378,6 +378,8 @@ PYBIND11_MODULE(ormi_backend, m) {
           "Element-wise nodes realized as a GEMM epilogue (ormi_hip_gemm_ex) in this process.");
     m.def("set_gemm_epilogue", &hip::set_gemm_epilogue, py::arg("on"),
           "Turn GEMM epilogue fusion on or off (default: on unless ORMI_GEMM_EPILOGUE=0).");
+    m.def("gemm_pair_count", &hip::gemm_pair_count,
+          "Pairs of independent products the HIP scheduler ran as one grouped GEMM launch in this process.");
     m.def("_plan_kernel", &plan_kernel);
     m.def("_plan_group", &plan_group);
     m.def("realize_all", &execute_graph_group,

@@ -1440,7 +1440,11 @@ namespace ormi_hip {
 static int gemm_run_locked(const ormi_gemm_desc* d, const Epi& epi, long long batch, bool noalloc, bool packed);
 static int gemm_packed_locked(const ormi_gemm_desc* d, const Epi& epi, long long batch);
 
-static int gemm_run(const ormi_gemm_desc* d, const ormi_gemm_epilogue* epi_in, bool noalloc) {
+// Checks one call's arguments and converts its epilogue; *nothing is set when
+// the product has no elements (nothing to launch).
+static int gemm_check(const ormi_gemm_desc* d, const ormi_gemm_epilogue* epi_in, long long* batch_out, Epi* epi,
+                      bool* nothing) {
+    *nothing = false;
     if (!d) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_gemm: null descriptor");
     if (d->M < 0 || d->N < 0 || d->K < 0) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_gemm: negative dimension");
     if (d->batch_ndim < 0 || d->batch_ndim > ORMI_GEMM_MAX_BATCH_DIMS)
@@ -1453,14 +1457,24 @@ static int gemm_run(const ormi_gemm_desc* d, const ormi_gemm_epilogue* epi_in, b
         batch *= d->batch_shape[i];  // <= 65535 * (2^31 - 1) before the check below: no overflow
         if (batch > 65535) return fail(ORMI_HIP_ERR_UNSUPPORTED, "ormi_hip_gemm: more than 65535 batches");
     }
-    if ((long long)d->M * d->N == 0) return ORMI_HIP_OK;
+    *batch_out = batch;
+    if ((long long)d->M * d->N == 0) {
+        *nothing = true;
+        return ORMI_HIP_OK;
+    }
     // With K == 0 the operands hold no elements (an empty buffer may have no
     // address) and are never read.
     if (!d->c || (d->K > 0 && (!d->a || !d->b))) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_gemm: null operand");
     if (batch * d->M > 0x7fffffffLL) return fail(ORMI_HIP_ERR_UNSUPPORTED, "ormi_hip_gemm: more than 2^31 output rows");
+    return make_epi(d, epi_in, batch, epi);
+}
+
+static int gemm_run(const ormi_gemm_desc* d, const ormi_gemm_epilogue* epi_in, bool noalloc) {
+    long long batch = 1;
     Epi epi;
-    int rc = make_epi(d, epi_in, batch, &epi);
-    if (rc != ORMI_HIP_OK) return rc;
+    bool nothing = false;
+    int rc = gemm_check(d, epi_in, &batch, &epi, &nothing);
+    if (rc != ORMI_HIP_OK || nothing) return rc;
     rc = ensure_init();
     if (rc != ORMI_HIP_OK) return rc;
     rc = drain_queue();
@@ -1469,6 +1483,149 @@ static int gemm_run(const ormi_gemm_desc* d, const ormi_gemm_epilogue* epi_in, b
     // Held until this call's kernels are enqueued (see g_ws_mu).
     std::lock_guard<std::mutex> ws_lock(g_ws_mu);
     return gemm_run_locked(d, epi, batch, noalloc, false);
+}
+
+// ------------------------------------------------------------ GEMM pairs --
+// Whether product d (one batch) runs alone as fp32 direct-load configuration
+// 1 with whole 128x128 tiles, no K split and its epilogue in the store: the
+// conditions gemm_run_locked takes that path under, so that the pair kernel,
+// which computes each tile as that path does, gives the same bits. a_kc /
+// b_kc: the operand layouts that path would use.
+static bool pair_eligible(const ormi_gemm_desc* d, const Epi& epi, long long batch, bool* a_kc, bool* b_kc) {
+    if (d->dtype != ORMI_DTYPE_F32 || batch != 1 || d->K <= 0) return false;
+    if (env_cfg("ORMI_GEMM_F32_DMA", 1) == 0) return false;
+    *a_kc = d->a_stride_k == 1;
+    *b_kc = d->b_stride_k == 1;
+    const bool a_mc = d->a_stride_m == 1, b_nc = d->b_stride_n == 1;
+    if (!(*a_kc || a_mc) || !(*b_kc || b_nc) || !aligned16(d->a) || !aligned16(d->b)) return false;
+    const long long a_other = *a_kc ? d->a_stride_m : d->a_stride_k;
+    const long long b_other = *b_kc ? d->b_stride_n : d->b_stride_k;
+    if (a_other % 4 != 0 || b_other % 4 != 0) return false;
+    if (d->M % 128 != 0 || d->N % 128 != 0 || d->K % 32 != 0) return false;  // whole tiles (and 16-byte chunks)
+    const long long a_span32 = *a_kc ? 256LL * d->a_stride_m * 4 : 64LL * d->a_stride_k * 4 + 1024;
+    const long long b_span32 = *b_kc ? 256LL * d->b_stride_n * 4 : 64LL * d->b_stride_k * 4 + 1024;
+    if (a_span32 >= (1LL << 32) || b_span32 >= (1LL << 32)) return false;
+    // Configuration 1 without a K split: at least one tile per compute unit.
+    const long long tiles = (long long)(d->M / 128) * (d->N / 128);
+    const int forced = env_cfg("ORMI_GEMM_F32_DMA_CFG", -1);
+    if ((forced >= 0 && forced <= 9 && forced != 1) || tiles < compute_units()) return false;
+    return epi.kind == ORMI_GEMM_EPI_NONE || (epi.kind != ORMI_GEMM_EPI_UNARY && epi_in_store(epi));
+}
+
+// Byte ranges [lo, hi) a product reads and writes (one batch).
+struct Ranges {
+    intptr_t r_lo[4], r_hi[4], w_lo[2], w_hi[2];
+    int nr = 0, nw = 0;
+};
+static void add_range(intptr_t* lo, intptr_t* hi, int* n, const void* base, long long e_lo, long long e_hi) {
+    lo[*n] = (intptr_t)base + (intptr_t)e_lo * 4;
+    hi[*n] = (intptr_t)base + (intptr_t)e_hi * 4 + 4;
+    ++*n;
+}
+static Ranges ranges_of(const ormi_gemm_desc* d, const Epi& epi) {
+    Ranges r;
+    long long lo = 0, hi = 0;
+    span(d->M, d->a_stride_m, &lo, &hi);
+    span(d->K, d->a_stride_k, &lo, &hi);
+    add_range(r.r_lo, r.r_hi, &r.nr, d->a, lo, hi);
+    lo = hi = 0;
+    span(d->K, d->b_stride_k, &lo, &hi);
+    span(d->N, d->b_stride_n, &lo, &hi);
+    add_range(r.r_lo, r.r_hi, &r.nr, d->b, lo, hi);
+    if (epi_reads_d(epi)) {
+        lo = hi = 0;
+        span(d->M, epi.d_sm, &lo, &hi);
+        span(d->N, epi.d_sn, &lo, &hi);
+        add_range(r.r_lo, r.r_hi, &r.nr, epi.d, lo, hi);
+    }
+    if (epi.kind != ORMI_GEMM_EPI_NONE && epi.s) add_range(r.r_lo, r.r_hi, &r.nr, epi.s, 0, 0);
+    const long long mn = (long long)d->M * d->N;
+    add_range(r.w_lo, r.w_hi, &r.nw, d->c, 0, mn - 1);
+    if (epi.kind == ORMI_GEMM_EPI_UNARY && epi.aux) add_range(r.w_lo, r.w_hi, &r.nw, epi.aux, 0, mn - 1);
+    return r;
+}
+// Whether running x and y in either order (or at once) gives the same result:
+// neither writes what the other reads or writes.
+static bool independent(const Ranges& x, const Ranges& y) {
+    auto meet = [](intptr_t a0, intptr_t a1, intptr_t b0, intptr_t b1) { return a0 < b1 && b0 < a1; };
+    for (int i = 0; i < x.nw; ++i) {
+        for (int j = 0; j < y.nr; ++j)
+            if (meet(x.w_lo[i], x.w_hi[i], y.r_lo[j], y.r_hi[j])) return false;
+        for (int j = 0; j < y.nw; ++j)
+            if (meet(x.w_lo[i], x.w_hi[i], y.w_lo[j], y.w_hi[j])) return false;
+    }
+    for (int i = 0; i < y.nw; ++i)
+        for (int j = 0; j < x.nr; ++j)
+            if (meet(y.w_lo[i], y.w_hi[i], x.r_lo[j], x.r_hi[j])) return false;
+    return true;
+}
+
+static GemmParams pair_params(const ormi_gemm_desc* d, const Epi& epi) {
+    GemmParams p{};
+    p.a = (const char*)d->a;
+    p.b = (const char*)d->b;
+    p.c = d->c;
+    p.M = d->M; p.N = d->N; p.K = d->K;
+    p.a_sm = d->a_stride_m; p.a_sk = d->a_stride_k;
+    p.b_sk = d->b_stride_k; p.b_sn = d->b_stride_n;
+    p.batch = 1;
+    p.splits = 1;
+    p.k_per_split = d->K;
+    p.tiles_m = d->M / 128;
+    p.tiles_n = d->N / 128;
+    p.epi = epi;
+    return p;
+}
+
+static int gemm_pair(const ormi_gemm_desc* d0, const ormi_gemm_epilogue* e0, const ormi_gemm_desc* d1,
+                     const ormi_gemm_epilogue* e1, int* grouped) {
+    if (grouped) *grouped = 0;
+    long long b0 = 1, b1 = 1;
+    Epi epi0, epi1;
+    bool none0 = false, none1 = false;
+    int rc = gemm_check(d0, e0, &b0, &epi0, &none0);
+    if (rc != ORMI_HIP_OK) return rc;
+    rc = gemm_check(d1, e1, &b1, &epi1, &none1);
+    if (rc != ORMI_HIP_OK) return rc;
+    rc = ensure_init();
+    if (rc != ORMI_HIP_OK) return rc;
+    rc = drain_queue();
+    if (rc != ORMI_HIP_OK) return rc;
+    std::lock_guard<std::mutex> ws_lock(g_ws_mu);
+    bool ak0 = false, bk0 = false, ak1 = false, bk1 = false;
+    const int mode = env_cfg("ORMI_GEMM_PAIR", 1);
+    if (!none0 && !none1 && mode != 0 && pair_eligible(d0, epi0, b0, &ak0, &bk0) &&
+        pair_eligible(d1, epi1, b1, &ak1, &bk1) && independent(ranges_of(d0, epi0), ranges_of(d1, epi1))) {
+        const GemmParams p0 = pair_params(d0, epi0), p1 = pair_params(d1, epi1);
+        const long long t0 = (long long)p0.tiles_m * p0.tiles_n, t1 = (long long)p1.tiles_m * p1.tiles_n;
+        const int groups = (int)std::min<long long>(compute_units(), t0 + t1);
+        // Grouping pays while each work-group's stream is short: one box, dX
+        // (1024 x 4096, TT, gelu') with dW (4096 x 1024, FF, SGD), both at
+        // depth K, two launches -> one: K 64 28.2 -> 25.7 us, 128 36.1 -> 33.8,
+        // 256 50.8 -> 48.3, 512 79.2 -> 76.7 (32 k-tiles per work-group), but
+        // K 1024 136.7 -> 137.6 (64), and C5's layer-2 pair (256) 500.5 ->
+        // 515.8: a stream twice as long runs each k-tile slower (two 4-tile
+        // persistent launches of one product beat one 8-tile launch by 23 us).
+        // So by default (1) only streams of at most kPairMaxKTiles k-tiles per
+        // work-group are grouped; 2 groups every eligible pair.
+        constexpr long long kPairMaxKTiles = 48;
+        const long long per_group = (t0 * (p0.K / 32) + t1 * (p1.K / 32) + groups - 1) / groups;
+        // The kernel takes the products in one order of layouts; independent
+        // products may run in either.
+        const bool launched = (mode == 2 || per_group <= kPairMaxKTiles) &&
+                              (run32_dma_pair(p0, ak0, bk0, p1, ak1, bk1, groups) ||
+                               run32_dma_pair(p1, ak1, bk1, p0, ak0, bk0, groups));
+        if (launched) {
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return fail(ORMI_HIP_ERR_RUNTIME, std::string("ormi_hip_gemm_pair launch: ") + hipGetErrorString(e));
+            if (grouped) *grouped = 1;
+            return ORMI_HIP_OK;
+        }
+    }
+    // Otherwise the two products in order, each as its own call would run.
+    if (!none0) rc = gemm_run_locked(d0, epi0, b0, false, false);
+    if (rc != ORMI_HIP_OK || none1) return rc;
+    return gemm_run_locked(d1, epi1, b1, false, false);
 }
 
 // Packed operands (gemm_pack_kernel), grown on demand and kept, like the
@@ -1756,4 +1913,9 @@ extern "C" int ormi_hip_gemm_ex(const ormi_gemm_desc* d, const ormi_gemm_epilogu
 
 extern "C" int ormi_hip_gemm_ex_noalloc(const ormi_gemm_desc* d, const ormi_gemm_epilogue* epi) {
     return gemm_run(d, epi, true);
+}
+
+extern "C" int ormi_hip_gemm_pair(const ormi_gemm_desc* d0, const ormi_gemm_epilogue* e0, const ormi_gemm_desc* d1,
+                                  const ormi_gemm_epilogue* e1, int* grouped) {
+    return ormi_hip::gemm_pair(d0, e0, d1, e1, grouped);
 }

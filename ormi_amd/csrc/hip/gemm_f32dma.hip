@@ -122,6 +122,7 @@ __device__ __forceinline__ u32x4_t frag32(const lds_char* lds, int row0, int s) 
 template <int BM, int BN, int BK, int WGM, int WGN, bool A_KC, bool B_KC>
 struct Il32 {
     static constexpr int NW = WGM * WGN, KS = BK / 8;
+    static constexpr bool kAKC = A_KC, kBKC = B_KC;
     static constexpr int WTM = BM / WGM, WTN = BN / WGN, TM = WTM / 32, TN = WTN / 32;
     static constexpr int A_BYTES = BM * BK * 4, STAGE = A_BYTES + BN * BK * 4;
     using PlanA = Dma32<BM, A_KC, NW, BK>;
@@ -134,10 +135,12 @@ struct Il32 {
     static constexpr int load_lo(int s) { return s >= KS - 1 ? PER_TILE : s * PER_TILE / (KS - 1); }
     static constexpr int mem_ops(int s) { return NR + load_lo(s + 1) - load_lo(s); }
 
-    template <int S>
+    // LA / LB: the load plans (PlanA / PlanB, or plans of the same extents for
+    // another operand layout: issuing a load does not depend on the layout).
+    template <int S, class LA, class LB>
     __device__ __forceinline__ static void mem_op(int o, u32x4_t (&fa)[TM], u32x4_t (&fb)[TN],
                                                   const lds_char* rs, int rks, int wm, int wn, lds_char* fs,
-                                                  const char* ta, const char* tb, const PlanA& pa, const PlanB& pb) {
+                                                  const char* ta, const char* tb, const LA& pa, const LB& pb) {
         // Reads in the order the next step's first MFMAs use them: A0, B0.., A1..
         if (o == 0) {
             fa[0] = frag32<BM, A_KC, BK>(rs, wm * WTM, rks);
@@ -156,11 +159,11 @@ struct Il32 {
     // MFMAs of one k-step, element-major (consecutive MFMAs on one
     // accumulator are TM * TN apart), each followed by its share of the
     // step's memory instructions.
-    template <int S>
+    template <int S, class LA, class LB>
     __device__ __forceinline__ static void run(f32x16_t (&acc)[TM][TN], const u32x4_t (&ua)[TM],
                                                const u32x4_t (&ub)[TN], u32x4_t (&fa)[TM], u32x4_t (&fb)[TN],
                                                const lds_char* rs, int rks, int wm, int wn, lds_char* fs,
-                                               const char* ta, const char* tb, const PlanA& pa, const PlanB& pb) {
+                                               const char* ta, const char* tb, const LA& pa, const LB& pb) {
         constexpr int NO = mem_ops(S);
 #pragma unroll
         for (int n = 0; n < NM; ++n) {
@@ -170,7 +173,7 @@ struct Il32 {
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int o = n * NO / NM; o < (n + 1) * NO / NM; ++o) {
-                mem_op<S>(o, fa, fb, rs, rks, wm, wn, fs, ta, tb, pa, pb);
+                mem_op<S, LA, LB>(o, fa, fb, rs, rks, wm, wn, fs, ta, tb, pa, pb);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
@@ -478,6 +481,216 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32dma_persist_kernel(Gem
     }
 }
 
+// Two independent products in one persistent launch (the dX and dW GEMMs of
+// one layer's backward read the same dZ and nothing of each other). Problem q
+// has its own operands, layouts (A_KCq / B_KCq), K and epilogue (EKq), each in
+// whole tiles with one batch and no K split. The tiles of problem 0, then of
+// problem 1, form one list; work-group b takes entries b, b + G, b + 2G, ...,
+// so it runs its problem-0 tiles first, then its problem-1 tiles, as one
+// stream of k-tiles through one LDS ring: the first k-tiles of its problem-1
+// stream are loading while its last problem-0 tile finishes. A tile is
+// computed exactly as gemm_f32dma_kernel / gemm_f32dma_persist_kernel compute
+// it (the same k-steps in the same order, the same epilogue), so each output
+// is bit-identical to its product's own launch.
+template <int BM, int BN, int BK, int WGM, int WGN, int STAGES, bool A_KC0, bool B_KC0, int EK0, bool A_KC1,
+          bool B_KC1, int EK1>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32dma_pair_kernel(GemmParams p0, GemmParams p1) {
+    static_assert(STAGES >= 2 && STAGES <= 5, "2 to 5 stages");
+    using St0 = Il32<BM, BN, BK, WGM, WGN, A_KC0, B_KC0>;
+    using St1 = Il32<BM, BN, BK, WGM, WGN, A_KC1, B_KC1>;
+    constexpr int TM = St0::TM, TN = St0::TN, WTM = St0::WTM, WTN = St0::WTN, KS = St0::KS;
+    constexpr int A_BYTES = St0::A_BYTES, STAGE = St0::STAGE, PER_TILE = St0::PER_TILE;
+    static_assert(St1::STAGE == STAGE && St1::PER_TILE == PER_TILE && St1::PA == St0::PA, "one ring for both");
+    __shared__ __attribute__((aligned(1024))) char smem[STAGES * STAGE];
+
+    const int T0 = p0.tiles_m * p0.tiles_n, T1 = p1.tiles_m * p1.tiles_n, G = gridDim.x;
+    const int b = blockIdx.x;
+    const int mine = (T0 + T1 - b + G - 1) / G;           // list entries of this work-group
+    const int mine0 = b < T0 ? (T0 - b + G - 1) / G : 0;  // ... of problem 0, which come first
+    const int KT0 = p0.K / BK, KT1 = p1.K / BK;
+    const long long GT0 = (long long)mine0 * KT0, GT = GT0 + (long long)(mine - mine0) * KT1;
+    // Problem 1's value if q, else problem 0's. By value: a conditional over
+    // two lvalues selects between their addresses, which keeps both in
+    // scratch memory.
+    auto pick = [](bool q, auto v0, auto v1) { return q ? v1 : v0; };
+    // Entry i of this work-group: its problem's tile index, XCD-aware remap,
+    // then groups of 4 tile rows (the one-problem kernels' order).
+    auto tile_origin = [&](int i, int& m0, int& n0) {
+        const int u = b + i * G;
+        const bool q = u >= T0;
+        const int T = pick(q, T0, T1), tiles_m = pick(q, p0.tiles_m, p1.tiles_m), tiles_n = pick(q, p0.tiles_n, p1.tiles_n);
+        int t = q ? u - T0 : u;
+        if ((T & 7) == 0) t = (t & 7) * (T >> 3) + (t >> 3);
+        constexpr int GROUP = 4;
+        const int group_size = GROUP * tiles_n;
+        const int g = t / group_size, first_m = g * GROUP;
+        const int gm = min(tiles_m - first_m, GROUP);
+        m0 = (first_m + (t % group_size) % gm) * BM;
+        n0 = ((t % group_size) / gm) * BN;
+    };
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave / WGN, wn = wave % WGN;
+    // Per-lane load offsets of each problem's layouts (whole tiles: independent
+    // of the tile), and the ones of the problem the load stream is in.
+    typename St0::PlanA pa0;
+    typename St0::PlanB pb0;
+    typename St1::PlanA pa1;
+    typename St1::PlanB pb1;
+    pa0.init(p0.a_sm, p0.a_sk, 0, p0.M);
+    pb0.init(p0.b_sn, p0.b_sk, 0, p0.N);
+    pa1.init(p1.a_sm, p1.a_sk, 0, p1.M);
+    pb1.init(p1.b_sn, p1.b_sk, 0, p1.N);
+    typename St0::PlanA la;
+    typename St0::PlanB lb;
+    // Next k-tile of the stream to load: entry li, k-tile lkt of it, at ta /
+    // tb; it stays on the last one once the stream is exhausted.
+    int li = 0, lkt = 0, lkts = 0;
+    const char* ta;
+    const char* tb;
+    long long a_step = 0, b_step = 0;
+    auto set_load_tile = [&](int i) {
+        int m0, n0;
+        tile_origin(i, m0, n0);
+        const bool q = b + i * G >= T0;
+        if (!q) {
+            ta = p0.a + St0::PlanA::origin(p0.a_sm, p0.a_sk, m0, 0);
+            tb = p0.b + St0::PlanB::origin(p0.b_sn, p0.b_sk, n0, 0);
+            a_step = St0::PlanA::kstep(p0.a_sk);
+            b_step = St0::PlanB::kstep(p0.b_sk);
+        } else {
+            ta = p1.a + St1::PlanA::origin(p1.a_sm, p1.a_sk, m0, 0);
+            tb = p1.b + St1::PlanB::origin(p1.b_sn, p1.b_sk, n0, 0);
+            a_step = St1::PlanA::kstep(p1.a_sk);
+            b_step = St1::PlanB::kstep(p1.b_sk);
+        }
+        lkts = pick(q, KT0, KT1);
+#pragma unroll
+        for (int s = 0; s < St0::PA; ++s) la.voff[s] = pick(q, pa0.voff[s], pa1.voff[s]);
+#pragma unroll
+        for (int s = 0; s < St0::PB; ++s) lb.voff[s] = pick(q, pb0.voff[s], pb1.voff[s]);
+    };
+    auto advance = [&]() {
+        if (lkt + 1 < lkts) {
+            ++lkt;
+            ta += a_step;
+            tb += b_step;
+        } else if (li + 1 < mine) {
+            ++li;
+            lkt = 0;
+            set_load_tile(li);
+        }
+    };
+    set_load_tile(0);
+    lds_char* const lds = (lds_char*)smem;
+    // The epilogues' scales are read once, before the loop (a load of one at a
+    // tile's end would make the compiler drain every outstanding load).
+    const float sv0 = EK0 != ORMI_GEMM_EPI_NONE && p0.epi.s
+                          ? __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(*p0.epi.s))) : 0.0f;
+    const float sv1 = EK1 != ORMI_GEMM_EPI_NONE && p1.epi.s
+                          ? __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(*p1.epi.s))) : 0.0f;
+    asm volatile("" ::"s"(p0.c), "s"(p0.N), "s"(sv0), "s"(p1.c), "s"(p1.N), "s"(sv1));
+
+    f32x16_t acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    if (GT == 0) return;
+
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s) {
+        const char* ua = uniform_ptr(ta);
+        const char* ub = uniform_ptr(tb);
+#pragma unroll
+        for (int d = 0; d < St0::PA; ++d) la.issue_one(lds + s * STAGE, ua, d);
+#pragma unroll
+        for (int d = 0; d < St0::PB; ++d) lb.issue_one(lds + s * STAGE + A_BYTES, ub, d);
+        if (s + 1 < GT) advance();
+    }
+    wait_vmcnt<(STAGES - 2) * PER_TILE>();
+    lds_barrier();
+    u32x4_t fa[2][TM], fb[2][TN];
+    // Fragments of k-step 0 of the k-tile in `stage`, in problem St's layouts.
+    auto first_frags = [&](auto st, int at) __attribute__((always_inline)) {
+        using S = decltype(st);
+        const lds_char* cur = lds + at * STAGE;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) fa[0][i] = frag32<BM, S::kAKC, BK>(cur, wm * WTM + i * 32, 0);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) fb[0][j] = frag32<BN, S::kBKC, BK>(cur + A_BYTES, wn * WTN + j * 32, 0);
+    };
+    int stage = 0, free_stage = STAGES - 1;
+    // The k-tiles [g_lo, g_hi) of the stream, all of problem St's tiles
+    // (entries i_lo, i_lo + 1, ...), each KT k-tiles deep; the epilogue kind EK
+    // and params p of that problem.
+    auto run = [&](auto st, auto ek, const GemmParams& p, float sv, long long g_lo, long long g_hi, int i_lo,
+                   int KT) __attribute__((always_inline)) {
+        using St = decltype(st);
+        constexpr int EK = decltype(ek)::value;
+        int tile = i_lo, kt = 0, cm0, cn0;
+        tile_origin(tile, cm0, cn0);
+        for (long long g = g_lo; g < g_hi; ++g) {
+            const int next = stage + 1 == STAGES ? 0 : stage + 1;
+            const lds_char* cur = lds + stage * STAGE;
+            lds_char* fs = lds + free_stage * STAGE;
+            const char* ua = uniform_ptr(ta);
+            const char* ub = uniform_ptr(tb);
+            Steps<St, 0>::run(acc, fa, fb, cur, wm, wn, fs, ua, ub, la, lb);
+            wait_vmcnt_lds<(STAGES - 2) * PER_TILE>();
+            lds_barrier();
+            St::template run<KS - 1>(acc, fa[1], fb[1], fa[0], fb[0], lds + next * STAGE, 0, wm, wn, fs, ua, ub, la, lb);
+            asm volatile("" ::: "memory");
+            if (g + STAGES < GT) advance();
+            stage = next;
+            free_stage = free_stage + 1 == STAGES ? 0 : free_stage + 1;
+            if (++kt == KT) {
+                if constexpr (EK != ORMI_GEMM_EPI_NONE) {
+                    float dv[TM][TN][16];
+                    epi_tile<TM, TN, false, EK>(p.epi, sv, p.c, p.epi.aux, p.epi.d, p.N, cm0 + wm * WTM, cn0 + wn * WTN,
+                                                acc, dv, epi_reads_d(p.epi));
+                } else {
+#pragma unroll
+                    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+                        for (int j = 0; j < TN; ++j) {
+                            const int col = cn0 + wn * WTN + j * 32 + (lane & 31);
+#pragma unroll
+                            for (int r = 0; r < 16; ++r) {
+                                const int row = cm0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                                p.c[(long long)row * p.N + col] = acc[i][j][r];
+                            }
+                        }
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+                kt = 0;
+                if (g + 1 < g_hi) tile_origin(++tile, cm0, cn0);
+            }
+        }
+    };
+    if (GT0 > 0) {
+        first_frags(St0{}, 0);
+        run(St0{}, FnConst<EK0>{}, p0, sv0, 0, GT0, 0, KT0);
+    }
+    if (GT > GT0) {
+        // The last problem-0 step read k-step 0 of this k-tile in problem 0's
+        // layouts; the k-tile has landed (the barrier before that step), so
+        // read it again in problem 1's.
+        first_frags(St1{}, stage);
+        run(St1{}, FnConst<EK1>{}, p1, sv1, GT0, GT, mine0, KT1);
+    }
+    // No load may still be writing this workgroup's LDS when it exits.
+    wait_vmcnt<0>();
+}
+
 template <int BM, int BN, int BK, int WGM, int WGN, int STAGES>
 struct F32DmaLauncher {
     template <bool A_KC, bool B_KC>
@@ -539,6 +752,30 @@ void cfg32_dma(int id, int* bm, int* bn, int* bk) {
 }
 void run32_dma_persist(const GemmParams& p, int groups, bool a_kc, bool b_kc) {
     F32DmaLauncher<128, 128, 32, 2, 4, 4>::run_persist(p, groups, a_kc, b_kc);
+}
+
+namespace {
+template <int EK0, int EK1>
+void launch_pair(const GemmParams& p0, const GemmParams& p1, int groups) {
+    gemm_f32dma_pair_kernel<128, 128, 32, 2, 4, 4, true, true, EK0, false, false, EK1><<<groups, 512>>>(p0, p1);
+}
+}  // namespace
+
+// The layouts and epilogues one layer's backward produces: problem 0 is
+// dZ Wᵀ (both operands k-contiguous), plain or with the activation's
+// derivative in the store (MUL_FN_D); problem 1 is Xᵀ dZ (both operands
+// mn-contiguous), plain or with the SGD update in the store (ADD).
+bool run32_dma_pair(const GemmParams& p0, bool a_kc0, bool b_kc0, const GemmParams& p1, bool a_kc1, bool b_kc1,
+                    int groups) {
+    if (!(a_kc0 && b_kc0 && !a_kc1 && !b_kc1)) return false;
+    const int k0 = p0.epi.kind, k1 = p1.epi.kind;
+    if (k0 != ORMI_GEMM_EPI_NONE && k0 != ORMI_GEMM_EPI_MUL_FN_D) return false;
+    if (k1 != ORMI_GEMM_EPI_NONE && k1 != ORMI_GEMM_EPI_ADD) return false;
+    if (k0 == ORMI_GEMM_EPI_NONE && k1 == ORMI_GEMM_EPI_NONE) launch_pair<ORMI_GEMM_EPI_NONE, ORMI_GEMM_EPI_NONE>(p0, p1, groups);
+    else if (k0 == ORMI_GEMM_EPI_NONE) launch_pair<ORMI_GEMM_EPI_NONE, ORMI_GEMM_EPI_ADD>(p0, p1, groups);
+    else if (k1 == ORMI_GEMM_EPI_NONE) launch_pair<ORMI_GEMM_EPI_MUL_FN_D, ORMI_GEMM_EPI_NONE>(p0, p1, groups);
+    else launch_pair<ORMI_GEMM_EPI_MUL_FN_D, ORMI_GEMM_EPI_ADD>(p0, p1, groups);
+    return true;
 }
 void run32_dma(int id, const GemmParams& p, dim3 grid, bool a_kc, bool b_kc, bool epi) {
     if (id < 0 || id > 9) id = 1;

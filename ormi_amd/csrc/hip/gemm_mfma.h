@@ -128,7 +128,7 @@ inline bool epi_in_store(const Epi& e) {
     return e.kind == ORMI_GEMM_EPI_ADD;
 }
 
-__device__ __forceinline__ bool epi_reads_d(const Epi& e) {
+__host__ __device__ __forceinline__ bool epi_reads_d(const Epi& e) {
     return e.kind == ORMI_GEMM_EPI_ADD || e.kind == ORMI_GEMM_EPI_MUL_FN_D;
 }
 
@@ -566,5 +566,11 @@ void run32_dma(int id, const GemmParams& p, dim3 grid, bool a_kc, bool b_kc, boo
 // work-groups walk the p.tiles_m x p.tiles_n tiles; whole tiles, one batch,
 // no K split; p.epi (its kind compiled in) applied in the store.
 void run32_dma_persist(const GemmParams& p, int groups, bool a_kc, bool b_kc);
+// Two independent products of configuration 1 as one persistent launch of
+// `groups` work-groups (each in whole tiles, one batch, no K split, the
+// epilogue in the store); false, with nothing launched, when the pair of
+// layouts and epilogue kinds is not one the kernel is instantiated for.
+bool run32_dma_pair(const GemmParams& p0, bool a_kc0, bool b_kc0, const GemmParams& p1, bool a_kc1, bool b_kc1,
+                    int groups);
 
 }  // namespace ormi_hip
