@@ -816,6 +816,107 @@ def gemm_k_sweep(out_md: Path, cmd: str, rounds: int = 3, n: int = 10) -> None:
     print(out_md.read_text())
 
 
+def gemm_pair_sweep(out_md: Path, cmd: str, rounds: int = 5, n: int = 20) -> None:
+    """Grouped against separate launches of a layer's backward products
+    through ormi_hip_gemm_pair: dX = dZ W^T (both operands k-contiguous, the
+    activation derivative gelu' in the store) and dW = X^T dZ (both
+    mn-contiguous, the SGD update in place), at the C5 layer shapes over a range
+    of depths and at C5's own layer-2 pair. ORMI_GEMM_PAIR=0 runs them as two
+    launches, =2 as one whatever the depth; the default (1) groups pairs of at
+    most 48 k-tiles per work-group. Best of `rounds` interleaved rounds of n
+    calls (HIP events)."""
+    ev = Events()
+    lib = ev.lib
+
+    class Epi(ctypes.Structure):
+        _fields_ = [("kind", ctypes.c_int), ("fn", ctypes.c_int), ("form", ctypes.c_int), ("s", ctypes.c_void_p),
+                    ("d", ctypes.c_void_p), ("d_stride_m", ctypes.c_int64), ("d_stride_n", ctypes.c_int64),
+                    ("d_batch_stride", ctypes.c_int64 * 4), ("aux", ctypes.c_void_p)]
+
+    lib.ormi_hip_malloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
+    lib.ormi_hip_memcpy_h2d.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]
+    lib.ormi_hip_free.argtypes = [ctypes.c_void_p]
+    lib.ormi_hip_gemm_pair.argtypes = [ctypes.POINTER(_GemmDesc), ctypes.POINTER(Epi), ctypes.POINTER(_GemmDesc),
+                                       ctypes.POINTER(Epi), ctypes.POINTER(ctypes.c_int)]
+    lib.ormi_hip_last_error.restype = ctypes.c_char_p
+    props = _Props()
+    assert lib.ormi_hip_init(0) == 0 and lib.ormi_hip_get_props(ctypes.byref(props)) == 0
+    cus = props.compute_units
+    rng = np.random.default_rng(0)
+    held = []
+
+    def put(a):
+        p = ctypes.c_void_p()
+        assert lib.ormi_hip_malloc(ctypes.byref(p), max(a.nbytes, 4)) == 0, lib.ormi_hip_last_error()
+        assert lib.ormi_hip_memcpy_h2d(p, a.ctypes.data, a.nbytes) == 0, lib.ormi_hip_last_error()
+        held.append(p)
+        return p
+
+    def rand(*shape):
+        return (rng.standard_normal(shape) / 8).astype(np.float32)
+
+    scale = put(np.array([1e-3], np.float32))
+
+    def dx(M, N, K):
+        g = _GemmDesc(dtype=0, M=M, N=N, K=K, a=put(rand(M, K)), a_stride_m=K, a_stride_k=1, b=put(rand(N, K)),
+                      b_stride_k=1, b_stride_n=K, c=put(np.zeros((M, N), np.float32)))
+        return g, Epi(kind=3, fn=8, d=put(rand(M, N)), d_stride_m=N, d_stride_n=1)
+
+    def dw(M, N, K):
+        c = put(rand(M, N))
+        g = _GemmDesc(dtype=0, M=M, N=N, K=K, a=put(rand(K, M)), a_stride_m=1, a_stride_k=M, b=put(rand(K, N)),
+                      b_stride_k=N, b_stride_n=1, c=c)
+        return g, Epi(kind=1, form=1, s=scale, d=c, d_stride_m=N, d_stride_n=1)
+
+    cases = [(f"1024x4096 + 4096x1024, K {k}", (1024, 4096, k), (4096, 1024, k)) for k in (64, 128, 256, 512, 1024)]
+    cases += [("1024x4096 + 4096x4096, K 256", (1024, 4096, 256), (4096, 4096, 256)),
+              ("C5 layer 2: 1024x4096 K 4096 + 4096x4096 K 1024", (1024, 4096, 4096), (4096, 4096, 1024))]
+    built = [(name, dx(*x), dw(*w), x, w) for name, x, w in cases]
+    best = collections.defaultdict(lambda: math.inf)
+    grouped_by = {}
+    saved = os.environ.get("ORMI_GEMM_PAIR")
+    try:
+        for r in range(rounds):
+            for name, (g0, e0), (g1, e1), _, _ in built:
+                for mode in (("0", "2", "1") if r % 2 == 0 else ("1", "2", "0")):
+                    os.environ["ORMI_GEMM_PAIR"] = mode
+                    flag = ctypes.c_int()
+                    args = (ctypes.byref(g0), ctypes.byref(e0), ctypes.byref(g1), ctypes.byref(e1), ctypes.byref(flag))
+                    for _ in range(2):
+                        assert lib.ormi_hip_gemm_pair(*args) == 0, lib.ormi_hip_last_error()
+                    grouped_by[(name, mode)] = flag.value
+                    ev.sync()
+                    t0, t1 = ev.new(), ev.new()
+                    ev.record(t0)
+                    for _ in range(n):
+                        lib.ormi_hip_gemm_pair(*args)
+                    ev.record(t1)
+                    best[(name, mode)] = min(best[(name, mode)], ev.elapsed_ms(t0, t1) / n * 1e3)
+    finally:
+        if saved is None:
+            os.environ.pop("ORMI_GEMM_PAIR", None)
+        else:
+            os.environ["ORMI_GEMM_PAIR"] = saved
+    lines = ["# Grouped GEMM pairs: one launch against two, by depth", "", f"Command (from the repo root): `{cmd}`", "",
+             "ormi_hip_gemm_pair on dX = dZ W^T (k-contiguous operands, gelu' in the store) and dW = X^T dZ "
+             "(mn-contiguous operands, SGD update in place), fp32. k-tiles/wg: the 32-deep k-tiles each of the "
+             f"{cus} work-groups streams when grouped. two = ORMI_GEMM_PAIR=0, one = 2, default = 1 (grouped only "
+             f"up to 48 k-tiles per work-group). Best of {rounds} interleaved rounds of {n} calls, HIP events.", "",
+             "| products | k-tiles/wg | two launches us | one launch us | one vs two | default us (grouped) |",
+             "|---|---|---|---|---|---|"]
+    for name, _, _, x, w in built:
+        tiles = (x[0] // 128) * (x[1] // 128) * (x[2] // 32) + (w[0] // 128) * (w[1] // 128) * (w[2] // 32)
+        groups = min(cus, (x[0] // 128) * (x[1] // 128) + (w[0] // 128) * (w[1] // 128))
+        two, one, dflt = best[(name, "0")], best[(name, "2")], best[(name, "1")]
+        lines.append(f"| {name} | {-(-tiles // groups)} | {two:.1f} | {one:.1f} | {one / two - 1:+.1%} | "
+                     f"{dflt:.1f} ({'yes' if grouped_by[(name, '1')] else 'no'}) |")
+        log(lines[-1])
+    for p in held:
+        lib.ormi_hip_free(p)
+    out_md.write_text("\n".join(lines) + "\n")
+    print(out_md.read_text())
+
+
 def torch_c5_step_ms(torch, steps: int) -> float:
     """The C5 step written in PyTorch on the same inputs as bench_c5 (seed 4):
     fp32 matmuls (hipBLASLt), erf GELU, MSE, autograd, SGD lr 1e-3. For the
@@ -1197,6 +1298,8 @@ def main():
                     help="summarize a rocprofv3 --kernel-trace run into per-kernel durations (no GPU needed); "
                          "--trace-cmd gives the command that made the run")
     ap.add_argument("--trace-cmd", default="", help="the rocprofv3 command recorded by --trace-report")
+    ap.add_argument("--gemm-pairs", metavar="OUT_MD",
+                    help="a layer's backward GEMM pair as one launch against two, by depth (markdown)")
     ap.add_argument("--mfma-ceiling", metavar="OUT_MD",
                     help="register-only MFMA loops: the matrix cores' sustained bf16 and fp32 rates (markdown)")
     ap.add_argument("--vendor-gemm", metavar="OUT_MD",
@@ -1213,6 +1316,9 @@ def main():
         return
     if args.mfma_ceiling:
         mfma_ceiling(Path(args.mfma_ceiling), f"python3 bench.py --mfma-ceiling {args.mfma_ceiling}")
+        return
+    if args.gemm_pairs:
+        gemm_pair_sweep(Path(args.gemm_pairs), f"python3 bench.py --gemm-pairs {args.gemm_pairs}")
         return
     if args.mfma_report:
         only = args.only or "c4"
