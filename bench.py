@@ -823,7 +823,7 @@ def gemm_pair_sweep(out_md: Path, cmd: str, rounds: int = 5, n: int = 20) -> Non
     mn-contiguous, the SGD update in place), at the C5 layer shapes over a range
     of depths and at C5's own layer-2 pair. ORMI_GEMM_PAIR=0 runs them as two
     launches, =2 as one whatever the depth; the default (1) groups pairs of at
-    most 48 k-tiles per work-group. Best of `rounds` interleaved rounds of n
+    most 64 k-tiles per work-group. Best of `rounds` interleaved rounds of n
     calls (HIP events)."""
     ev = Events()
     lib = ev.lib
@@ -897,11 +897,45 @@ def gemm_pair_sweep(out_md: Path, cmd: str, rounds: int = 5, n: int = 20) -> Non
             os.environ.pop("ORMI_GEMM_PAIR", None)
         else:
             os.environ["ORMI_GEMM_PAIR"] = saved
+    # Stream length alone: one launch over twice the tiles (two column halves of
+    # one product, so twice the tiles per work-group) against a launch per half.
+    lib.ormi_hip_gemm_ex.argtypes = [ctypes.POINTER(_GemmDesc), ctypes.POINTER(Epi)]
+    halves = []
+    for name, form, M, N, K in (("X^T dZ (mn-contiguous), 4096 x 8192, K 1024", "dw", 4096, 8192, 1024),
+                                ("dZ W^T (k-contiguous), 2048 x 4096, K 4096", "dx", 2048, 4096, 4096)):
+        if form == "dw":  # halves split N: B and C columns
+            A, B, C = put(rand(K, M)), put(rand(K, N)), put(np.zeros((M, N), np.float32))
+            whole = _GemmDesc(dtype=0, M=M, N=N, K=K, a=A, a_stride_m=1, a_stride_k=M, b=B, b_stride_k=N, b_stride_n=1, c=C)
+            parts = [_GemmDesc(dtype=0, M=M, N=N // 2, K=K, a=A, a_stride_m=1, a_stride_k=M,
+                               b=ctypes.c_void_p(B.value + h * (N // 2) * 4), b_stride_k=N, b_stride_n=1,
+                               c=put(np.zeros((M, N // 2), np.float32))) for h in (0, 1)]
+        else:  # halves split M: A rows and C rows
+            A, B, C = put(rand(M, K)), put(rand(N, K)), put(np.zeros((M, N), np.float32))
+            whole = _GemmDesc(dtype=0, M=M, N=N, K=K, a=A, a_stride_m=K, a_stride_k=1, b=B, b_stride_k=1, b_stride_n=K, c=C)
+            parts = [_GemmDesc(dtype=0, M=M // 2, N=N, K=K, a=ctypes.c_void_p(A.value + h * (M // 2) * K * 4),
+                               a_stride_m=K, a_stride_k=1, b=B, b_stride_k=1, b_stride_n=K,
+                               c=ctypes.c_void_p(C.value + h * (M // 2) * N * 4)) for h in (0, 1)]
+        halves.append((name, whole, parts, (M // 128) * (N // 128), K // 32))
+    hbest = collections.defaultdict(lambda: math.inf)
+    for r in range(rounds):
+        for name, whole, parts, _, _ in halves:
+            for which in (("one", "two") if r % 2 == 0 else ("two", "one")):
+                calls = [whole] if which == "one" else parts
+                for g in calls:
+                    assert lib.ormi_hip_gemm_ex(ctypes.byref(g), None) == 0, lib.ormi_hip_last_error()
+                ev.sync()
+                t0, t1 = ev.new(), ev.new()
+                ev.record(t0)
+                for _ in range(n):
+                    for g in calls:
+                        lib.ormi_hip_gemm_ex(ctypes.byref(g), None)
+                ev.record(t1)
+                hbest[(name, which)] = min(hbest[(name, which)], ev.elapsed_ms(t0, t1) / n * 1e3)
     lines = ["# Grouped GEMM pairs: one launch against two, by depth", "", f"Command (from the repo root): `{cmd}`", "",
              "ormi_hip_gemm_pair on dX = dZ W^T (k-contiguous operands, gelu' in the store) and dW = X^T dZ "
              "(mn-contiguous operands, SGD update in place), fp32. k-tiles/wg: the 32-deep k-tiles each of the "
              f"{cus} work-groups streams when grouped. two = ORMI_GEMM_PAIR=0, one = 2, default = 1 (grouped only "
-             f"up to 48 k-tiles per work-group). Best of {rounds} interleaved rounds of {n} calls, HIP events.", "",
+             f"up to 64 k-tiles per work-group). Best of {rounds} interleaved rounds of {n} calls, HIP events.", "",
              "| products | k-tiles/wg | two launches us | one launch us | one vs two | default us (grouped) |",
              "|---|---|---|---|---|---|"]
     for name, _, _, x, w in built:
@@ -910,6 +944,14 @@ def gemm_pair_sweep(out_md: Path, cmd: str, rounds: int = 5, n: int = 20) -> Non
         two, one, dflt = best[(name, "0")], best[(name, "2")], best[(name, "1")]
         lines.append(f"| {name} | {-(-tiles // groups)} | {two:.1f} | {one:.1f} | {one / two - 1:+.1%} | "
                      f"{dflt:.1f} ({'yes' if grouped_by[(name, '1')] else 'no'}) |")
+        log(lines[-1])
+    lines += ["", "Stream length alone, no epilogue, through ormi_hip_gemm_ex: one product over 2T whole tiles in one "
+              "launch (the persistent kernel, 2T / 256 tiles per work-group) against its two halves (T tiles each) in "
+              "two launches. Same operands, same flops, same kernel code.", "",
+              "| product | tiles | k-tiles per tile | one launch us | two launches us | one vs two |", "|---|---|---|---|---|---|"]
+    for name, _, _, tiles, kt in halves:
+        one, two = hbest[(name, "one")], hbest[(name, "two")]
+        lines.append(f"| {name} | {tiles} | {kt} | {one:.1f} | {two:.1f} | {one / two - 1:+.1%} |")
         log(lines[-1])
     for p in held:
         lib.ormi_hip_free(p)

@@ -245,9 +245,9 @@ int ormi_hip_gemm_ex_noalloc(const ormi_gemm_desc* desc, const ormi_gemm_epilogu
  * persistent launch whose work-groups take the first product's tiles, then the
  * second's, through one pipeline: the fill, the epilogue latency and the
  * last-wave tail are paid once instead of twice. That pays for shallow pairs
- * and costs for deep ones (a long persistent stream runs each k-tile slower),
- * so by default only pairs of at most 48 k-tiles (of 32) per work-group are
- * grouped. Otherwise the two run in order as their own calls would. *grouped
+ * (2-6% at up to 64 k-tiles of 32 per work-group) and not for deep ones, so by
+ * default only pairs of at most 64 k-tiles per work-group are grouped.
+ * Otherwise the two run in order as their own calls would. *grouped
  * (if not NULL) is set to 1 when they ran as one launch, else 0. Both
  * descriptors are checked before anything is launched: an invalid one returns
  * its error and launches nothing. ORMI_GEMM_PAIR=0 turns grouping off, =2

@@ -1601,14 +1601,12 @@ static int gemm_pair(const ormi_gemm_desc* d0, const ormi_gemm_epilogue* e0, con
         const int groups = (int)std::min<long long>(compute_units(), t0 + t1);
         // Grouping pays while each work-group's stream is short: one box, dX
         // (1024 x 4096, TT, gelu') with dW (4096 x 1024, FF, SGD), both at
-        // depth K, two launches -> one: K 64 28.2 -> 25.7 us, 128 36.1 -> 33.8,
-        // 256 50.8 -> 48.3, 512 79.2 -> 76.7 (32 k-tiles per work-group), but
-        // K 1024 136.7 -> 137.6 (64), and C5's layer-2 pair (256) 500.5 ->
-        // 515.8: a stream twice as long runs each k-tile slower (two 4-tile
-        // persistent launches of one product beat one 8-tile launch by 23 us).
+        // depth K, two launches -> one: K 64 28.0 -> 26.4 us, 256 50.6 ->
+        // 48.4, 512 79.1 -> 76.0, 1024 (64 k-tiles per work-group) 136.9 ->
+        // 134.2; C5's layer-2 pair (256 k-tiles per work-group) 499.8 -> 501.3.
         // So by default (1) only streams of at most kPairMaxKTiles k-tiles per
         // work-group are grouped; 2 groups every eligible pair.
-        constexpr long long kPairMaxKTiles = 48;
+        constexpr long long kPairMaxKTiles = 64;
         const long long per_group = (t0 * (p0.K / 32) + t1 * (p1.K / 32) + groups - 1) / groups;
         // The kernel takes the products in one order of layouts; independent
         // products may run in either.

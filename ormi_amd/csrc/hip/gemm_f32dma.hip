@@ -532,7 +532,9 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32dma_pair_kernel(GemmPa
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave / WGN, wn = wave % WGN;
     // Per-lane load offsets of each problem's layouts (whole tiles: independent
-    // of the tile), and the ones of the problem the load stream is in.
+    // of the tile). They never change: each stretch of the stream below loads
+    // with one problem's pair of them, so no per-lane value is reassigned in a
+    // loop (a reassigned one is copied between registers on every k-tile).
     typename St0::PlanA pa0;
     typename St0::PlanB pb0;
     typename St1::PlanA pa1;
@@ -541,40 +543,31 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32dma_pair_kernel(GemmPa
     pb0.init(p0.b_sn, p0.b_sk, 0, p0.N);
     pa1.init(p1.a_sm, p1.a_sk, 0, p1.M);
     pb1.init(p1.b_sn, p1.b_sk, 0, p1.N);
-    typename St0::PlanA la;
-    typename St0::PlanB lb;
     // Next k-tile of the stream to load: entry li, k-tile lkt of it, at ta /
-    // tb; it stays on the last one once the stream is exhausted.
-    int li = 0, lkt = 0, lkts = 0;
+    // tb; it stays on the last one once the stream is exhausted. All uniform.
+    int li = 0, lkt = 0;
     const char* ta;
     const char* tb;
-    long long a_step = 0, b_step = 0;
     auto set_load_tile = [&](int i) {
         int m0, n0;
         tile_origin(i, m0, n0);
-        const bool q = b + i * G >= T0;
-        if (!q) {
+        if (b + i * G < T0) {
             ta = p0.a + St0::PlanA::origin(p0.a_sm, p0.a_sk, m0, 0);
             tb = p0.b + St0::PlanB::origin(p0.b_sn, p0.b_sk, n0, 0);
-            a_step = St0::PlanA::kstep(p0.a_sk);
-            b_step = St0::PlanB::kstep(p0.b_sk);
         } else {
             ta = p1.a + St1::PlanA::origin(p1.a_sm, p1.a_sk, m0, 0);
             tb = p1.b + St1::PlanB::origin(p1.b_sn, p1.b_sk, n0, 0);
-            a_step = St1::PlanA::kstep(p1.a_sk);
-            b_step = St1::PlanB::kstep(p1.b_sk);
         }
-        lkts = pick(q, KT0, KT1);
-#pragma unroll
-        for (int s = 0; s < St0::PA; ++s) la.voff[s] = pick(q, pa0.voff[s], pa1.voff[s]);
-#pragma unroll
-        for (int s = 0; s < St0::PB; ++s) lb.voff[s] = pick(q, pb0.voff[s], pb1.voff[s]);
     };
-    auto advance = [&]() {
-        if (lkt + 1 < lkts) {
+    // One k-tile on, within the load stream's current problem Q (known where
+    // it is called, so its depth and steps are constants there), or on to the
+    // next entry, which may be the other problem's.
+    auto advance = [&](auto q_tag) __attribute__((always_inline)) {
+        constexpr int Q = decltype(q_tag)::value;
+        if (lkt + 1 < (Q ? KT1 : KT0)) {
             ++lkt;
-            ta += a_step;
-            tb += b_step;
+            ta += Q ? St1::PlanA::kstep(p1.a_sk) : St0::PlanA::kstep(p0.a_sk);
+            tb += Q ? St1::PlanB::kstep(p1.b_sk) : St0::PlanB::kstep(p0.b_sk);
         } else if (li + 1 < mine) {
             ++li;
             lkt = 0;
@@ -600,20 +593,29 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32dma_pair_kernel(GemmPa
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
     if (GT == 0) return;
 
+    // Prologue: k-tiles 0 .. STAGES-2, of either problem.
 #pragma unroll
     for (int s = 0; s < STAGES - 1; ++s) {
         const char* ua = uniform_ptr(ta);
         const char* ub = uniform_ptr(tb);
+        if (b + li * G < T0) {
 #pragma unroll
-        for (int d = 0; d < St0::PA; ++d) la.issue_one(lds + s * STAGE, ua, d);
+            for (int d = 0; d < St0::PA; ++d) pa0.issue_one(lds + s * STAGE, ua, d);
 #pragma unroll
-        for (int d = 0; d < St0::PB; ++d) lb.issue_one(lds + s * STAGE + A_BYTES, ub, d);
-        if (s + 1 < GT) advance();
+            for (int d = 0; d < St0::PB; ++d) pb0.issue_one(lds + s * STAGE + A_BYTES, ub, d);
+            if (s + 1 < GT) advance(FnConst<0>{});
+        } else {
+#pragma unroll
+            for (int d = 0; d < St1::PA; ++d) pa1.issue_one(lds + s * STAGE, ua, d);
+#pragma unroll
+            for (int d = 0; d < St1::PB; ++d) pb1.issue_one(lds + s * STAGE + A_BYTES, ub, d);
+            if (s + 1 < GT) advance(FnConst<1>{});
+        }
     }
     wait_vmcnt<(STAGES - 2) * PER_TILE>();
     lds_barrier();
     u32x4_t fa[2][TM], fb[2][TN];
-    // Fragments of k-step 0 of the k-tile in `stage`, in problem St's layouts.
+    // Fragments of k-step 0 of the k-tile in stage `at`, in problem St's layouts.
     auto first_frags = [&](auto st, int at) __attribute__((always_inline)) {
         using S = decltype(st);
         const lds_char* cur = lds + at * STAGE;
@@ -623,15 +625,16 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32dma_pair_kernel(GemmPa
         for (int j = 0; j < TN; ++j) fb[0][j] = frag32<BN, S::kBKC, BK>(cur + A_BYTES, wn * WTN + j * 32, 0);
     };
     int stage = 0, free_stage = STAGES - 1;
-    // The k-tiles [g_lo, g_hi) of the stream, all of problem St's tiles
-    // (entries i_lo, i_lo + 1, ...), each KT k-tiles deep; the epilogue kind EK
-    // and params p of that problem.
-    auto run = [&](auto st, auto ek, const GemmParams& p, float sv, long long g_lo, long long g_hi, int i_lo,
-                   int KT) __attribute__((always_inline)) {
+    // Compute-side position in the current problem: entry `tile`, k-tile kt,
+    // output origin (cm0, cn0).
+    int tile = 0, kt = 0, cm0 = 0, cn0 = 0;
+    // Stream steps [g_lo, g_hi): k-tiles of problem St (epilogue kind EK,
+    // params p, KT k-tiles per tile), loading problem LQ's k-tiles with its
+    // plans la / lb.
+    auto run = [&](auto st, auto ek, const GemmParams& p, float sv, int KT, auto lq, const auto& la, const auto& lb,
+                   long long g_lo, long long g_hi) __attribute__((always_inline)) {
         using St = decltype(st);
         constexpr int EK = decltype(ek)::value;
-        int tile = i_lo, kt = 0, cm0, cn0;
-        tile_origin(tile, cm0, cn0);
         for (long long g = g_lo; g < g_hi; ++g) {
             const int next = stage + 1 == STAGES ? 0 : stage + 1;
             const lds_char* cur = lds + stage * STAGE;
@@ -643,7 +646,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32dma_pair_kernel(GemmPa
             lds_barrier();
             St::template run<KS - 1>(acc, fa[1], fb[1], fa[0], fb[0], lds + next * STAGE, 0, wm, wn, fs, ua, ub, la, lb);
             asm volatile("" ::: "memory");
-            if (g + STAGES < GT) advance();
+            if (g + STAGES < GT) advance(lq);
             stage = next;
             free_stage = free_stage + 1 == STAGES ? 0 : free_stage + 1;
             if (++kt == KT) {
@@ -672,20 +675,27 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32dma_pair_kernel(GemmPa
 #pragma unroll
                         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
                 kt = 0;
-                if (g + 1 < g_hi) tile_origin(++tile, cm0, cn0);
+                if (++tile < mine) tile_origin(tile, cm0, cn0);
             }
         }
     };
+    // Step g loads k-tile min(g + STAGES - 1, GT - 1): from g1 on, problem 1's.
+    const long long g1 = GT > GT0 ? max(0LL, GT0 - (STAGES - 1)) : GT0;
     if (GT0 > 0) {
         first_frags(St0{}, 0);
-        run(St0{}, FnConst<EK0>{}, p0, sv0, 0, GT0, 0, KT0);
+        tile_origin(0, cm0, cn0);
+        run(St0{}, FnConst<EK0>{}, p0, sv0, KT0, FnConst<0>{}, pa0, pb0, 0, g1);
+        run(St0{}, FnConst<EK0>{}, p0, sv0, KT0, FnConst<1>{}, pa1, pb1, g1, GT0);
     }
     if (GT > GT0) {
         // The last problem-0 step read k-step 0 of this k-tile in problem 0's
         // layouts; the k-tile has landed (the barrier before that step), so
         // read it again in problem 1's.
         first_frags(St1{}, stage);
-        run(St1{}, FnConst<EK1>{}, p1, sv1, GT0, GT, mine0, KT1);
+        tile = mine0;
+        kt = 0;
+        tile_origin(tile, cm0, cn0);
+        run(St1{}, FnConst<EK1>{}, p1, sv1, KT1, FnConst<1>{}, pa1, pb1, GT0, GT);
     }
     // No load may still be writing this workgroup's LDS when it exits.
     wait_vmcnt<0>();

@@ -14,7 +14,7 @@ compared BIT FOR BIT with ormi_hip_gemm_ex on each descriptor in turn, over:
 and the calls that must NOT group (a product with fewer tiles than compute
 units, one product reading the other's output, an activation epilogue,
 layouts the kernel is not built for, ORMI_GEMM_PAIR=0, and by default a pair
-deeper than 48 k-tiles per work-group, such as C5's): those run as two calls
+deeper than 64 k-tiles per work-group, such as C5's layer 2): those run as two calls
 in order, which for the dependent pair means the second reads the first's
 result. ORMI_GEMM_PAIR=2 groups the deep pairs too, which is how the kernel is
 checked at C5's shapes. An invalid descriptor launches nothing. The products themselves are
@@ -216,10 +216,10 @@ def test_uneven_tile_counts_and_either_order(dev, shape, order):
     check_rows(pw, got[0] if pw is p0 else got[1])
 
 
-@pytest.mark.parametrize("K,grouped", [(256, 1), (512, 1), (1024, 0)])
+@pytest.mark.parametrize("K,grouped", [(256, 1), (1024, 1), (2048, 0)])
 def test_default_groups_shallow_pairs_only(dev, K, grouped):
     """ORMI_GEMM_PAIR unset: the C5 layer-3 shapes at depth K group while each
-    work-group's stream is at most 48 k-tiles (2 x K / 32), and run as two
+    work-group's stream is at most 64 k-tiles (2 x K / 32), and run as two
     calls beyond; the results are the same bits either way."""
     os.environ.pop("ORMI_GEMM_PAIR", None)
     rng = np.random.default_rng(K)
@@ -340,13 +340,13 @@ def test_scheduler_pairs_each_layers_backward_products(cabi, hip):
     """C5 at config size: the scheduler offers dZ2 = (dY W3^T) gelu'(Z2) with
     W3 - lr H2^T dY, and dZ1 with W2 - lr H1^T dZ2 (W1's update has no partner
     left). Grouped on request (ORMI_GEMM_PAIR=2) they are two launches per
-    step; by default they are too deep to group (64 and 256 k-tiles per
-    work-group) and run as two calls each. No bit of the step's results
-    changes: weights and loss equal those with ORMI_GEMM_PAIR=0."""
+    step; by default layer 3's pair (64 k-tiles per work-group) is grouped and
+    layer 2's (256) runs as two calls. No bit of the step's results changes:
+    weights and loss equal those with ORMI_GEMM_PAIR=0."""
     w2, l2, pairs2 = with_pair_mode("2", lambda: c5_step("hip"))
     assert pairs2 == 2, pairs2
     w1, l1, pairs1 = with_pair_mode(None, lambda: c5_step("hip"))
-    assert pairs1 == 0, pairs1
+    assert pairs1 == 1, pairs1
     w0, l0, pairs0 = with_pair_mode("0", lambda: c5_step("hip"))
     assert pairs0 == 0
     for a, b, c in zip(w2, w1, w0):
