@@ -74,6 +74,27 @@ namespace ormi::hip {
         return n.op != OpEnum::CAST || cast_target_is_float(n);
     }
 
+    size_t region_size(const NodePtr& root, size_t limit);
+
+    // A scalar seen through views: n is an unrealized view (a broadcast, a
+    // reshape, ...) whose source, down its chain of unrealized views, is an
+    // unrealized element-wise node of ONE element with a region of at most
+    // kMaxScalarRegion ops. Every element of n is that scalar, and its region
+    // reads only one-element operands (an element-wise op does not reduce), which
+    // a kernel of any shape reads with stride 0: so a consumer's kernel
+    // evaluates it itself instead of realizing it first, a kernel of one
+    // element (the loss's seed times its scale in a backward pass, before the
+    // broadcast to the loss's input). Returns the source, or nullptr.
+    constexpr size_t kMaxScalarRegion = 16;
+    static const NodePtr* scalar_view_source(const NodePtr& n) {
+        if (n->is_realized() || !is_view_op(n->op) || n->parents.empty()) return nullptr;
+        const NodePtr* src = &n->parents[0];
+        while (!(*src)->is_realized() && is_view_op((*src)->op) && !(*src)->parents.empty()) src = &(*src)->parents[0];
+        const Node& s = **src;
+        if (s.is_realized() || !fusible_interior(s) || shape_numel(s.view.shape) != 1) return nullptr;
+        return region_size(*src, kMaxScalarRegion) <= kMaxScalarRegion ? src : nullptr;
+    }
+
     std::vector<NodePtr> region_frontier(const NodePtr& root) {
         std::vector<NodePtr> frontier;
         SmallSet<Node> seen;
@@ -92,6 +113,11 @@ namespace ormi::hip {
                 if (fusible_interior(*p) && interior < kMaxRegion) {
                     stack.push_back(p.get());
                     ++interior;
+                } else if (const NodePtr* src = interior < kMaxRegion ? scalar_view_source(p) : nullptr) {
+                    if (seen.insert(src->get())) {
+                        stack.push_back(src->get());
+                        ++interior;
+                    }
                 } else {
                     frontier.push_back(p);
                 }
@@ -111,8 +137,16 @@ namespace ormi::hip {
             Node* n = stack.back();
             stack.pop_back();
             for (const auto& p : n->parents) {
-                if (!seen.insert(p.get()) || p->is_realized() || !fusible_interior(*p)) continue;
-                stack.push_back(p.get());
+                if (!seen.insert(p.get()) || p->is_realized()) continue;
+                Node* q = p.get();
+                if (!fusible_interior(*p)) {
+                    // A scalar seen through views counts with its own region
+                    // (whose size the source check bounds).
+                    const NodePtr* src = limit > kMaxScalarRegion ? scalar_view_source(p) : nullptr;
+                    if (!src || !seen.insert(src->get())) continue;
+                    q = src->get();
+                }
+                stack.push_back(q);
                 ++interior;
             }
         }
@@ -180,6 +214,8 @@ namespace ormi::hip {
         }
         SmallVec<Node*, 64> interior_post;
         SmallSet<Node> on_stack;
+        // Views read as the scalar they broadcast: the view's value is its source's.
+        SmallMap<Node, Node*> through;
         for (const auto& root : roots) {
             if (!is_interior(root.get())) throw std::runtime_error("HIP codegen: a grouped root is not an element-wise node.");
             if (value_of.find(root.get())) continue;  // inside an earlier root's region
@@ -189,10 +225,17 @@ namespace ormi::hip {
                 Frame& f = stack.back();
                 if (f.next < f.n->parents.size()) {
                     const NodePtr& p = f.n->parents[f.next++];
-                    if (value_of.find(p.get()) || on_stack.contains(p.get())) continue;
+                    if (value_of.find(p.get()) || on_stack.contains(p.get()) || through.find(p.get())) continue;
                     if (!p->is_realized() && is_interior(p.get())) {
                         on_stack.insert(p.get());
                         stack.push_back({p.get(), 0});
+                    } else if (const NodePtr* src = scalar_view_source(p)) {
+                        through.insert(p.get(), src->get());
+                        Node* q = src->get();
+                        if (!value_of.find(q) && !on_stack.contains(q)) {
+                            on_stack.insert(q);
+                            stack.push_back({q, 0});
+                        }
                     } else {
                         if (!p->is_realized()) throw std::runtime_error("HIP codegen: region input was not realized first.");
                         visit_leaf(p);
@@ -209,6 +252,7 @@ namespace ormi::hip {
         const int nleaves = (int)e.leaves.size();
         for (size_t k = 0; k < interior_post.size(); ++k) value_of.set(interior_post[k], nleaves + (int)k);
         auto id_of = [&](const Node* n) {
+            if (Node* const* q = through.find(n)) n = *q;
             const int* v = value_of.find(n);
             if (!v) throw std::runtime_error("HIP codegen: operand without a value.");
             return *v;
