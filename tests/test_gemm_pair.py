@@ -387,3 +387,28 @@ def test_scheduler_groups_a_shallow_pair_by_default(cabi, hip):
     for a, b in zip(got, want):
         np.testing.assert_array_equal(a, b)
     np.testing.assert_array_equal(l1, l0)
+
+
+def test_empty_and_zero_depth_products_run_alone(dev):
+    """A product with no elements launches nothing and its partner runs as its
+    own call; a product of depth 0 (C = 0 through its epilogue) is not
+    eligible, so the two run in order; a null descriptor is an error."""
+    rng = np.random.default_rng(11)
+    p1 = Problem(dev, rng, "dw", 4096, 1024, 256, ADD)
+    empty = Problem(dev, rng, "dx", 128, 128, 64)
+    empty.desc.M = 0
+    p1.reset()
+    assert run_pair(dev, empty, p1) == 0
+    got = p1.result()
+    p1.reset()
+    run_each(dev, p1)
+    np.testing.assert_array_equal(got, p1.result())
+
+    z = Problem(dev, rng, "dx", 1024, 4096, 64, MUL_FN_D)
+    z.desc.K = 0  # the product is 0: C = 0 * gelu'(D)
+    z.reset(), p1.reset()
+    assert run_pair(dev, z, p1) == 0
+    np.testing.assert_array_equal(z.result(), np.zeros((1024, 4096), np.float32) * 0)
+    grouped = ctypes.c_int(-1)
+    rc = dev.lib.ormi_hip_gemm_pair(None, None, ctypes.byref(p1.desc), ctypes.byref(p1.epi), ctypes.byref(grouped))
+    assert rc != 0 and b"null descriptor" in dev.lib.ormi_hip_last_error()

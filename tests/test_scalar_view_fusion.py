@@ -107,3 +107,34 @@ def test_scalar_chain_matches_the_realized_scalar(ob, hip):
     s = scalar().realize()  # the unfused path: the scalar's own kernel, then the product
     want = (X * s.reshape((1, 1)).expand((512, 256))).numpy()
     np.testing.assert_array_equal(bits(got), bits(want))
+
+
+@pytest.mark.gpu
+def test_scalar_view_in_a_reduction_prologue_and_a_grouped_realize(ob, hip):
+    """The scalar is also evaluated inside a reduction's prologue (one kernel for
+    sum(x * s) over rows) and inside a multi-output kernel of realize_all."""
+    from ormi_amd import realize_all
+
+    rng = np.random.default_rng(4)
+    x = rng.normal(0, 1, (256, 1024)).astype(np.float32)
+    X = T(x, hip)
+    a = T(np.float32(1.5), hip)
+
+    def view():
+        return (a * 0.5 - 0.25).reshape((1, 1)).expand((256, 1024))
+
+    red = (X * view()).sum(1)
+    plan = ob._plan_kernel(red._node)
+    before = ob._kernel_launches()
+    got = red.numpy()
+    assert ob._kernel_launches() - before == (2 if plan["two_pass"] else 1)
+    s = (a * 0.5 - 0.25).realize()
+    want = (X * s.reshape((1, 1)).expand((256, 1024))).sum(1).numpy()
+    np.testing.assert_array_equal(bits(got), bits(want))
+
+    u, v = X * view(), X + view()
+    before = ob._kernel_launches()
+    realize_all(u, v)
+    assert ob._kernel_launches() - before == 1
+    np.testing.assert_array_equal(bits(u.numpy()), bits(x * np.float32(0.5)))
+    np.testing.assert_array_equal(bits(v.numpy()), bits(x + np.float32(0.5)))
