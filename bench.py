@@ -257,7 +257,54 @@ def cpu_baselines_extra() -> dict:
                  "sgemm_2048x1024x4096_ms": round(t32 * 1e3, 1),
                  "sgemm_2048x1024x4096_TFLOP/s": round(2 * 2048 * 1024 * 4096 / t32 / 1e12, 3),
                  "sample": "full shapes; the bf16 config as sgemm on fp32 values"}
+    out["C5"] = cpu_c5_step(threads, lib, timed)
     return out
+
+
+def cpu_c5_step(threads, lib: str, timed) -> dict:
+    """The C5 step in numpy float32 on the host: the same seed-4 inputs, the
+    eight GEMMs (numpy matmul on its bundled OpenBLAS, all host threads, for the
+    reference's cblas_sgemm), erf GELU and its derivative, the MSE and the SGD
+    update, as whole-array numpy passes (the reference's CPU element-wise path
+    is one unthreaded kernel per node, slower still)."""
+    from scipy.special import erf
+
+    rng = np.random.default_rng(4)
+    dims = [1024, 4096, 4096, 1024]
+    X = rng.normal(0, 1, (1024, 1024)).astype(np.float32)
+    T = rng.normal(0, 1, (1024, 1024)).astype(np.float32)
+    W = [rng.uniform(-math.sqrt(6 / i), math.sqrt(6 / i), (i, o)).astype(np.float32) for i, o in zip(dims, dims[1:])]
+    r2, c = np.float32(1 / math.sqrt(2)), np.float32(1.0 / (1024 * 1024))
+    inv_sqrt_2pi = np.float32(1 / math.sqrt(2 * math.pi))
+
+    def gelu(z):
+        return np.float32(0.5) * z * (np.float32(1) + erf(z * r2).astype(np.float32))
+
+    def gelu_grad(z):
+        return (np.float32(0.5) * (np.float32(1) + erf(z * r2).astype(np.float32))
+                + z * inv_sqrt_2pi * np.exp(np.float32(-0.5) * z * z))
+
+    def step():
+        z1 = X @ W[0]
+        h1 = gelu(z1)
+        z2 = h1 @ W[1]
+        h2 = gelu(z2)
+        y = h2 @ W[2]
+        d = y - T
+        loss = float((d * d).sum()) * float(c)
+        dy = c * d + c * d
+        dw3 = h2.T @ dy
+        dz2 = (dy @ W[2].T) * gelu_grad(z2)
+        dw2 = h1.T @ dz2
+        dz1 = (dz2 @ W[1].T) * gelu_grad(z1)
+        dw1 = X.T @ dz1
+        return loss, [w - dw * np.float32(1e-3) for w, dw in zip(W, (dw1, dw2, dw3))]
+
+    t = timed(step, 2)
+    flops = 146028888064
+    return {"kind": "stand-in: numpy float32 (matmul on its OpenBLAS, element-wise as whole-array passes)",
+            "cores": threads, "blas": lib, "step_ms": round(t * 1e3, 1),
+            "gemm_TFLOP/s": round(flops / t / 1e12, 3), "sample": "full step, batch 1024, 1024-4096-4096-1024"}
 
 
 def traffic_from_profile(label: str):
