@@ -703,6 +703,144 @@ extern "C" __global__ __launch_bounds__(256) void ormi_mfma_probe_f32(float* out
 """
 
 
+HBM_PROBE_SRC = r"""
+typedef float f4 __attribute__((ext_vector_type(4)));
+// Block b reads chunk b (ch float4), 4 loads per thread in flight.
+extern "C" __global__ __launch_bounds__(256) void ormi_hbm_read_chunk(const f4* __restrict__ x, long long n4,
+                                                                      long long ch, float* out) {
+    float acc = 0.f;
+    const long long base = (long long)blockIdx.x * ch;
+    for (long long i = threadIdx.x; i < ch; i += 1024) {
+        f4 v[4];
+        for (int u = 0; u < 4; ++u) {
+            const long long j = base + i + u * 256;
+            v[u] = (i + u * 256 < ch && j < n4) ? x[j] : f4{0.f, 0.f, 0.f, 0.f};
+        }
+        for (int u = 0; u < 4; ++u) acc += v[u].x + v[u].y + v[u].z + v[u].w;
+    }
+    if (acc == 12345.678f) out[0] = acc;  // keeps the loads; never true for the zeroed input
+}
+// Grid stride, one load per thread per iteration.
+extern "C" __global__ __launch_bounds__(256) void ormi_hbm_read_stride(const f4* __restrict__ x, long long n4,
+                                                                       float* out) {
+    float acc = 0.f;
+    const long long n = (long long)gridDim.x * 256;
+    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n4; i += n) {
+        const f4 v = x[i];
+        acc += v.x + v.y + v.z + v.w;
+    }
+    if (acc == 12345.678f) out[0] = acc;
+}
+// Grid stride copy with non-temporal stores (the element-wise kernels' stores).
+extern "C" __global__ __launch_bounds__(256) void ormi_hbm_copy(f4* __restrict__ y, const f4* __restrict__ x,
+                                                                long long n4) {
+    const long long n = (long long)gridDim.x * 256;
+    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n4; i += n)
+        __builtin_nontemporal_store(x[i], y + i);
+}
+// Grid stride, non-temporal stores only.
+extern "C" __global__ __launch_bounds__(256) void ormi_hbm_write(f4* __restrict__ y, long long n4) {
+    const long long n = (long long)gridDim.x * 256;
+    const f4 z = {1.f, 2.f, 3.f, 4.f};
+    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n4; i += n) __builtin_nontemporal_store(z, y + i);
+}
+"""
+
+
+def hbm_ceiling(out_md: Path, cmd: str, rounds: int = 7, n: int = 10) -> None:
+    """What HBM streams sustain on this card: plain read, copy and write kernels
+    over memory the 256 MB Infinity Cache does not hold, compiled and launched
+    through libormi_hip's hipRTC entry points, HIP events, median of `rounds`
+    sets of n launches after 8 untimed. The ceilings C2 (a copy's traffic) and
+    C3 (reads) are compared with. Writes a markdown table to out_md."""
+    ev = Events()
+    lib = ev.lib
+    lib.ormi_hip_last_error.restype = ctypes.c_char_p
+    lib.ormi_hip_rtc_compile.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p), ctypes.c_int,
+                                         ctypes.POINTER(ctypes.c_uint64)]
+    lib.ormi_hip_launch.argtypes = [ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint32),
+                                    ctypes.c_uint32, ctypes.POINTER(ctypes.c_void_p)]
+    lib.ormi_hip_malloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
+    lib.ormi_hip_free.argtypes = [ctypes.c_void_p]
+    lib.ormi_hip_memset_d32.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_size_t]
+    assert lib.ormi_hip_init(0) == 0
+    props = _Props()
+    assert lib.ormi_hip_get_props(ctypes.byref(props)) == 0
+    cus = props.compute_units
+    # One 2 GiB buffer in eight 256 MiB slices; launches rotate over four slice
+    # sets, so each touches memory last used 1.5 GiB of traffic earlier (the
+    # Infinity Cache holds none of it).
+    slice_b = 256 << 20
+    base = ctypes.c_void_p()
+    assert lib.ormi_hip_malloc(ctypes.byref(base), 8 * slice_b) == 0, lib.ormi_hip_last_error()
+    assert lib.ormi_hip_memset_d32(base, 0, 8 * slice_b // 4) == 0
+    out = ctypes.c_void_p()
+    assert lib.ormi_hip_malloc(ctypes.byref(out), 4) == 0
+
+    def at(k):
+        return ctypes.c_void_p(base.value + k * slice_b)
+
+    handles = {}
+    for name in ("ormi_hbm_read_chunk", "ormi_hbm_read_stride", "ormi_hbm_copy", "ormi_hbm_write"):
+        h = ctypes.c_uint64()
+        if lib.ormi_hip_rtc_compile(HBM_PROBE_SRC.encode(), name.encode(), None, 0, ctypes.byref(h)) != 0:
+            raise SystemExit("hbm probe: " + lib.ormi_hip_last_error().decode())
+        handles[name] = h.value
+    n4_two, n4_one = 2 * slice_b // 16, slice_b // 16
+    chunk = 8192 // 16  # 8 KB per block: the row reductions' segment
+    keep = []
+
+    def argv(*vals):
+        cs = [v if isinstance(v, ctypes.c_void_p) else ctypes.c_longlong(v) for v in vals]
+        keep.append(cs)
+        return (ctypes.c_void_p * len(cs))(*[ctypes.addressof(c) for c in cs])
+
+    # (label, kernel, grid, one argument set per rotation step, bytes per launch)
+    cases = [
+        ("read 512 MiB, 8 KB per work-group, 4 loads in flight per thread", "ormi_hbm_read_chunk", n4_two // chunk,
+         [argv(at(2 * r), n4_two, chunk, out) for r in range(4)], 2 * slice_b),
+        (f"read 512 MiB, grid stride over {16 * cus} work-groups", "ormi_hbm_read_stride", 16 * cus,
+         [argv(at(2 * r), n4_two, out) for r in range(4)], 2 * slice_b),
+        (f"copy 256 MiB to 256 MiB, non-temporal stores, {64 * cus} work-groups", "ormi_hbm_copy", 64 * cus,
+         [argv(at(4 + r), at(r), n4_one) for r in range(4)], 2 * slice_b),
+        (f"write 512 MiB, non-temporal stores, {64 * cus} work-groups", "ormi_hbm_write", 64 * cus,
+         [argv(at(2 * r), n4_two) for r in range(4)], 2 * slice_b),
+    ]
+    rows = []
+    for label, kname, grid_x, arg_sets, nbytes in cases:
+        grid = (ctypes.c_uint32 * 3)(grid_x, 1, 1)
+        block = (ctypes.c_uint32 * 3)(256, 1, 1)
+        for i in range(8):
+            assert lib.ormi_hip_launch(handles[kname], grid, block, 0, arg_sets[i % 4]) == 0, lib.ormi_hip_last_error()
+        ev.sync()
+        times = []
+        for _ in range(rounds):
+            e0, e1 = ev.new(), ev.new()
+            ev.record(e0)
+            for i in range(n):
+                lib.ormi_hip_launch(handles[kname], grid, block, 0, arg_sets[i % 4])
+            ev.record(e1)
+            ev.sync()
+            times.append(ev.elapsed_ms(e0, e1) / n)
+        t = sorted(times)[rounds // 2]
+        tbs = nbytes / (t * 1e-3) / 1e12
+        rows.append(f"| {label} | {nbytes / 2**20:.0f} | {t * 1e3:.1f} | {tbs:.2f} | {tbs / (HBM_PEAK_GBS / 1000):.1%} |")
+        log(rows[-1])
+    bufs = [base]
+    for p in bufs + [out]:
+        lib.ormi_hip_free(p)
+    lines = ["# HBM stream ceilings (plain read, copy and write kernels)", "", f"Command (from the repo root): `{cmd}`", "",
+             "Kernels (`HBM_PROBE_SRC` in bench.py) compiled and launched through libormi_hip's hipRTC entry points, "
+             "128-bit accesses, 512 MiB moved per launch, launches rotating over four slice sets of one 2 GiB buffer "
+             "(each launch touches memory last used 1.5 GiB of traffic earlier, so the 256 MB Infinity Cache serves "
+             f"none of it), HIP events, median of {rounds} sets of {n} launches after 8 untimed. These are what the "
+             "card's HBM streams sustain with plain kernels; the element-wise and reduction kernels are measured "
+             "against them.", "",
+             "| kernel | MiB moved | us | TB/s | of 8 TB/s |", "|---|---|---|---|---|"] + rows
+    out_md.write_text("\n".join(lines) + "\n")
+    print(out_md.read_text())
+
+
 def mfma_probe_values(seed: int = 7) -> np.ndarray:
     """8 x 512 operand words, each two bf16 of N(0, 1/64) values (the statistics
     of the C4 inputs); read as fp32, a word is about its upper value."""
@@ -1387,6 +1525,8 @@ def main():
                     help="summarize a rocprofv3 --kernel-trace run into per-kernel durations (no GPU needed); "
                          "--trace-cmd gives the command that made the run")
     ap.add_argument("--trace-cmd", default="", help="the rocprofv3 command recorded by --trace-report")
+    ap.add_argument("--hbm-ceiling", metavar="OUT_MD",
+                    help="plain read, copy and write kernels: what the card's HBM streams sustain (markdown)")
     ap.add_argument("--gemm-pairs", metavar="OUT_MD",
                     help="a layer's backward GEMM pair as one launch against two, by depth (markdown)")
     ap.add_argument("--mfma-ceiling", metavar="OUT_MD",
@@ -1405,6 +1545,9 @@ def main():
         return
     if args.mfma_ceiling:
         mfma_ceiling(Path(args.mfma_ceiling), f"python3 bench.py --mfma-ceiling {args.mfma_ceiling}")
+        return
+    if args.hbm_ceiling:
+        hbm_ceiling(Path(args.hbm_ceiling), f"python3 bench.py --hbm-ceiling {args.hbm_ceiling}")
         return
     if args.gemm_pairs:
         gemm_pair_sweep(Path(args.gemm_pairs), f"python3 bench.py --gemm-pairs {args.gemm_pairs}")
