@@ -412,3 +412,62 @@ def test_empty_and_zero_depth_products_run_alone(dev):
     grouped = ctypes.c_int(-1)
     rc = dev.lib.ormi_hip_gemm_pair(None, None, ctypes.byref(p1.desc), ctypes.byref(p1.epi), ctypes.byref(grouped))
     assert rc != 0 and b"null descriptor" in dev.lib.ormi_hip_last_error()
+
+
+def random_net_step(dev, seed):
+    """A random MLP step at widths where the backward products can pair
+    (1024-4096 wide, batch 1024 or 2048): random activations, biases and loss,
+    updates and loss realized together. Returns the new parameters, the loss
+    and the step's grouped launches."""
+    import math
+
+    from ormi_amd import Tensor, realize_all
+    from ormi_amd import ormi_backend as ob
+
+    rng = np.random.default_rng(700 + seed)
+    L = int(rng.integers(2, 4))
+    dims = [int(rng.choice([1024, 2048, 4096])) for _ in range(L + 1)]
+    n = int(rng.choice([1024, 2048]))
+    acts = [str(rng.choice(["none", "relu", "tanh", "gelu"])) for _ in range(L)]
+    X = Tensor(rng.standard_normal((n, dims[0])).astype(np.float32), dev)
+    Y = Tensor(rng.standard_normal((n, dims[-1])).astype(np.float32), dev)
+    Ws = [Tensor((rng.standard_normal((i, o)) / math.sqrt(i)).astype(np.float32), dev, requires_grad=True)
+          for i, o in zip(dims, dims[1:])]
+    bs = [Tensor(rng.standard_normal(o).astype(np.float32) * 0.1, dev, requires_grad=True) if rng.random() < 0.3 else None
+          for o in dims[1:]]
+    h = X
+    for W, b, act in zip(Ws, bs, acts):
+        h = h @ W
+        if b is not None:
+            h = h + b
+        if act != "none":
+            h = getattr(h, act)()
+    if rng.random() < 0.5:
+        d = h - Y
+        loss = (d * d).sum() * (1.0 / (n * dims[-1]))
+    else:
+        loss = (h * Y).sum() * 0.5
+    loss.backward()
+    params = Ws + [b for b in bs if b is not None]
+    ups = [p - p.grad * 1e-3 for p in params]
+    order = [int(i) for i in rng.permutation(len(ups))]
+    before = ob.gemm_pair_count()
+    realize_all(*[ups[i] for i in order], loss)
+    pairs = ob.gemm_pair_count() - before
+    out = [u.numpy() for u in ups] + [loss.numpy()]
+    loss.zero_grad_graph()
+    return out, pairs
+
+
+def test_random_networks_pair_bit_identically(cabi, hip):
+    """Six random networks: with every eligible pair grouped (ORMI_GEMM_PAIR=2)
+    the parameters and loss are the same bits as with none (0); pairs form."""
+    total = 0
+    for seed in range(6):
+        got, pairs = with_pair_mode("2", lambda: random_net_step("hip", seed))
+        want, none = with_pair_mode("0", lambda: random_net_step("hip", seed))
+        assert none == 0
+        total += pairs
+        for a, b in zip(got, want):
+            np.testing.assert_array_equal(np.atleast_1d(a).view(np.uint32), np.atleast_1d(b).view(np.uint32))
+    assert total > 0
