@@ -471,3 +471,37 @@ def test_random_networks_pair_bit_identically(cabi, hip):
         for a, b in zip(got, want):
             np.testing.assert_array_equal(np.atleast_1d(a).view(np.uint32), np.atleast_1d(b).view(np.uint32))
     assert total > 0
+
+
+def test_bf16_products_run_as_two_calls(dev):
+    """The pair kernel is fp32: two bf16 products (fp32 output) are not grouped
+    and give exactly what two ormi_hip_gemm_ex calls give."""
+    rng = np.random.default_rng(13)
+
+    def bf16(x):
+        b = np.ascontiguousarray(x, np.float32).view(np.uint32)
+        return ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)  # round to nearest even
+
+    def put16(x):
+        h = bf16(x)
+        p = ctypes.c_void_p()
+        assert dev.lib.ormi_hip_malloc(ctypes.byref(p), h.nbytes) == 0
+        assert dev.lib.ormi_hip_memcpy_h2d(p, h.ctypes.data, h.nbytes) == 0
+        dev.bufs.append(p)
+        return p
+
+    descs = []
+    for M, N, K in ((2048, 2048, 256), (2048, 2048, 512)):
+        d = GemmDesc(dtype=3, M=M, N=N, K=K, a=put16(rng.standard_normal((M, K))), a_stride_m=K, a_stride_k=1,
+                     b=put16(rng.standard_normal((K, N))), b_stride_k=N, b_stride_n=1,
+                     c=dev.put(np.zeros((M, N), np.float32)))
+        descs.append(d)
+    grouped = ctypes.c_int(-1)
+    assert dev.lib.ormi_hip_gemm_pair(ctypes.byref(descs[0]), None, ctypes.byref(descs[1]), None,
+                                      ctypes.byref(grouped)) == 0, dev.lib.ormi_hip_last_error()
+    assert grouped.value == 0
+    got = [dev.get(d.c, (d.M, d.N)) for d in descs]
+    for d in descs:
+        assert dev.lib.ormi_hip_gemm_ex(ctypes.byref(d), None) == 0
+    for g, d in zip(got, descs):
+        np.testing.assert_array_equal(g, dev.get(d.c, (d.M, d.N)))
