@@ -731,6 +731,21 @@ extern "C" __global__ __launch_bounds__(256) void ormi_hbm_read_stride(const f4*
     }
     if (acc == 12345.678f) out[0] = acc;
 }
+// The same with non-temporal loads.
+extern "C" __global__ __launch_bounds__(256) void ormi_hbm_read_chunk_nt(const f4* __restrict__ x, long long n4,
+                                                                         long long ch, float* out) {
+    float acc = 0.f;
+    const long long base = (long long)blockIdx.x * ch;
+    for (long long i = threadIdx.x; i < ch; i += 1024) {
+        f4 v[4];
+        for (int u = 0; u < 4; ++u) {
+            const long long j = base + i + u * 256;
+            v[u] = (i + u * 256 < ch && j < n4) ? __builtin_nontemporal_load(x + j) : f4{0.f, 0.f, 0.f, 0.f};
+        }
+        for (int u = 0; u < 4; ++u) acc += v[u].x + v[u].y + v[u].z + v[u].w;
+    }
+    if (acc == 12345.678f) out[0] = acc;
+}
 // Grid stride copy with non-temporal stores (the element-wise kernels' stores).
 extern "C" __global__ __launch_bounds__(256) void ormi_hbm_copy(f4* __restrict__ y, const f4* __restrict__ x,
                                                                 long long n4) {
@@ -738,11 +753,24 @@ extern "C" __global__ __launch_bounds__(256) void ormi_hbm_copy(f4* __restrict__
     for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n4; i += n)
         __builtin_nontemporal_store(x[i], y + i);
 }
+// The same with non-temporal loads (the element-wise kernels' loads of large read-once operands).
+extern "C" __global__ __launch_bounds__(256) void ormi_hbm_copy_nt(f4* __restrict__ y, const f4* __restrict__ x,
+                                                                   long long n4) {
+    const long long n = (long long)gridDim.x * 256;
+    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n4; i += n)
+        __builtin_nontemporal_store(__builtin_nontemporal_load(x + i), y + i);
+}
 // Grid stride, non-temporal stores only.
 extern "C" __global__ __launch_bounds__(256) void ormi_hbm_write(f4* __restrict__ y, long long n4) {
     const long long n = (long long)gridDim.x * 256;
     const f4 z = {1.f, 2.f, 3.f, 4.f};
     for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n4; i += n) __builtin_nontemporal_store(z, y + i);
+}
+// Grid stride, plain stores.
+extern "C" __global__ __launch_bounds__(256) void ormi_hbm_write_plain(f4* __restrict__ y, long long n4) {
+    const long long n = (long long)gridDim.x * 256;
+    const f4 z = {1.f, 2.f, 3.f, 4.f};
+    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n4; i += n) y[i] = z;
 }
 """
 
@@ -781,7 +809,8 @@ def hbm_ceiling(out_md: Path, cmd: str, rounds: int = 7, n: int = 10) -> None:
         return ctypes.c_void_p(base.value + k * slice_b)
 
     handles = {}
-    for name in ("ormi_hbm_read_chunk", "ormi_hbm_read_stride", "ormi_hbm_copy", "ormi_hbm_write"):
+    for name in ("ormi_hbm_read_chunk", "ormi_hbm_read_chunk_nt", "ormi_hbm_read_stride", "ormi_hbm_copy",
+                 "ormi_hbm_copy_nt", "ormi_hbm_write", "ormi_hbm_write_plain"):
         h = ctypes.c_uint64()
         if lib.ormi_hip_rtc_compile(HBM_PROBE_SRC.encode(), name.encode(), None, 0, ctypes.byref(h)) != 0:
             raise SystemExit("hbm probe: " + lib.ormi_hip_last_error().decode())
@@ -799,11 +828,17 @@ def hbm_ceiling(out_md: Path, cmd: str, rounds: int = 7, n: int = 10) -> None:
     cases = [
         ("read 512 MiB, 8 KB per work-group, 4 loads in flight per thread", "ormi_hbm_read_chunk", n4_two // chunk,
          [argv(at(2 * r), n4_two, chunk, out) for r in range(4)], 2 * slice_b),
+        ("the same, non-temporal loads", "ormi_hbm_read_chunk_nt", n4_two // chunk,
+         [argv(at(2 * r), n4_two, chunk, out) for r in range(4)], 2 * slice_b),
         (f"read 512 MiB, grid stride over {16 * cus} work-groups", "ormi_hbm_read_stride", 16 * cus,
          [argv(at(2 * r), n4_two, out) for r in range(4)], 2 * slice_b),
         (f"copy 256 MiB to 256 MiB, non-temporal stores, {64 * cus} work-groups", "ormi_hbm_copy", 64 * cus,
          [argv(at(4 + r), at(r), n4_one) for r in range(4)], 2 * slice_b),
+        ("the same, non-temporal loads too", "ormi_hbm_copy_nt", 64 * cus,
+         [argv(at(4 + r), at(r), n4_one) for r in range(4)], 2 * slice_b),
         (f"write 512 MiB, non-temporal stores, {64 * cus} work-groups", "ormi_hbm_write", 64 * cus,
+         [argv(at(2 * r), n4_two) for r in range(4)], 2 * slice_b),
+        ("the same, plain stores", "ormi_hbm_write_plain", 64 * cus,
          [argv(at(2 * r), n4_two) for r in range(4)], 2 * slice_b),
     ]
     rows = []

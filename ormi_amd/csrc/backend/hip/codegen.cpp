@@ -90,10 +90,13 @@ namespace ormi::hip {
             x.map_unroll = std::clamp(env_int("ORMI_MAP_UNROLL", x.map_unroll), 1, 8);
             x.map_blocks_per_cu = std::clamp(env_int("ORMI_MAP_BLOCKS_PER_CU", x.map_blocks_per_cu), 1, 1024);
             x.row_unroll = std::clamp(env_int("ORMI_ROW_UNROLL", x.row_unroll), 1, 8);
+            x.row_waves = env_int("ORMI_ROW_WAVES", x.row_waves);
+            if (x.row_waves != 1 && x.row_waves != 2 && x.row_waves != 4) x.row_waves = 4;
             x.col_waves = std::clamp(env_int("ORMI_COL_WAVES", x.col_waves), 1, 16);
             x.col_cwaves = std::clamp(env_int("ORMI_COL_CWAVES", x.col_cwaves), 1, 16);
             x.map_nt_loads = env_int("ORMI_MAP_NT_LOADS", x.map_nt_loads) != 0;
             x.reduce_nt_loads = env_int("ORMI_REDUCE_NT_LOADS", x.reduce_nt_loads) != 0;
+            x.nt_min_bytes = std::max(0, env_int("ORMI_NT_MIN_MIB", (int)(x.nt_min_bytes >> 20))) * (1LL << 20);
             x.map_nt_stores = env_int("ORMI_MAP_NT_STORES", x.map_nt_stores) != 0;
             x.map_off32 = env_int("ORMI_MAP_OFF32", x.map_off32) != 0;
             x.map_rows = env_int("ORMI_MAP_ROWS", x.map_rows) != 0;
@@ -260,7 +263,29 @@ namespace ormi::hip {
             int vec = 1;
             int vec_dim = -1;  // dim whose coordinate advances by VEC
             int rows = 0;      // map tile alignment to the last dim (plan_map_multi)
+            // Non-temporal hint on the loads of streamed leaves: those with no
+            // zero stride in the canonical (size-1-free) dims, whose elements
+            // the kernel reads once. A broadcast leaf (a bias row re-read by
+            // every row) keeps plain loads, so its lines stay in the L2.
             bool nt_loads = false;
+            bool streamed(size_t L) const {
+                for (long long s : c.st[L])
+                    if (s == 0) return false;
+                return true;
+            }
+            // Bytes the streamed leaves bring in over `numel` kernel elements.
+            long long streamed_bytes(long long numel) const {
+                long long b = 0;
+                for (size_t L = 0; L < e.leaves.size(); ++L)
+                    if (!scalar[L] && streamed(L)) b += numel * (long long)dtype_size(e.leaves[L].dtype);
+                return b;
+            }
+            // The hint pays on streams larger than the caches (measured on a
+            // 128 MiB copy: 45.4 -> 43.5 us). On small operands, which the
+            // Infinity Cache may still hold from their producer, it costs.
+            void choose_nt_loads(bool enabled, long long numel) {
+                nt_loads = enabled && streamed_bytes(numel) >= tuning().nt_min_bytes;
+            }
             // Output dtypes of a map: bf16 and fp16 share a storage type, so the
             // argument list alone does not tell their stores apart.
             std::vector<DType> out_dtypes;
@@ -408,7 +433,7 @@ namespace ormi::hip {
                 const std::string p = "L" + std::to_string(L);
                 if (scalar[L]) return;  // hoisted
                 const bool unit = vec > 1 && c.st[L][vec_dim] == 1;
-                const bool nt = nt_loads;
+                const bool nt = nt_loads && streamed(L);
                 if (unit) {
                     const char* vt = dt == DType::Float32 ? "ormi_f4" : "ormi_u16x4";
                     const std::string addr = elem_ptr(std::string("const ") + vt + "*", p, off, dtype_size(dt), true);
@@ -602,13 +627,12 @@ namespace ormi::hip {
             const Tuning& t = tuning();
             s += kind;
             s += '|';
-            for (long long v : {(long long)t.map_unroll, (long long)t.row_unroll, (long long)t.col_waves}) {
+            for (long long v : {(long long)t.map_unroll, (long long)t.row_unroll, (long long)t.col_waves, (long long)t.row_waves}) {
                 append_int(s, v);
                 s += ',';
             }
-            s += char('0' + t.map_nt_loads);
+            s += char('0' + g.nt_loads);
             s += char('0' + t.map_nt_stores);
-            s += char('0' + t.reduce_nt_loads);
             s += '|';
             for (const auto& d : g.args.decls) {
                 s += d.is_const ? 'c' : 'm';
@@ -761,7 +785,6 @@ namespace ormi::hip {
         const int block = 256, unroll = tn.map_unroll;
         Gen g(expr);
         g.out_dtypes = out_dtypes;
-        g.nt_loads = tn.map_nt_loads;
         g.want_off32 = tn.map_off32;
         for (int s : shape) g.c.dims.push_back({(long long)s, G_M});
         for (const auto& L : expr.leaves) g.c.st.push_back(L.st);
@@ -776,6 +799,7 @@ namespace ormi::hip {
             if (!vector_dtype(out_dtypes[r]) || ((uintptr_t)outs[r] % 16) != 0) g.vec = 1;
         long long numel = 1;
         for (auto& d : g.c.dims) numel *= d.size;
+        g.choose_nt_loads(tn.map_nt_loads, numel);
         const long long G = numel / g.vec;
         const long long tile = (long long)block * unroll;
         const long long tiles = (G + tile - 1) / tile;
@@ -971,7 +995,6 @@ namespace ormi::hip {
             if (red[d]) last_red = d;
 
         Gen g(expr);
-        g.nt_loads = tn.reduce_nt_loads;
         // Kernel dim order: O dims, R dims, I dims (each in logical order).
         std::vector<int> perm;
         for (int d = 0; d < n; ++d) if (!red[d] && d < last_red) perm.push_back(d);
@@ -986,6 +1009,7 @@ namespace ormi::hip {
         canonicalize(g.c, g.scalar);
 
         const long long O = group_size(g.c, G_O), R = group_size(g.c, G_R), I = group_size(g.c, G_I);
+        g.choose_nt_loads(tn.reduce_nt_loads, O * R * I);
         if (R >= (1ll << 31)) throw std::runtime_error("HIP reduce: reduced extent above 2^31 elements.");
         const std::vector<int> od = dims_of(g.c, G_O), rd = dims_of(g.c, G_R), id = dims_of(g.c, G_I);
         const bool column = !id.empty();
@@ -1009,6 +1033,12 @@ namespace ormi::hip {
             P = RG == 0 ? 1 : (RG + CH - 1) / CH;  // drop empty parts
             g.choose_idx(O * P * 64 + RG * V + 64 * V * RU);
             plan.two_pass = P > 1;
+            // Long rows that need no split: WR waves of one block share a row
+            // and combine their results through LDS in wave order. Shorter
+            // waves leave a shorter tail when the grid drains (C3's 32 KB
+            // rows: 78.4 us with four waves per row against 81.6 with one,
+            // the same reads).
+            const int WR = (P == 1 && CH >= 1024) ? tn.row_waves : 1;
             const StoreEpilogue* ep1 = plan.two_pass ? nullptr : ep;  // the finishing kernel stores a split result
             g.args.ptr(false, "void", "outp", plan.two_pass ? nullptr : out);  // workspace bound later
             g.args.ptr(false, "int", "outi", nullptr);
@@ -1020,18 +1050,29 @@ namespace ormi::hip {
             g.args.i64("CH", CH);
             g.declare_dims();
             g.declare_strides();
-            k.grid[0] = (uint32_t)std::max(1LL, (O * P + 3) / 4);
+            const int UPB = 4 / WR;  // (row, part) units per 256-thread block
+            k.grid[0] = (uint32_t)std::max(1LL, (O * P + UPB - 1) / UPB);
             k.plan.kind = "row";
             k.plan.op = name;
-            for (auto [key, v] : {std::pair<const char*, long long>{"O", O}, {"R", R}, {"vec", V}, {"parts", P}, {"idx", g.idx32 ? 32 : 64}})
+            for (auto [key, v] : {std::pair<const char*, long long>{"O", O}, {"R", R}, {"vec", V}, {"parts", P},
+                                  {"waves_per_row", WR}, {"idx", g.idx32 ? 32 : 64}})
                 k.plan.add(key, v);
-            resolve(g, std::string("row") + name, 256, k, [&] {
+            resolve(g, std::string("row") + name + (WR > 1 ? "_w" + std::to_string(WR) : std::string()), 256, k, [&] {
                 const std::string t = g.idx();
                 std::ostringstream& b = g.body();
                 g.hoist_scalars(b, "  ");
                 b << "  const int lane = threadIdx.x & 63;\n";
-                b << "  const " << t << " wid = (" << t << ")blockIdx.x * 4 + (" << t << ")(threadIdx.x >> 6);\n";
-                b << "  if (wid >= (" << t << ")NO * (" << t << ")NP) return;\n";
+                if (WR == 1) {
+                    b << "  const " << t << " wid = (" << t << ")blockIdx.x * 4 + (" << t << ")(threadIdx.x >> 6);\n";
+                    b << "  if (wid >= (" << t << ")NO * (" << t << ")NP) return;\n";
+                } else {
+                    // Every wave reaches the barrier below; a wave past the last
+                    // unit reads unit 0's row and its result is dropped.
+                    b << "  const int wv = (int)(threadIdx.x >> 6), q = wv % " << WR << ";\n";
+                    b << "  const " << t << " wid_ = (" << t << ")blockIdx.x * " << UPB << " + (" << t << ")(wv / " << WR << ");\n";
+                    b << "  const bool live = wid_ < (" << t << ")NO * (" << t << ")NP;\n";
+                    b << "  const " << t << " wid = live ? wid_ : 0;\n";
+                }
                 b << "  const " << t << " o = wid / (" << t << ")NP, p = wid - o * (" << t << ")NP;\n";
                 g.declare_coords(b, "  ", od);
                 g.decompose(b, "  ", "o", od);
@@ -1040,8 +1081,18 @@ namespace ormi::hip {
                     std::string off = g.offset(L, od);
                     b << "  const " << t << " base" << L << " = " << (off.empty() ? "0" : off) << ";\n";
                 }
-                b << "  const " << t << " rg0 = p * (" << t << ")CH;\n";
-                b << "  const " << t << " rg1 = rg0 + (" << t << ")CH < (" << t << ")RG ? rg0 + (" << t << ")CH : (" << t << ")RG;\n";
+                if (WR == 1) {
+                    b << "  const " << t << " rg0 = p * (" << t << ")CH;\n";
+                    b << "  const " << t << " rg1 = rg0 + (" << t << ")CH < (" << t << ")RG ? rg0 + (" << t << ")CH : (" << t << ")RG;\n";
+                } else {
+                    // Wave q takes the q-th of WR consecutive pieces of the part, each a
+                    // whole number of 64-group strides.
+                    b << "  const " << t << " pr0 = p * (" << t << ")CH;\n";
+                    b << "  const " << t << " pr1 = pr0 + (" << t << ")CH < (" << t << ")RG ? pr0 + (" << t << ")CH : (" << t << ")RG;\n";
+                    b << "  const " << t << " sc = ((pr1 - pr0 + " << WR - 1 << ") / " << WR << " + 63) / 64 * 64;\n";
+                    b << "  const " << t << " rg0 = pr0 + q * sc < pr1 ? pr0 + q * sc : pr1;\n";
+                    b << "  const " << t << " rg1 = rg0 + sc < pr1 ? rg0 + sc : pr1;\n";
+                }
                 if (is_sum) b << "  float acc[" << V << "];\n#pragma unroll\n  for (int k = 0; k < " << V << "; ++k) acc[k] = 0.0f;\n";
                 // max / argmax: one (value, index) chain per vector slot, so
                 // the V chains advance independently.
@@ -1077,9 +1128,17 @@ namespace ormi::hip {
                     emit_step(1, "    ");
                     b << "  }\n";
                 }
+                // WR > 1: the unit's waves leave their results in LDS; after the
+                // barrier, lane 0 of wave q = 0 combines them in wave order.
+                if (WR > 1) b << "  __shared__ float red_v_[4];\n" << (is_sum ? "" : "  __shared__ int red_i_[4];\n");
                 if (is_sum) {
                     b << "  float s = " << (V > 1 ? "(acc[0] + acc[1]) + (acc[2] + acc[3])" : "acc[0]") << ";\n";
                     b << "  s = ormi_wave_sum(s);\n";
+                    if (WR > 1) {
+                        b << "  if (lane == 0) red_v_[wv] = s;\n  __syncthreads();\n";
+                        b << "  if (!live || q != 0) return;\n";
+                        b << "#pragma unroll\n  for (int w = 1; w < " << WR << "; ++w) s += red_v_[wv + w];\n";
+                    }
                     b << "  if (lane == 0) {\n    ((float*)outp)[wid] = s;\n";
                     emit_epilogue(b, "    ", ep1, "s", "wid");
                     b << "  }\n";
@@ -1092,6 +1151,11 @@ namespace ormi::hip {
                     b << "  float bv = mv[0]; int bi = mi[0];\n";
                     b << "#pragma unroll\n  for (int k = 1; k < " << V << "; ++k) ormi_am_take(bv, bi, mv[k], mi[k]);\n";
                     b << "  ormi_wave_argmax(bv, bi);\n";
+                    if (WR > 1) {
+                        b << "  if (lane == 0) { red_v_[wv] = bv; red_i_[wv] = bi; }\n  __syncthreads();\n";
+                        b << "  if (!live || q != 0) return;\n";
+                        b << "#pragma unroll\n  for (int w = 1; w < " << WR << "; ++w) ormi_am_take(bv, bi, red_v_[wv + w], red_i_[wv + w]);\n";
+                    }
                     b << "  if (lane == 0) {\n";
                     if (is_arg) b << "    if (NP == 1) ((long long*)outp)[wid] = (long long)bi; else { ((float*)outp)[wid] = bv; outi[wid] = bi; }\n";
                     else b << "    ((float*)outp)[wid] = bv; if (NP > 1) outi[wid] = bi;\n";

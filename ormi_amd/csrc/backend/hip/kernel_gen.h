@@ -101,11 +101,15 @@ namespace ormi::hip {
         int map_unroll = 2;        // VEC groups per thread per iteration (map)
         int map_blocks_per_cu = 64;
         int row_unroll = 4;        // VEC groups per lane per iteration (row reduce)
+        int row_waves = 4;         // waves sharing one long row (row reduce; 1, 2 or 4)
         int col_waves = 16;        // waves per block (column reduce)
         int col_cwaves = 8;        // of those, waves side by side across the kept columns
-        bool map_nt_loads = false;    // non-temporal hint on a map's operand loads
+        bool map_nt_loads = true;     // non-temporal hint on a map's operand loads
         bool map_nt_stores = true;    // non-temporal hint on a map's output stores
         bool reduce_nt_loads = true;  // non-temporal hint on a reduction's loads
+        // Both load hints apply only to leaves read once (no broadcast), in
+        // kernels whose such leaves bring in at least this many bytes.
+        long long nt_min_bytes = 64LL << 20;
         bool map_off32 = true;        // 32-bit byte offsets from uniform bases when they fit (map)
         bool map_rows = true;         // row-aligned tiles when a tile covers whole rows or lies in one (map)
     };

@@ -341,6 +341,44 @@ def test_column_kernels_keyed_by_column_waves(ob, cpu, cabi):
     assert all(len(names) == 3 for names in seen.values()), seen
 
 
+def test_long_rows_share_waves(ob, cpu, cabi):
+    """Rows of at least 1024 groups, enough of them for one pass, are shared by
+    four waves of a block that combine through LDS in wave order; shorter rows
+    and split rows keep one wave per (row, part). The two layouts are different
+    kernels (the name carries the wave count) and both compile."""
+    def plan(shape, red):
+        return ob._plan_kernel(getattr(ob, red)(_cpu(np.zeros(shape))._node, [1], False))
+
+    for red in ("sum", "max", "argmax"):
+        long_rows, short_rows, split = plan((4099, 4108), red), plan((4099, 4092), red), plan((64, 8192), red)
+        assert "waves_per_row=4" in long_rows["plan"] and "__syncthreads()" in long_rows["source"], long_rows["plan"]
+        assert "waves_per_row=1" in short_rows["plan"] and "__syncthreads()" not in short_rows["source"]
+        assert "waves_per_row=1" in split["plan"] and split["two_pass"], split["plan"]
+        assert long_rows["name"] != short_rows["name"]
+        for d in (long_rows, short_rows):
+            rc, _ = _compile_only(cabi, d["source"], ob._rtc_options())
+            assert rc == ORMI_HIP_OK, (red, d["plan"], cabi.ormi_hip_last_error())
+
+
+def test_non_temporal_loads_only_for_large_read_once_operands(ob, cpu):
+    """Loads carry the non-temporal hint only for operands read once (no zero
+    stride), and only when those bring in at least 64 MiB: the C2 chain's
+    (8192, 4096) input is hinted, its bias row (re-read by every row) is not,
+    and a (1024, 4096) chain or row sum is not hinted at all."""
+    def body(d):
+        return d["source"].split('extern "C"')[1]
+
+    x, bias = np.zeros((8192, 4096), np.float32), np.zeros(4096, np.float32)
+    d = ob._plan_kernel((_cpu(x) + _cpu(bias)).tanh()._node)
+    src = body(d)
+    assert src.count("__builtin_nontemporal_load(") == 1, src
+    assert "__builtin_nontemporal_load((const ormi_f4*)((const char*)L0" in src, src
+    small = body(ob._plan_kernel((_cpu(x[:1024]) + _cpu(bias)).tanh()._node))
+    assert "__builtin_nontemporal_load(" not in small
+    assert "__builtin_nontemporal_load(" in body(ob._plan_kernel(ob.sum(_cpu(x)._node, [1], False)))
+    assert "__builtin_nontemporal_load(" not in body(ob._plan_kernel(ob.sum(_cpu(x[:1024])._node, [1], False)))
+
+
 def test_kernel_cache_tells_bf16_from_f16(ob, cpu):
     """bf16 and fp16 share a storage type (unsigned short). The generator's
     kernel cache must still key on the element type: a bf16 leaf (or output)

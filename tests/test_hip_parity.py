@@ -396,6 +396,8 @@ def test_c3_column_sum(cpu, hip, c3):
 @pytest.mark.parametrize("shape,axes", [
     ((7, 5), (0,)), ((7, 5), (1,)), ((7, 5), None), ((3, 4, 5), (0, 2)), ((3, 4, 5), (1,)),
     ((2, 3, 4, 5), (1, 2)), ((1, 1000003), (1,)), ((1000003,), None), ((513, 3), (0,)), ((5, 1, 7), (1,)),
+    # long rows, enough of them for one pass: four waves share a row (uneven pieces; 128-bit and scalar loads)
+    ((4099, 4108), (1,)), ((4100, 4097), (1,)),
 ])
 def test_reduction_shapes(cpu, hip, shape, axes):
     rng = np.random.default_rng(24)
@@ -424,10 +426,12 @@ def test_argmax_ties_and_nan(cpu, hip):
     assert_bits_equal(T(x, hip).max(1).numpy(), T(x, cpu).max(1).numpy())
 
 
-@pytest.mark.parametrize("shape,axis", [((3, 1 << 20), 1), ((1 << 16, 6), 0), ((5, 1003), 1), ((1003, 70), 0)])
+@pytest.mark.parametrize("shape,axis", [((3, 1 << 20), 1), ((1 << 16, 6), 0), ((5, 1003), 1), ((1003, 70), 0),
+                                        ((4099, 4108), 1), ((4100, 4097), 1)])
 def test_argmax_edge_cases_all_paths(cpu, hip, shape, axis):
-    """Row, column and two-pass (split) reductions: the first maximum wins across
-    lanes, vector slots and parts; all -inf, NaN first / later, +-0 first."""
+    """Row, column and two-pass (split) reductions, and rows that several waves
+    share: the first maximum wins across lanes, vector slots, waves and parts;
+    all -inf, NaN first / later, +-0 first."""
     rng = np.random.default_rng(43)
     x = rng.standard_normal(shape).astype(np.float32)
     xm = np.moveaxis(x, axis, -1)  # view: reduced axis last
