@@ -92,6 +92,7 @@ namespace ormi::hip {
             x.row_unroll = std::clamp(env_int("ORMI_ROW_UNROLL", x.row_unroll), 1, 8);
             x.row_waves = env_int("ORMI_ROW_WAVES", x.row_waves);
             if (x.row_waves != 1 && x.row_waves != 2 && x.row_waves != 4) x.row_waves = 4;
+            x.row_waves_min_groups = std::max(1, env_int("ORMI_ROW_WAVES_MIN_GROUPS", x.row_waves_min_groups));
             x.col_waves = std::clamp(env_int("ORMI_COL_WAVES", x.col_waves), 1, 16);
             x.col_cwaves = std::clamp(env_int("ORMI_COL_CWAVES", x.col_cwaves), 1, 16);
             x.map_nt_loads = env_int("ORMI_MAP_NT_LOADS", x.map_nt_loads) != 0;
@@ -627,7 +628,8 @@ namespace ormi::hip {
             const Tuning& t = tuning();
             s += kind;
             s += '|';
-            for (long long v : {(long long)t.map_unroll, (long long)t.row_unroll, (long long)t.col_waves, (long long)t.row_waves}) {
+            for (long long v : {(long long)t.map_unroll, (long long)t.row_unroll, (long long)t.col_waves, (long long)t.row_waves,
+                                (long long)t.row_waves_min_groups}) {
                 append_int(s, v);
                 s += ',';
             }
@@ -1038,7 +1040,7 @@ namespace ormi::hip {
             // waves leave a shorter tail when the grid drains (C3's 32 KB
             // rows: 78.4 us with four waves per row against 81.6 with one,
             // the same reads).
-            const int WR = (P == 1 && CH >= 1024) ? tn.row_waves : 1;
+            const int WR = (P == 1 && CH >= tn.row_waves_min_groups) ? tn.row_waves : 1;
             const StoreEpilogue* ep1 = plan.two_pass ? nullptr : ep;  // the finishing kernel stores a split result
             g.args.ptr(false, "void", "outp", plan.two_pass ? nullptr : out);  // workspace bound later
             g.args.ptr(false, "int", "outi", nullptr);

@@ -102,6 +102,7 @@ namespace ormi::hip {
         int map_blocks_per_cu = 64;
         int row_unroll = 4;        // VEC groups per lane per iteration (row reduce)
         int row_waves = 4;         // waves sharing one long row (row reduce; 1, 2 or 4)
+        int row_waves_min_groups = 1024;  // row length (VEC groups) from which rows are shared
         int col_waves = 16;        // waves per block (column reduce)
         int col_cwaves = 8;        // of those, waves side by side across the kept columns
         bool map_nt_loads = true;     // non-temporal hint on a map's operand loads
