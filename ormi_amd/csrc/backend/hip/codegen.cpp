@@ -1186,24 +1186,24 @@ namespace ormi::hip {
                     sb << "  if (o >= NO) return;\n";
                     sb << "  const float* pv = pvals + o * NP; const int* pi = pidx + o * NP;\n";
                     // Each lane combines its partials q = lane, lane + 64, ... in
-                    // that order; eight are loaded before they are combined, so
-                    // the loads overlap instead of each waiting out a latency.
+                    // that order; sixteen are loaded before they are combined
+                    // (past NP they are skipped, not added), so each batch of 1024
+                    // partials costs one memory latency instead of one per load.
                     sb << "  long long q = lane;\n";
                     if (is_sum) {
                         sb << "  float s = 0.0f;\n";
-                        sb << "  for (; q + 448 < NP; q += 512) {\n    float v[8];\n#pragma unroll\n"
-                              "    for (int u = 0; u < 8; ++u) v[u] = pv[q + 64 * u];\n#pragma unroll\n"
-                              "    for (int u = 0; u < 8; ++u) s += v[u];\n  }\n";
-                        sb << "  for (; q < NP; q += 64) s += pv[q];\n";
+                        sb << "  for (; q < NP; q += 1024) {\n    float v[16];\n#pragma unroll\n"
+                              "    for (int u = 0; u < 16; ++u) v[u] = q + 64 * u < NP ? pv[q + 64 * u] : 0.0f;\n#pragma unroll\n"
+                              "    for (int u = 0; u < 16; ++u) if (q + 64 * u < NP) s += v[u];\n  }\n";
                         sb << "  s = ormi_wave_sum(s);\n  if (lane == 0) {\n    ((float*)outp)[o] = s;\n";
                         emit_epilogue(sb, "    ", ep, "s", "o");
                         sb << "  }\n";
                     } else {
                         sb << "  float bv = -__builtin_inff(); int bi = 0x7fffffff;\n";
-                        sb << "  for (; q + 448 < NP; q += 512) {\n    float v[8]; int ix[8];\n#pragma unroll\n"
-                              "    for (int u = 0; u < 8; ++u) { v[u] = pv[q + 64 * u]; ix[u] = pi[q + 64 * u]; }\n"
-                              "#pragma unroll\n    for (int u = 0; u < 8; ++u) ormi_am_take(bv, bi, v[u], ix[u]);\n  }\n";
-                        sb << "  for (; q < NP; q += 64) ormi_am_take(bv, bi, pv[q], pi[q]);\n";
+                        sb << "  for (; q < NP; q += 1024) {\n    float v[16]; int ix[16];\n#pragma unroll\n"
+                              "    for (int u = 0; u < 16; ++u) { const bool in = q + 64 * u < NP; v[u] = in ? pv[q + 64 * u] : 0.0f; "
+                              "ix[u] = in ? pi[q + 64 * u] : 0; }\n"
+                              "#pragma unroll\n    for (int u = 0; u < 16; ++u) if (q + 64 * u < NP) ormi_am_take(bv, bi, v[u], ix[u]);\n  }\n";
                         sb << "  ormi_wave_argmax(bv, bi);\n";
                         if (is_arg) sb << "  if (lane == 0) ((long long*)outp)[o] = (long long)bi;\n";
                         else {
