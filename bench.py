@@ -1637,6 +1637,10 @@ def main():
         print(json.dumps({"only": args.only, **res}), flush=True)
         return
     main_res = bench_c2(args, ev)
+    props = _Props()
+    assert ev.lib.ormi_hip_get_props(ctypes.byref(props)) == 0
+    device = {"name": props.name.decode(errors="replace"), "compute_units": props.compute_units,
+              "peak_clock_mhz": props.clock_khz // 1000, "hbm_bytes": props.total_mem_bytes}
     extra = {}
     if not args.no_extra:
         n = max(10, min(args.steps, 30))
@@ -1670,6 +1674,7 @@ def main():
         # Untimed: the process's first C2 realize, which compiles the fused
         # kernel through hipRTC before launching it.
         "first_realize_ms": round(main_res["first_realize_ms"], 1),
+        "device": device,
         "extra": extra,
     }
     print(json.dumps(line), flush=True)
