@@ -144,6 +144,17 @@ def c2_bytes(rows=8192, cols=4096):
     return 4 * (rows * cols * 2 + cols + rows)  # read x, bias, scale; write z
 
 
+def host_cpu_model() -> str:
+    """The host CPU's model name as /proc/cpuinfo gives it, or "unknown"."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline_c2(target_s: float = 10.0) -> dict:
     """Oracle on one core: per-node execute_graph (what Ormi's CPU backend does on
     .numpy()) over a row sample of the C2 workload, repeated to ~target_s."""
@@ -175,7 +186,8 @@ def cpu_baseline_c2(target_s: float = 10.0) -> dict:
         "value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
         "sample": f"C2 rows 0..{rows} of (8192,4096) (1/8 of the workload), per-node execute_graph, "
                   f"{reps} reps, {per * 1e3:.1f} ms/rep; fused-tape execute_jit {fused * 1e3:.1f} ms "
-                  f"({c2_bytes(rows, cols) / fused / 1e9:.4f} GB/s); host {os.cpu_count()} cpus visible",
+                  f"({c2_bytes(rows, cols) / fused / 1e9:.4f} GB/s); host {os.cpu_count()} cpus visible "
+                  f"({host_cpu_model()})",
     }
 
 
