@@ -95,6 +95,9 @@ namespace ormi::hip {
             x.row_waves_min_groups = std::max(1, env_int("ORMI_ROW_WAVES_MIN_GROUPS", x.row_waves_min_groups));
             x.col_waves = std::clamp(env_int("ORMI_COL_WAVES", x.col_waves), 1, 16);
             x.col_cwaves = std::clamp(env_int("ORMI_COL_CWAVES", x.col_cwaves), 1, 16);
+            x.map_wg_per_cu = std::clamp(env_int("ORMI_MAP_WG_PER_CU", x.map_wg_per_cu), 0, 32);
+            x.row_wg_per_cu = std::clamp(env_int("ORMI_ROW_WG_PER_CU", x.row_wg_per_cu), 0, 32);
+            x.row_max_wg_per_cu = std::clamp(env_int("ORMI_ROW_MAX_WG_PER_CU", x.row_max_wg_per_cu), 0, 32);
             x.map_nt_loads = env_int("ORMI_MAP_NT_LOADS", x.map_nt_loads) != 0;
             x.reduce_nt_loads = env_int("ORMI_REDUCE_NT_LOADS", x.reduce_nt_loads) != 0;
             x.nt_min_bytes = std::max(0, env_int("ORMI_NT_MIN_MIB", (int)(x.nt_min_bytes >> 20))) * (1LL << 20);
@@ -104,6 +107,23 @@ namespace ormi::hip {
             return x;
         }();
         return t;
+    }
+
+    // Dynamic LDS that lets at most n work-groups of a kernel share one CU
+    // (gfx950: 160 KB of LDS per CU, allocated in 512-byte units), leaving
+    // 1 KB per work-group for the kernel's own LDS; 0 when n is 0 or the
+    // grid would not fill n per CU anyway. Fewer concurrent streams use HBM
+    // better, down to the point where too few waves are left to cover the
+    // arithmetic. Measured on C2's shapes: the copy y = -x took 43.7-43.8 us
+    // at the 8 per CU its registers allow, 42.0-42.3 at 5; C2's chain 44.4 at
+    // 8, 44.1 at 5, 45.4-45.6 at 4. C3's row sum with four waves per 32 KB
+    // row 79.7-80.2 us at 8, 76.1-76.4 at 3; its row max 80.3-80.4 at 8,
+    // 75.9-76.1 at 4, 82.1-82.4 at 3 (each element extends a dependent
+    // (value, index) chain).
+    static uint32_t occupancy_lds(int n, long long grid, int cu) {
+        if (n <= 0 || grid <= (long long)n * std::max(cu, 1)) return 0;
+        constexpr int kCuLds = 160 * 1024;
+        return (uint32_t)((kCuLds / n - 1024) / 512 * 512);
     }
 
     FastDiv make_fastdiv(uint32_t d) {
@@ -856,6 +876,7 @@ namespace ormi::hip {
             g.args.i64("P", tile / Dl);
         }
         k.grid[0] = (uint32_t)grid;
+        k.lds = occupancy_lds(tn.map_wg_per_cu, grid, cu);
         k.plan.kind = "map";
         k.plan.add("ndim", n);
         k.plan.add("vec", g.vec);
@@ -864,6 +885,7 @@ namespace ormi::hip {
         k.plan.add("rows", rows);
         k.plan.add("groups", G);
         k.plan.add("unroll", unroll);
+        if (k.lds) k.plan.add("lds", k.lds);
         if (nout > 1) k.plan.add("outputs", (long long)nout);
         resolve(g, "map", block, k, [&] {
             std::vector<int> all, outer;
@@ -1054,11 +1076,13 @@ namespace ormi::hip {
             g.declare_strides();
             const int UPB = 4 / WR;  // (row, part) units per 256-thread block
             k.grid[0] = (uint32_t)std::max(1LL, (O * P + UPB - 1) / UPB);
+            k.lds = occupancy_lds(is_sum ? tn.row_wg_per_cu : tn.row_max_wg_per_cu, k.grid[0], cu);
             k.plan.kind = "row";
             k.plan.op = name;
             for (auto [key, v] : {std::pair<const char*, long long>{"O", O}, {"R", R}, {"vec", V}, {"parts", P},
                                   {"waves_per_row", WR}, {"idx", g.idx32 ? 32 : 64}})
                 k.plan.add(key, v);
+            if (k.lds) k.plan.add("lds", k.lds);
             resolve(g, std::string("row") + name + (WR > 1 ? "_w" + std::to_string(WR) : std::string()), 256, k, [&] {
                 const std::string t = g.idx();
                 std::ostringstream& b = g.body();
@@ -1455,6 +1479,7 @@ namespace ormi::hip {
                     k.grid[i] = c.grid[i];
                     k.block[i] = c.block[i];
                 }
+                k.lds = c.lds;
                 k.args = c.args;
             }
             for (const auto& [slot, src] : c.ptr_slots) k.args[slot] = slot_value(src, e, outs, ep);
@@ -1564,12 +1589,12 @@ namespace ormi::hip {
             }
         }
         if (k.args.size() <= ORMI_HIP_QUEUED_MAX_ARGS) {
-            ORMI_HIP_CHECK(ormi_hip_launch_queued(handle, k.grid, k.block, 0, k.args.data(), (int)k.args.size()));
+            ORMI_HIP_CHECK(ormi_hip_launch_queued(handle, k.grid, k.block, k.lds, k.args.data(), (int)k.args.size()));
         } else {
             std::vector<uint64_t> vals = k.args;
             std::vector<void*> ptrs(vals.size());
             for (size_t i = 0; i < vals.size(); ++i) ptrs[i] = &vals[i];
-            ORMI_HIP_CHECK(ormi_hip_launch(handle, k.grid, k.block, 0, ptrs.data()));
+            ORMI_HIP_CHECK(ormi_hip_launch(handle, k.grid, k.block, k.lds, ptrs.data()));
         }
     }
 }

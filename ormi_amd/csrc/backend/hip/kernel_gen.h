@@ -87,6 +87,10 @@ namespace ormi::hip {
         uint64_t handle = 0;         // compiled kernel, once known
         uint32_t grid[3] = {1, 1, 1};
         uint32_t block[3] = {256, 1, 1};
+        // Dynamic LDS per work-group, allocated at launch and never touched by
+        // the kernel: it caps the work-groups resident per CU (see
+        // Tuning::map_wg_per_cu).
+        uint32_t lds = 0;
         std::vector<uint64_t> args;  // every parameter is 8 bytes
         PlanInfo plan;
         // Arguments that hold a buffer address, as (argument index, source):
@@ -105,6 +109,12 @@ namespace ormi::hip {
         int row_waves_min_groups = 1024;  // row length (VEC groups) from which rows are shared
         int col_waves = 16;        // waves per block (column reduce)
         int col_cwaves = 8;        // of those, waves side by side across the kept columns
+        // Work-groups resident per CU for map / row-reduction kernels whose grid
+        // would hold more (0: no cap). HBM streams run faster with fewer
+        // concurrent ones: see occupancy_lds.
+        int map_wg_per_cu = 5;
+        int row_wg_per_cu = 3;      // row sums
+        int row_max_wg_per_cu = 4;  // row max / argmax: a longer dependent chain per element
         bool map_nt_loads = true;     // non-temporal hint on a map's operand loads
         bool map_nt_stores = true;    // non-temporal hint on a map's output stores
         bool reduce_nt_loads = true;  // non-temporal hint on a reduction's loads

@@ -200,6 +200,7 @@ namespace {
         d["name"] = k.name;
         d["plan"] = k.plan.text();
         d["grid"] = std::vector<uint32_t>{k.grid[0], k.grid[1], k.grid[2]};
+        d["lds"] = k.lds;
         d["num_args"] = k.args.size();
         return d;
     }

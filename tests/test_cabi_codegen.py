@@ -379,6 +379,27 @@ def test_non_temporal_loads_only_for_large_read_once_operands(ob, cpu):
     assert "__builtin_nontemporal_load(" not in body(ob._plan_kernel(ob.sum(_cpu(x[:1024])._node, [1], False)))
 
 
+def test_large_streams_cap_work_groups_per_cu(ob, cpu):
+    """Map and row-reduction kernels whose grid would put more work-groups on
+    a CU than the measured best (5 for maps, 3 for row sums, 4 for row max /
+    argmax) get dynamic LDS that leaves room for only that many of them
+    (160 KB per CU, 1 KB kept for the kernel's own LDS); small grids get none."""
+    def lds(d):
+        return d["lds"]
+
+    def cap(n):
+        return (160 * 1024 // n - 1024) // 512 * 512
+
+    x = np.zeros((8192, 4096), np.float32)
+    big_map = ob._plan_kernel((_cpu(x) * 2.0)._node)
+    assert lds(big_map) == cap(5) and f"lds={cap(5)}" in big_map["plan"]
+    assert 5 * (cap(5) + 512) <= 160 * 1024 < 6 * cap(5)
+    assert lds(ob._plan_kernel((_cpu(x[:512]) * 2.0)._node)) == 0   # 512 work-groups: 2 per CU
+    assert lds(ob._plan_kernel(ob.sum(_cpu(x)._node, [1], False))) == cap(3)
+    assert lds(ob._plan_kernel(ob.max(_cpu(x)._node, [1], False))) == cap(4)
+    assert lds(ob._plan_kernel(ob.sum(_cpu(x[:256])._node, [1], False))) == 0
+
+
 def test_kernel_cache_tells_bf16_from_f16(ob, cpu):
     """bf16 and fp16 share a storage type (unsigned short). The generator's
     kernel cache must still key on the element type: a bf16 leaf (or output)
