@@ -862,19 +862,33 @@ def hbm_ceiling(out_md: Path, cmd: str, rounds: int = 7, n: int = 10) -> None:
         ("the same, plain stores", "ormi_hbm_write_plain", 64 * cus,
          [argv(at(2 * r), n4_two) for r in range(4)], 2 * slice_b),
     ]
+
+    # The same kernels with at most w work-groups per CU: a launch-time LDS
+    # reservation they do not touch (160 KB per CU; as the element-wise and
+    # row-reduction kernels are launched).
+    def capped(w):
+        return (160 * 1024 // w - 1024) // 512 * 512
+
+    for w in (5, 3):
+        cases.append((f"non-temporal read, 8 KB per work-group, at most {w} per CU", "ormi_hbm_read_chunk_nt",
+                      n4_two // chunk, cases[1][3], 2 * slice_b, capped(w)))
+        cases.append((f"non-temporal copy, at most {w} work-groups per CU", "ormi_hbm_copy_nt", 64 * cus,
+                      cases[4][3], 2 * slice_b, capped(w)))
     rows = []
-    for label, kname, grid_x, arg_sets, nbytes in cases:
+    for case in cases:
+        label, kname, grid_x, arg_sets, nbytes = case[:5]
+        lds = case[5] if len(case) > 5 else 0
         grid = (ctypes.c_uint32 * 3)(grid_x, 1, 1)
         block = (ctypes.c_uint32 * 3)(256, 1, 1)
         for i in range(8):
-            assert lib.ormi_hip_launch(handles[kname], grid, block, 0, arg_sets[i % 4]) == 0, lib.ormi_hip_last_error()
+            assert lib.ormi_hip_launch(handles[kname], grid, block, lds, arg_sets[i % 4]) == 0, lib.ormi_hip_last_error()
         ev.sync()
         times = []
         for _ in range(rounds):
             e0, e1 = ev.new(), ev.new()
             ev.record(e0)
             for i in range(n):
-                lib.ormi_hip_launch(handles[kname], grid, block, 0, arg_sets[i % 4])
+                lib.ormi_hip_launch(handles[kname], grid, block, lds, arg_sets[i % 4])
             ev.record(e1)
             ev.sync()
             times.append(ev.elapsed_ms(e0, e1) / n)

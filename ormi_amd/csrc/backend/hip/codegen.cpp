@@ -113,8 +113,11 @@ namespace ormi::hip {
     // (gfx950: 160 KB of LDS per CU, allocated in 512-byte units), leaving
     // 1 KB per work-group for the kernel's own LDS; 0 when n is 0 or the
     // grid would not fill n per CU anyway. Fewer concurrent streams use HBM
-    // better, down to the point where too few waves are left to cover the
-    // arithmetic. Measured on C2's shapes: the copy y = -x took 43.7-43.8 us
+    // better where a kernel writes about as much as it reads, or where its
+    // work-groups read long streams, down to the point where too few waves
+    // are left to cover the arithmetic; short-lived read-only work-groups
+    // need every slot (the ceiling probe's 8 KB-per-work-group read: 7.13 TB/s
+    // uncapped, 6.37 at 5 per CU, 4.25 at 3). Measured on C2's shapes: the copy y = -x took 43.7-43.8 us
     // at the 8 per CU its registers allow, 42.0-42.3 at 5; C2's chain 44.4 at
     // 8, 44.1 at 5, 45.4-45.6 at 4. C3's row sum with four waves per 32 KB
     // row 79.7-80.2 us at 8, 76.1-76.4 at 3; its row max 80.3-80.4 at 8,
@@ -876,7 +879,12 @@ namespace ormi::hip {
             g.args.i64("P", tile / Dl);
         }
         k.grid[0] = (uint32_t)grid;
-        k.lds = occupancy_lds(tn.map_wg_per_cu, grid, cu);
+        // The cap pays where the kernel writes about as much as it reads (a
+        // copy, C2); a kernel that mostly reads keeps every slot (the capped
+        // read-only kernels of the ceiling probe ran slower).
+        long long write_bytes = 0;
+        for (DType dt : out_dtypes) write_bytes += (long long)dtype_size(dt);
+        if (2 * write_bytes >= g.streamed_bytes(1)) k.lds = occupancy_lds(tn.map_wg_per_cu, grid, cu);
         k.plan.kind = "map";
         k.plan.add("ndim", n);
         k.plan.add("vec", g.vec);
@@ -1076,7 +1084,9 @@ namespace ormi::hip {
             g.declare_strides();
             const int UPB = 4 / WR;  // (row, part) units per 256-thread block
             k.grid[0] = (uint32_t)std::max(1LL, (O * P + UPB - 1) / UPB);
-            k.lds = occupancy_lds(is_sum ? tn.row_wg_per_cu : tn.row_max_wg_per_cu, k.grid[0], cu);
+            // Shared rows only (long-lived work-groups of 32 KB of reads and more;
+            // the cap starves short-lived ones, as in the ceiling probe).
+            if (WR > 1) k.lds = occupancy_lds(is_sum ? tn.row_wg_per_cu : tn.row_max_wg_per_cu, k.grid[0], cu);
             k.plan.kind = "row";
             k.plan.op = name;
             for (auto [key, v] : {std::pair<const char*, long long>{"O", O}, {"R", R}, {"vec", V}, {"parts", P},

@@ -383,7 +383,8 @@ def test_large_streams_cap_work_groups_per_cu(ob, cpu):
     """Map and row-reduction kernels whose grid would put more work-groups on
     a CU than the measured best (5 for maps, 3 for row sums, 4 for row max /
     argmax) get dynamic LDS that leaves room for only that many of them
-    (160 KB per CU, 1 KB kept for the kernel's own LDS); small grids get none."""
+    (160 KB per CU, 1 KB kept for the kernel's own LDS). Small grids, maps
+    that mostly read, and rows that one wave covers get none."""
     def lds(d):
         return d["lds"]
 
@@ -398,6 +399,10 @@ def test_large_streams_cap_work_groups_per_cu(ob, cpu):
     assert lds(ob._plan_kernel(ob.sum(_cpu(x)._node, [1], False))) == cap(3)
     assert lds(ob._plan_kernel(ob.max(_cpu(x)._node, [1], False))) == cap(4)
     assert lds(ob._plan_kernel(ob.sum(_cpu(x[:256])._node, [1], False))) == 0
+    y, z = np.ones((8192, 4096), np.float32), np.full((8192, 4096), 2.0, np.float32)
+    assert lds(ob._plan_kernel((_cpu(x) + _cpu(y) + _cpu(z))._node)) == 0  # reads 3x what it writes
+    short = ob._plan_kernel(ob.sum(_cpu(np.zeros((65536, 512), np.float32))._node, [1], False))
+    assert "waves_per_row=1" in short["plan"] and lds(short) == 0
 
 
 def test_kernel_cache_tells_bf16_from_f16(ob, cpu):
