@@ -95,6 +95,7 @@ namespace ormi::hip {
             x.row_waves_min_groups = std::max(1, env_int("ORMI_ROW_WAVES_MIN_GROUPS", x.row_waves_min_groups));
             x.col_waves = std::clamp(env_int("ORMI_COL_WAVES", x.col_waves), 1, 16);
             x.col_cwaves = std::clamp(env_int("ORMI_COL_CWAVES", x.col_cwaves), 1, 16);
+            x.col_unroll = std::clamp(env_int("ORMI_COL_UNROLL", x.col_unroll), 1, 8);
             x.map_wg_per_cu = std::clamp(env_int("ORMI_MAP_WG_PER_CU", x.map_wg_per_cu), 0, 32);
             x.row_wg_per_cu = std::clamp(env_int("ORMI_ROW_WG_PER_CU", x.row_wg_per_cu), 0, 32);
             x.row_max_wg_per_cu = std::clamp(env_int("ORMI_ROW_MAX_WG_PER_CU", x.row_max_wg_per_cu), 0, 32);
@@ -652,7 +653,7 @@ namespace ormi::hip {
             s += kind;
             s += '|';
             for (long long v : {(long long)t.map_unroll, (long long)t.row_unroll, (long long)t.col_waves, (long long)t.row_waves,
-                                (long long)t.row_waves_min_groups}) {
+                                (long long)t.row_waves_min_groups, (long long)t.col_unroll}) {
                 append_int(s, v);
                 s += ',';
             }
@@ -1296,7 +1297,7 @@ namespace ormi::hip {
         resolve(g, std::string("col") + name, block, k, [&] {
             const std::string t = g.idx();
             std::ostringstream& b = g.body();
-            const int CU = 4;  // rows in flight per wave
+            const int CU = tn.col_unroll;  // rows in flight per wave
             g.hoist_scalars(b, "  ");
             b << "  __shared__ float sv[" << WR << "][" << 64 * WC << "][" << V << "];\n";
             if (!is_sum) b << "  __shared__ int si[" << WR << "][" << 64 * WC << "][" << V << "];\n";

@@ -109,6 +109,7 @@ namespace ormi::hip {
         int row_waves_min_groups = 1024;  // row length (VEC groups) from which rows are shared
         int col_waves = 16;        // waves per block (column reduce)
         int col_cwaves = 8;        // of those, waves side by side across the kept columns
+        int col_unroll = 2;        // rows in flight per wave (column reduce)
         // Work-groups resident per CU for map / row-reduction kernels whose grid
         // would hold more (0: no cap). HBM streams run faster with fewer
         // concurrent ones: see occupancy_lds.
