@@ -398,6 +398,8 @@ def test_c3_column_sum(cpu, hip, c3):
     ((2, 3, 4, 5), (1, 2)), ((1, 1000003), (1,)), ((1000003,), None), ((513, 3), (0,)), ((5, 1, 7), (1,)),
     # long rows, enough of them for one pass: four waves share a row (uneven pieces; 128-bit and scalar loads)
     ((4099, 4108), (1,)), ((4100, 4097), (1,)),
+    # one long row in ~2,900 parts: the finish pass combines them in batches of 1,024 with a guarded tail
+    ((1, 3000017), (1,)),
 ])
 def test_reduction_shapes(cpu, hip, shape, axes):
     rng = np.random.default_rng(24)
