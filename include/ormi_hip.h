@@ -46,7 +46,9 @@ extern "C" {
  * (reference csrc/backend/cuda/allocator.cu:20-25). ormi_hip_init fails with
  * ORMI_HIP_ERR_NO_DEVICE when no GPU is visible, which makes the HIP device
  * absent the same way a throwing CUDAAllocator constructor does
- * (reference csrc/tests/test_utils.h:17-21). */
+ * (reference csrc/tests/test_utils.h:17-21). A device of another architecture
+ * than the one the library was built for (gfx950, the target its kernels are
+ * written and tuned for) is refused with ORMI_HIP_ERR_UNSUPPORTED. */
 int ormi_hip_device_count(int* count);
 int ormi_hip_init(int device);
 

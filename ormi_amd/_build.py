@@ -43,6 +43,7 @@ ARCH = os.environ.get("ORMI_HIP_ARCH", "gfx950")
 HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    f'-DORMI_HIP_TARGET="{ARCH}"',  # ormi_hip_init refuses a device of another architecture
 ]
 CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-ffp-contract=off", "-Wall", "-Wno-unused-function"]
 

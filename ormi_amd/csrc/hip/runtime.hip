@@ -15,6 +15,11 @@
 #include <unordered_map>
 #include <vector>
 
+// The architecture the library is built for (set by the build; gfx950).
+#ifndef ORMI_HIP_TARGET
+#define ORMI_HIP_TARGET "gfx950"
+#endif
+
 #include "ormi_hip.h"
 #include "ormi_hip_internal.h"
 #include "device/ormi_device.h"
@@ -458,8 +463,17 @@ int ormi_hip_init(int device) {
     int n = 0;
     if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return fail(ORMI_HIP_ERR_NO_DEVICE, "HIP Error: no GPU device is visible to this process");
     if (device < 0 || device >= n) return fail(ORMI_HIP_ERR_INVALID, "ormi_hip_init: device index out of range");
+    hipDeviceProp_t props;
+    ORMI_HIP_TRY(hipGetDeviceProperties(&props, device));
+    // The precompiled kernels exist for the build's target only, and the
+    // generated kernels' launch shapes assume gfx950's 160 KB of LDS per CU.
+    const size_t tn = std::strlen(ORMI_HIP_TARGET);
+    if (std::strncmp(props.gcnArchName, ORMI_HIP_TARGET, tn) != 0 ||
+        (props.gcnArchName[tn] != '\0' && props.gcnArchName[tn] != ':'))
+        return fail(ORMI_HIP_ERR_UNSUPPORTED, std::string("ormi_hip_init: this library is built for ") + ORMI_HIP_TARGET +
+                                                  "; device " + std::to_string(device) + " is " + props.gcnArchName);
     ORMI_HIP_TRY(hipSetDevice(device));
-    ORMI_HIP_TRY(hipGetDeviceProperties(&s.props, device));
+    s.props = props;
     const int rc = gemm_scratch_setup();
     if (rc != ORMI_HIP_OK) return rc;
     s.arch = s.props.gcnArchName;
