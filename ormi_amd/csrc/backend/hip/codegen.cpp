@@ -112,18 +112,18 @@ namespace ormi::hip {
 
     // Dynamic LDS that lets at most n work-groups of a kernel share one CU
     // (gfx950: 160 KB of LDS per CU, allocated in 512-byte units), leaving
-    // 1 KB per work-group for the kernel's own LDS; 0 when n is 0 or the
-    // grid would not fill n per CU anyway. Fewer concurrent streams use HBM
-    // better where a kernel writes about as much as it reads, or where its
+    // 1 KB per work-group for the kernel's own LDS; 0 when n is 0 or the grid
+    // would not fill n per CU anyway. Fewer concurrent streams use HBM better
+    // where a kernel writes about as much as it reads, or where its
     // work-groups read long streams, down to the point where too few waves
-    // are left to cover the arithmetic; short-lived read-only work-groups
-    // need every slot (the ceiling probe's 8 KB-per-work-group read: 7.13 TB/s
-    // uncapped, 6.37 at 5 per CU, 4.25 at 3). Measured on C2's shapes: the copy y = -x took 43.7-43.8 us
-    // at the 8 per CU its registers allow, 42.0-42.3 at 5; C2's chain 44.4 at
-    // 8, 44.1 at 5, 45.4-45.6 at 4. C3's row sum with four waves per 32 KB
-    // row 79.7-80.2 us at 8, 76.1-76.4 at 3; its row max 80.3-80.4 at 8,
-    // 75.9-76.1 at 4, 82.1-82.4 at 3 (each element extends a dependent
-    // (value, index) chain).
+    // are left to cover the arithmetic. Short-lived read-only work-groups
+    // need every slot instead (a one-shot 8 KB read per work-group: 7.13 TB/s
+    // uncapped, 6.37 at 5 per CU, 4.25 at 3). Measured on C2's shapes: the
+    // copy y = -x took 43.7-43.8 us at the 8 per CU its registers allow and
+    // 42.0-42.3 at 5; C2's chain 44.4 at 8, 44.1 at 5, 45.4-45.6 at 4. C3's
+    // row sum with four waves per 32 KB row took 79.7-80.2 us at 8 and
+    // 76.1-76.4 at 3; its row max 80.3-80.4 at 8, 75.9-76.1 at 4 and
+    // 82.1-82.4 at 3 (each element extends a dependent (value, index) chain).
     static uint32_t occupancy_lds(int n, long long grid, int cu) {
         if (n <= 0 || grid <= (long long)n * std::max(cu, 1)) return 0;
         constexpr int kCuLds = 160 * 1024;
