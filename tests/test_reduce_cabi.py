@@ -141,6 +141,7 @@ def graph_reduce(x, op, axes, dev):
 CASES = [
     # name, shape, axes
     ("row", (1024, 8192), (1,)),
+    ("row_shared", (4103, 4108), (1,)),   # four waves per row, work-group cap
     ("row_few_rows", (3, 100003), (1,)),
     ("col", (4096, 2048), (0,)),
     ("col_ragged", (777, 131), (0,)),
