@@ -168,11 +168,12 @@ def test_column_and_global_sums_of_a_broadcast_map(lib, cpu, hip, axes):
 def test_max_and_argmax_of_a_scaled_shifted_input(lib, cpu, hip, op):
     """max / argmax over rows of x * s - t (t a per-row column (R, 1)), on a
     transposed x and with ties: exact against numpy and the oracle; the few-row
-    case (3 rows of 100003) takes two passes, once with the caller's workspace."""
+    case (3 rows of 100003) takes two passes, once with the caller's workspace,
+    and 4100 rows of 1100 are shared by four waves each (strided, scalar loads)."""
     from ormi_amd import Tensor
 
     rng = np.random.default_rng(83 + op)
-    for rows, cols in ((2048, 1000), (3, 100003)):
+    for rows, cols in ((2048, 1000), (3, 100003), (4100, 1100)):
         base = rng.integers(-20, 20, (cols, rows)).astype(np.float32)   # stored transposed
         x = base.T                                                     # (rows, cols), strides (1, rows)
         t = rng.integers(-3, 3, (rows, 1)).astype(np.float32)
