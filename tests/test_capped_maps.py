@@ -46,3 +46,12 @@ def test_capped_maps_are_exact(hip):
     assert same_bits((X + Y).numpy(), x + y)
     assert same_bits((X + Y + Z).numpy(), (x + y) + z)
     assert same_bits(X.astype("bfloat16").numpy(), bf16_nearest_f64(x))
+    # a 64 MiB bf16 leaf: its 16-bit vector loads carry the non-temporal hint
+    X16 = T(x, hip, dtype="bfloat16")
+    assert same_bits((X16 * 1.0).numpy(), bf16_nearest_f64(x))
+
+
+def test_bf16_leaf_of_64_mib_takes_the_load_hint(ob, cpu):
+    x = arrays()[0]
+    src = ob._plan_kernel((T(x, cpu, dtype="bfloat16") * 1.0)._node)["source"].split('extern "C"')[1]
+    assert "__builtin_nontemporal_load((const ormi_u16x4*)" in src, src
