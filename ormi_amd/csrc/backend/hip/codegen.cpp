@@ -96,6 +96,8 @@ namespace ormi::hip {
             x.col_waves = std::clamp(env_int("ORMI_COL_WAVES", x.col_waves), 1, 16);
             x.col_cwaves = std::clamp(env_int("ORMI_COL_CWAVES", x.col_cwaves), 1, 16);
             x.col_unroll = std::clamp(env_int("ORMI_COL_UNROLL", x.col_unroll), 1, 8);
+            x.col_fin_split = env_int("ORMI_COL_FIN_SPLIT", x.col_fin_split);
+            if (x.col_fin_split != 1 && x.col_fin_split != 2 && x.col_fin_split != 4 && x.col_fin_split != 8) x.col_fin_split = 1;
             x.map_wg_per_cu = std::clamp(env_int("ORMI_MAP_WG_PER_CU", x.map_wg_per_cu), 0, 32);
             x.row_wg_per_cu = std::clamp(env_int("ORMI_ROW_WG_PER_CU", x.row_wg_per_cu), 0, 32);
             x.row_max_wg_per_cu = std::clamp(env_int("ORMI_ROW_MAX_WG_PER_CU", x.row_max_wg_per_cu), 0, 32);
@@ -653,7 +655,7 @@ namespace ormi::hip {
             s += kind;
             s += '|';
             for (long long v : {(long long)t.map_unroll, (long long)t.row_unroll, (long long)t.col_waves, (long long)t.row_waves,
-                                (long long)t.row_waves_min_groups, (long long)t.col_unroll}) {
+                                (long long)t.row_waves_min_groups, (long long)t.col_unroll, (long long)t.col_fin_split}) {
                 append_int(s, v);
                 s += ',';
             }
@@ -1385,17 +1387,42 @@ namespace ormi::hip {
             declare_epilogue(g2, ep);
             g2.args.i64("NE", O * I);
             g2.args.i64("NP", P);
-            s2.grid[0] = (uint32_t)std::max(1LL, (O * I + 255) / 256);
+            // Sums: FS lanes per column, each adding a consecutive run of parts
+            // in part order, then lane 0 of the column adds the FS runs in order.
+            const int FS = is_sum ? tn.col_fin_split : 1;
+            s2.grid[0] = (uint32_t)std::max(1LL, (O * I * FS + 255) / 256);
             s2.plan.kind = "column-finish";
             s2.plan.op = name;
-            resolve(g2, std::string("colfin") + name, 256, s2, [&] {
+            s2.plan.add("lanes_per_column", FS);
+            resolve(g2, std::string("colfin") + name + (FS > 1 ? "_s" + std::to_string(FS) : std::string()), 256, s2, [&] {
                 std::ostringstream& sb = g2.body();
-                sb << "  const long long e = (long long)blockIdx.x * 256 + threadIdx.x;\n";
-                sb << "  if (e >= NE) return;\n";
                 // Parts are combined in part order; their loads are issued FIN at a
                 // time (one round trip per FIN parts, not one per part). 16 measured
                 // best: 64 loads in flight with 64-thread blocks was slower.
                 constexpr int FIN = 16;
+                if (FS > 1) {
+                    // All lanes reach the shuffles: a lane past the last column
+                    // reads column NE-1 and stores nothing.
+                    sb << "  const long long ex = ((long long)blockIdx.x * 256 + threadIdx.x) / " << FS << ";\n";
+                    sb << "  const int q = threadIdx.x % " << FS << ";\n";
+                    sb << "  const long long e = ex < NE ? ex : NE - 1;\n";
+                    sb << "  const long long run = (NP + " << FS - 1 << ") / " << FS << ", p0 = q * run;\n";
+                    sb << "  const long long p1 = p0 + run < NP ? p0 + run : NP;\n";
+                    sb << "  float s = 0.0f;\n  for (long long q0 = p0; q0 < p1; q0 += " << FIN << ") {\n";
+                    sb << "    float v[" << FIN << "];\n";
+                    sb << "#pragma unroll\n    for (int j = 0; j < " << FIN << "; ++j) v[j] = q0 + j < p1 ? pvals[(q0 + j) * NE + e] : 0.0f;\n";
+                    sb << "#pragma unroll\n    for (int j = 0; j < " << FIN << "; ++j) if (q0 + j < p1) s += v[j];\n  }\n";
+                    sb << "  const int lane = threadIdx.x & 63;\n";
+                    sb << "  float t = s;\n";
+                    sb << "#pragma unroll\n  for (int k = 1; k < " << FS << "; ++k) t += __shfl(s, lane + k, 64);\n";
+                    sb << "  if (q != 0 || ex >= NE) return;\n";
+                    sb << "  s = t;\n";
+                    sb << "  ((float*)outp)[e] = s;\n";
+                    emit_epilogue(sb, "  ", ep, "s", "e");
+                    return;
+                }
+                sb << "  const long long e = (long long)blockIdx.x * 256 + threadIdx.x;\n";
+                sb << "  if (e >= NE) return;\n";
                 if (is_sum) {
                     sb << "  float s = 0.0f;\n  for (long long q0 = 0; q0 < NP; q0 += " << FIN << ") {\n";
                     sb << "    float v[" << FIN << "];\n";

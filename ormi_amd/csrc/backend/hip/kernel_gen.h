@@ -110,6 +110,7 @@ namespace ormi::hip {
         int col_waves = 16;        // waves per block (column reduce)
         int col_cwaves = 8;        // of those, waves side by side across the kept columns
         int col_unroll = 2;        // rows in flight per wave (column reduce)
+        int col_fin_split = 4;     // lanes per column in a column sum's finish pass (1, 2, 4 or 8)
         // Work-groups resident per CU for map / row-reduction kernels whose grid
         // would hold more (0: no cap). HBM streams run faster with fewer
         // concurrent ones: see occupancy_lds.
