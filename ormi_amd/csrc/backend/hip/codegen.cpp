@@ -1261,7 +1261,7 @@ namespace ormi::hip {
         // the kept extent is narrow.
         const long long IG = I / V;
         int WC = 1;
-        while (WC * 2 <= tn.col_cwaves && WC * 64LL < IG) WC *= 2;
+        while (WC * 2 <= std::min(tn.col_cwaves, tn.col_waves) && WC * 64LL < IG) WC *= 2;
         const int WR = std::max(1, tn.col_waves / WC);
         const int W = WC * WR;
         const int block = 64 * W;

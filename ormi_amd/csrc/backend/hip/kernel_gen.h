@@ -108,7 +108,7 @@ namespace ormi::hip {
         int row_waves = 4;         // waves sharing one long row (row reduce; 1, 2 or 4)
         int row_waves_min_groups = 1024;  // row length (VEC groups) from which rows are shared
         int col_waves = 16;        // waves per block (column reduce)
-        int col_cwaves = 8;        // of those, waves side by side across the kept columns
+        int col_cwaves = 16;       // of those, waves side by side across the kept columns
         int col_unroll = 2;        // rows in flight per wave (column reduce)
         int col_fin_split = 4;     // lanes per column in a column sum's finish pass (1, 2, 4 or 8)
         // Work-groups resident per CU for map / row-reduction kernels whose grid

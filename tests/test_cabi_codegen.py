@@ -326,7 +326,7 @@ def test_map_and_reduce_plans_past_2_31_use_64_bit_indices(ob, cpu):
 
 def test_column_kernels_keyed_by_column_waves(ob, cpu, cabi):
     """A column reduction's waves across columns follow the kept extent (1 for 6
-    columns, 2 for 70, 4 for 2048), and the emitted body depends on it, so the
+    columns, 2 for 70, 8 for 2048), and the emitted body depends on it, so the
     kernel cache keys it: a narrow plan compiled first must not serve a wider one
     whose grid assumes more columns per block."""
     seen = {}
