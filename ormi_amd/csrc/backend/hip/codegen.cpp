@@ -99,6 +99,7 @@ namespace ormi::hip {
             x.col_fin_split = env_int("ORMI_COL_FIN_SPLIT", x.col_fin_split);
             if (x.col_fin_split != 1 && x.col_fin_split != 2 && x.col_fin_split != 4 && x.col_fin_split != 8) x.col_fin_split = 1;
             x.map_wg_per_cu = std::clamp(env_int("ORMI_MAP_WG_PER_CU", x.map_wg_per_cu), 0, 32);
+            x.map_row_tile_wg_per_cu = std::clamp(env_int("ORMI_MAP_ROW_TILE_WG_PER_CU", x.map_row_tile_wg_per_cu), 0, 32);
             x.row_wg_per_cu = std::clamp(env_int("ORMI_ROW_WG_PER_CU", x.row_wg_per_cu), 0, 32);
             x.row_max_wg_per_cu = std::clamp(env_int("ORMI_ROW_MAX_WG_PER_CU", x.row_max_wg_per_cu), 0, 32);
             x.map_nt_loads = env_int("ORMI_MAP_NT_LOADS", x.map_nt_loads) != 0;
@@ -107,6 +108,7 @@ namespace ormi::hip {
             x.map_nt_stores = env_int("ORMI_MAP_NT_STORES", x.map_nt_stores) != 0;
             x.map_off32 = env_int("ORMI_MAP_OFF32", x.map_off32) != 0;
             x.map_rows = env_int("ORMI_MAP_ROWS", x.map_rows) != 0;
+            x.map_row_tiles = env_int("ORMI_MAP_ROW_TILES", x.map_row_tiles) != 0;
             return x;
         }();
         return t;
@@ -831,7 +833,7 @@ namespace ormi::hip {
         const long long G = numel / g.vec;
         const long long tile = (long long)block * unroll;
         const long long tiles = (G + tile - 1) / tile;
-        const long long grid = std::max(1LL, std::min(tiles, (long long)std::max(cu, 1) * tn.map_blocks_per_cu));
+        long long grid = std::max(1LL, std::min(tiles, (long long)std::max(cu, 1) * tn.map_blocks_per_cu));
         // The grid-stride cursor reaches G + grid * tile before the loop exits.
         int out_bytes = 1;
         for (DType dt : out_dtypes) out_bytes = std::max(out_bytes, (int)dtype_size(dt));
@@ -848,7 +850,12 @@ namespace ormi::hip {
         //          coordinates are uniform per tile, so they and the loads of
         //          operands that vary only across rows are scalar work, and every
         //          tile is full, so stores need no bounds guard;
-        //  rows 3: a tile is exactly one row (tile == Dl): both of the above.
+        //  rows 3: a tile is exactly one row (tile == Dl): both of the above;
+        //  rows 4: rows 2 where operands vary only along the last dim (a bias
+        //          row): a tile is `unroll` consecutive rows of one 256-group
+        //          window (NW = Dl / 256 windows per row), so each lane loads those
+        //          operands once for all its rows. The grid is a multiple of NW,
+        //          so a block keeps its window and loads them once per block.
         const int n_last = n - 1;
         const long long Dl = g.c.dims[n_last].size / g.vec;
         if (tn.map_rows && g.idx32 && n >= 2 && Dl > 0) {
@@ -856,16 +863,34 @@ namespace ormi::hip {
             else if (tile % Dl == 0) g.rows = 1;
             else if (Dl % tile == 0) g.rows = 2;
         }
+        // Leaves that vary only along the last dim: zero stride on every outer dim.
+        std::vector<bool> only_last(expr.leaves.size(), false);
+        bool any_only_last = false;
+        for (size_t L = 0; L < expr.leaves.size(); ++L) {
+            if (g.scalar[L]) continue;
+            bool o = true;
+            for (int d = 0; d < n_last; ++d) o = o && g.c.st[L][d] == 0;
+            only_last[L] = o;
+            any_only_last = any_only_last || o;
+        }
+        long long NW = 0;
+        const long long R = Dl > 0 ? G / Dl : 0;
+        if (g.rows == 2 && any_only_last && tn.map_row_tiles && unroll > 1 && R % unroll == 0) {
+            NW = Dl / block;
+            const long long gr = grid / NW * NW;
+            if (gr >= NW) {
+                g.rows = 4;
+                grid = gr;
+            }
+        }
         const int rows = g.rows;
-        // Leaves loaded once before the loop (rows 1 and 3): zero stride on every outer dim.
+        // Leaves loaded once before the loop (rows 1, 3 and 4).
         std::vector<bool> hoist(expr.leaves.size(), false), in_loop(expr.leaves.size(), true);
-        if (rows == 1 || rows == 3)
+        if (rows == 1 || rows == 3 || rows == 4)
             for (size_t L = 0; L < expr.leaves.size(); ++L) {
                 if (g.scalar[L]) continue;
-                bool only_last = true;
-                for (int d = 0; d < n_last; ++d) only_last = only_last && g.c.st[L][d] == 0;
-                hoist[L] = only_last;
-                in_loop[L] = !only_last;
+                hoist[L] = only_last[L];
+                in_loop[L] = !only_last[L];
             }
 
         // A single output keeps the name "out"; several are out0, out1, ...
@@ -881,13 +906,21 @@ namespace ormi::hip {
             g.args.i64("R", G / Dl);
             g.args.i64("P", tile / Dl);
         }
+        if (rows == 4) {
+            g.args.i64("R", R);
+            g.args.i64("NW", NW);
+        }
         k.grid[0] = (uint32_t)grid;
         // The cap pays where the kernel writes about as much as it reads (a
         // copy, C2); a kernel that mostly reads keeps every slot (the capped
-        // read-only kernels of the ceiling probe ran slower).
+        // read-only kernels of the ceiling probe ran slower). Tiles of several
+        // rows take one more work-group per CU: C2 on them ran 43.6-43.9 us at
+        // 6, 44.2-44.6 at 5 and 44.2-44.4 at 7, against 44.0-44.1 on one-row
+        // tiles at 5 (44.3-44.6 at 6).
         long long write_bytes = 0;
         for (DType dt : out_dtypes) write_bytes += (long long)dtype_size(dt);
-        if (2 * write_bytes >= g.streamed_bytes(1)) k.lds = occupancy_lds(tn.map_wg_per_cu, grid, cu);
+        if (2 * write_bytes >= g.streamed_bytes(1))
+            k.lds = occupancy_lds(rows == 4 ? tn.map_row_tile_wg_per_cu : tn.map_wg_per_cu, grid, cu);
         k.plan.kind = "map";
         k.plan.add("ndim", n);
         k.plan.add("vec", g.vec);
@@ -970,6 +1003,29 @@ namespace ormi::hip {
                 b << "      const " << t << " " << cl << " = (col0 + " << lane << ") * " << V << ";\n";
                 load_all("      ", in_loop);
                 b << "    }\n";
+            } else if (rows == 4) {
+                // The grid is a multiple of NW, so a block's window (blockIdx.x
+                // mod NW) is the same in every tile it visits; its rows advance
+                // by gridDim.x / NW tiles of `unroll` rows.
+                b << "  const " << t << " col0 = ((" << t << ")blockIdx.x % (" << t << ")NW) * " << block << ";\n";
+                b << "  const " << t << " " << cl << " = (col0 + " << tid << ") * " << V << ";\n";
+                g.declare_leaf_regs(b, "  ", unroll, hoist);
+                b << "  {\n    const int u = 0;\n";
+                load_all("    ", hoist);
+                b << "  }\n";
+                for (size_t L = 0; L < expr.leaves.size(); ++L)
+                    if (hoist[L])
+                        b << "#pragma unroll\n  for (int u = 1; u < " << unroll << "; ++u)\n#pragma unroll\n    for (int k = 0; k < "
+                          << V << "; ++k) x" << L << "[u][k] = x" << L << "[0][k];\n";
+                b << "  for (" << t << " row0 = (" << t << ")blockIdx.x / (" << t << ")NW * " << unroll << "; row0 < (" << t
+                  << ")R; row0 += (" << t << ")gridDim.x / (" << t << ")NW * " << unroll << ") {\n";
+                g.declare_leaf_regs(b, "    ", unroll, in_loop);
+                b << "#pragma unroll\n    for (int u = 0; u < " << unroll << "; ++u) {\n";
+                b << "      const " << t << " row = row0 + u;\n";
+                g.declare_coords(b, "      ", outer);
+                g.decompose(b, "      ", "row", outer);
+                load_all("      ", in_loop);
+                b << "    }\n";
             } else {
                 b << "  for (" << t << " base = (" << t << ")blockIdx.x * tile; base < (" << t << ")G; base += (" << t
                   << ")gridDim.x * tile) {\n";
@@ -991,7 +1047,8 @@ namespace ormi::hip {
             g.eval(b, "        ", "u", "k");
             for (size_t r = 0; r < nout; ++r) b << "        " << res(r) << "[k] = " << g.root_names[r] << ";\n";
             b << "      }\n";
-            b << "      const " << t << " go = base + " << lane << ";\n";
+            if (rows == 4) b << "      const " << t << " go = (row0 + u) * (" << t << ")" << Dn << " + col0 + " << tid << ";\n";
+            else b << "      const " << t << " go = base + " << lane << ";\n";
             if (guard) b << "      if (go < (" << t << ")G) {\n";
             const std::string ind = guard ? "        " : "      ";
             const bool nt = tn.map_nt_stores;

@@ -115,6 +115,7 @@ namespace ormi::hip {
         // would hold more (0: no cap). HBM streams run faster with fewer
         // concurrent ones: see occupancy_lds.
         int map_wg_per_cu = 5;
+        int map_row_tile_wg_per_cu = 6;  // the same for maps on tiles of several rows (bias rows)
         int row_wg_per_cu = 3;      // row sums
         int row_max_wg_per_cu = 4;  // row max / argmax: a longer dependent chain per element
         bool map_nt_loads = true;     // non-temporal hint on a map's operand loads
@@ -125,6 +126,7 @@ namespace ormi::hip {
         long long nt_min_bytes = 64LL << 20;
         bool map_off32 = true;        // 32-bit byte offsets from uniform bases when they fit (map)
         bool map_rows = true;         // row-aligned tiles when a tile covers whole rows or lies in one (map)
+        bool map_row_tiles = true;    // tiles of `unroll` rows x 256 groups when an operand is a bias row (map)
     };
     const Tuning& tuning();
 

@@ -158,10 +158,12 @@ def test_generated_map_kernel_structure(ob, cpu, cabi):
 
 
 def row_mode_shapes(tile):
-    """(rows, cols) of fp32 maps whose tile of `tile` groups of 4 floats spans
-    whole rows (1), lies inside one row (2), is one row (3) or neither (0)."""
-    return {1: [(64, 128), (512, 256)], 3: [(8, 4 * tile), (512, 4 * tile)], 2: [(4, 8 * tile), (2, 12 * tile)],
-            0: [(10, 100), (7, 300)]}
+    """(rows, cols) of fp32 maps over a bias row whose tile of `tile` groups of 4
+    floats spans whole rows (1), lies inside one row (2: an odd row count), is
+    one row (3) or neither (0); with an even row count a tile inside one row
+    becomes `unroll` rows of one 256-group window (4)."""
+    return {1: [(64, 128), (512, 256)], 3: [(8, 4 * tile), (512, 4 * tile)], 2: [(3, 8 * tile), (5, 12 * tile)],
+            4: [(4, 8 * tile), (2, 12 * tile)], 0: [(10, 100), (7, 300)]}
 
 
 def test_kernel_source_is_shape_independent(ob, cpu):
@@ -178,11 +180,29 @@ def test_kernel_source_is_shape_independent(ob, cpu):
         assert f"rows={mode}" in a["plan"] and f"rows={mode}" in b["plan"], (a["plan"], b["plan"])
         assert a["name"] == b["name"] and a["source"] == b["source"]
         names[mode] = a["name"]
-    assert len(set(names.values())) == 4
+    assert len(set(names.values())) == 5
     assert plan(64, 128)["name"] != ob._plan_kernel((_cpu(np.zeros((64, 128))) * 2.0).exp()._node)["name"]
 
 
-@pytest.mark.parametrize("mode", [1, 2, 3, 0])
+def test_row_tiles_keep_a_window_per_block(ob, cpu):
+    """Tiles of `unroll` rows: the grid is a multiple of the 256-group windows of
+    a row (a block keeps its window while it walks rows), rounded down from the
+    64 blocks per CU when there are more tiles; an odd row count keeps one-row
+    tiles."""
+    tile = map_tile_groups(ob)
+
+    def plan(r, c):
+        X, B = _cpu(np.zeros((r, c))), _cpu(np.zeros(c))
+        return ob._plan_kernel(((X + B) * 2.0)._node)
+
+    for (r, c), grid in [((6, 12 * tile), 18), ((5472, 12 * tile), 16380), ((8200, 8 * tile), 16384)]:
+        d = plan(r, c)
+        windows = c // 4 // 256
+        assert "rows=4" in d["plan"] and d["grid"][0] == grid and grid % windows == 0, (r, c, d["plan"], d["grid"])
+    assert "rows=2" in plan(5471, 12 * tile)["plan"]
+
+
+@pytest.mark.parametrize("mode", [1, 2, 3, 4, 0])
 @pytest.mark.parametrize("variant", ["plain", "3d", "vec1", "multi"])
 def test_row_aligned_map_kernels_compile(ob, cpu, cabi, mode, variant):
     """Every tile alignment compiles for gfx950: two dims and three (outer
@@ -191,12 +211,12 @@ def test_row_aligned_map_kernels_compile(ob, cpu, cabi, mode, variant):
     one kernel."""
     tile = map_tile_groups(ob)
     r, c = row_mode_shapes(tile)[mode][0]
-    if variant == "vec1" and mode in (2, 3):
+    if variant == "vec1" and mode in (2, 3, 4):
         c //= 4
     x, bias, scale = _cpu(np.ones((r, c))), _cpu(np.ones(c)), _cpu(np.ones((r, 1)))
-    if variant == "3d":
-        x = _cpu(np.ones((2, 1, c))) * _cpu(np.ones((1, r, c)))
-        scale = _cpu(np.ones((2, r, 1)))
+    if variant == "3d":  # 3 r rows: odd for mode 2, even for mode 4
+        x = _cpu(np.ones((3, 1, c))) * _cpu(np.ones((1, r, c)))
+        scale = _cpu(np.ones((3, r, 1)))
     z = ((x + bias) * scale - x * 0.5)._node
     if variant == "vec1":
         z = ob.add(z, _view_leaf(ob, np.ones(r * c), [r, c], [1, r]))

@@ -3,7 +3,8 @@
 A map over a large grid that writes at least half as many bytes as it streams
 in (a copy, C2's chain, a two-input sum, a cast to bf16) is launched with an
 LDS reservation it never touches, so at most 5 of its work-groups share a CU;
-one that mostly reads (three inputs, one output) is not. The reservation
+one that mostly reads (three inputs, one output) is not. A map on tiles of
+two rows (over a bias row) takes at most 6. The reservation
 changes where work-groups run, never what they compute.
 
 CPU: which plans carry the reservation. GPU: the capped kernels bit for bit
@@ -35,6 +36,10 @@ def test_which_maps_are_capped(ob, cpu):
     for name, t in capped.items():
         assert ob._plan_kernel(t._node)["lds"] > 0, name
     assert ob._plan_kernel((X + Y + Z)._node)["lds"] == 0
+    # C2's chain over a bias row: tiles of two rows, at most 6 work-groups per CU
+    B, S = T(np.zeros(SHAPE[1], np.float32), cpu), T(np.ones((SHAPE[0], 1), np.float32), cpu)
+    c2 = ob._plan_kernel((((X + B) * S).tanh() * X.sigmoid() - 0.1 * X * X)._node)
+    assert "rows=4" in c2["plan"] and c2["lds"] == (160 * 1024 // 6 - 1024) // 512 * 512, c2["plan"]
     assert ob._plan_kernel((T(x[:256], cpu) * 2.0)._node)["lds"] == 0  # 256 work-groups: one per CU
 
 
@@ -45,6 +50,8 @@ def test_capped_maps_are_exact(hip):
     assert same_bits((X * 2.0).numpy(), x * np.float32(2.0))
     assert same_bits((X + Y).numpy(), x + y)
     assert same_bits((X + Y + Z).numpy(), (x + y) + z)
+    b, sc = y[0].copy(), z[:, :1].copy()  # a bias row and a per-row scale: tiles of two rows
+    assert same_bits(((X + T(b, hip)) * T(sc, hip) - X).numpy(), (x + b) * sc - x)
     assert same_bits(X.astype("bfloat16").numpy(), bf16_nearest_f64(x))
     # a 64 MiB bf16 leaf: its 16-bit vector loads carry the non-temporal hint
     X16 = T(x, hip, dtype="bfloat16")

@@ -224,7 +224,9 @@ def test_views_and_strides_as_leaves(cpu, hip):
 # group is 4 floats when every operand allows 128-bit accesses, else 1).
 # rows=1: a tile spans P whole rows (lane constants, last-dim-only operands
 # loaded once, a partial last tile when P does not divide the row count);
-# rows=2: a tile lies in one row; rows=3: a tile is one row; rows=0: neither.
+# rows=2: a tile lies in one row; rows=3: a tile is one row; rows=0: neither;
+# rows=4: rows=2 over a bias row with an even row count, the tile `unroll` rows
+# of one 256-group window (the bias loaded once per lane for all of them).
 def row_graph(dev, x, bias, scale, xt=None):
     X, B, S = T(x, dev), T(bias, dev), T(scale, dev)
     z = (X + B) * S - X * 0.5
@@ -246,10 +248,13 @@ def row_case(tile, case):
     """(shape, rows mode, 1-float groups) for a tile of `tile` groups."""
     return {"span": ((33, 256), 1, False), "span_full": ((32, 256), 1, False), "span_vec1": ((33, 256), 1, True),
             "one": ((6, 4 * tile), 3, False), "one_vec1": ((5, tile), 3, True), "inside": ((3, 8 * tile), 2, False),
-            "inside_vec1": ((2, 3 * tile), 2, True), "none": ((7, 300), 0, False)}[case]
+            "inside_vec1": ((3, 3 * tile), 2, True), "rowtile": ((4, 8 * tile), 4, False),
+            "rowtile_vec1": ((2, 3 * tile), 4, True), "rowtile_nw6": ((6, 12 * tile), 4, False),
+            "none": ((7, 300), 0, False)}[case]
 
 
-@pytest.mark.parametrize("case", ["span", "span_full", "span_vec1", "one", "one_vec1", "inside", "inside_vec1", "none"])
+@pytest.mark.parametrize("case", ["span", "span_full", "span_vec1", "one", "one_vec1", "inside", "inside_vec1", "rowtile",
+                                  "rowtile_vec1", "rowtile_nw6", "none"])
 def test_row_aligned_map_tiles(ob, cpu, hip, case):
     shape, mode, vec1 = row_case(map_tile_groups(ob), case)
     x, bias, scale, xt = row_inputs(*shape, vec1)
@@ -278,7 +283,24 @@ def test_row_aligned_map_tiles_3d(ob, cpu, hip, mode):
     assert_bits_equal(z.numpy(), graph(cpu).numpy())
 
 
-@pytest.mark.parametrize("case", ["span", "span_vec1", "one", "inside"])
+def test_row_tiles_3d(ob, cpu, hip):
+    """Tiles of two rows over a bias row with three dims that do not merge: each
+    row's outer coordinates come from its own index by division."""
+    c = 8 * map_tile_groups(ob)
+    rng = np.random.default_rng(34)
+    a, s, bias = (rng.standard_normal(sh).astype(np.float32) for sh in ((4, 1, c), (4, 3, 1), (c,)))
+
+    def graph(dev):
+        A, C, B = T(a, dev), T(s, dev), T(bias, dev)
+        return (A + B) * C - A / (C * C + 1.0)
+
+    z = graph(hip)
+    plan = ob._plan_kernel(z._node)["plan"]
+    assert "rows=4" in plan and "ndim=3" in plan, plan
+    assert_bits_equal(z.numpy(), graph(cpu).numpy())
+
+
+@pytest.mark.parametrize("case", ["span", "span_vec1", "one", "inside", "rowtile", "rowtile_nw6"])
 def test_row_aligned_map_tiles_grid_stride(ob, hip, case):
     """More tiles than the grid holds (64 blocks per CU), so every block walks
     several tiles and the row cursor advances with the grid stride. The chain is
@@ -290,7 +312,9 @@ def test_row_aligned_map_tiles_grid_stride(ob, hip, case):
     shape, mode, vec1 = {"span": ((grid * tile // 64 + 17, 256), 1, False),  # 64 groups a row
                          "span_vec1": ((grid * tile // 256 + 5, 256), 1, True),  # 256 groups a row
                          "one": ((grid + 16, 4 * tile), 3, False),
-                         "inside": ((grid // 2 + 8, 8 * tile), 2, False)}[case]
+                         "inside": ((grid // 2 + 9, 8 * tile), 2, False),
+                         "rowtile": ((grid // 2 + 8, 8 * tile), 4, False),  # 4 windows a row
+                         "rowtile_nw6": ((grid // 3 + 11, 12 * tile), 4, False)}[case]  # 6 windows: grid rounded to 16380
     x, bias, scale, xt = row_inputs(*shape, vec1, seed=33)
     z = row_graph(hip, x, bias, scale, xt)
     plan = ob._plan_kernel(z._node)["plan"]
