@@ -169,7 +169,7 @@ def cpu_baseline_c2(target_s: float = 10.0) -> dict:
     t0 = time.perf_counter()
     c2_graph(X, B, S).numpy()
     one = time.perf_counter() - t0
-    reps = max(1, min(20, int(target_s / max(one, 1e-3))))
+    reps = max(1, min(100, int(target_s / max(one, 1e-3))))
     t0 = time.perf_counter()
     for _ in range(reps):
         c2_graph(X, B, S).realize()
