@@ -1627,15 +1627,16 @@ def main():
         out_md = Path(args.mfma_report[1])
         mfma_report(Path(args.mfma_report[0]), out_md,
                     "rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_MFMA SQ_LDS_BANK_CONFLICT GRBM_GUI_ACTIVE "
-                    f"--kernel-trace -d gpurun_out/pmc_mfma_{only} -o run --output-format csv -- python3 bench.py "
+                    f"--kernel-trace -d {args.mfma_report[0]} -o run --output-format csv -- python3 bench.py "
                     f"--only {only} --steps {30 if only == 'c5' else 5} --warmup 1; python3 bench.py --only {only} "
-                    f"--mfma-report gpurun_out/pmc_mfma_{only} {out_md.as_posix()}")
+                    f"--mfma-report {args.mfma_report[0]} {out_md.as_posix()}")
         return
     if args.wave_report:
         wave_report(args.wave_report[:2], Path(args.wave_report[2]),
-                    " ; ".join(f"rocprofv3 --pmc {c} --kernel-trace -d gpurun_out/pmc_{k} -o run --output-format csv "
-                               "-- python3 bench.py --only c4 --steps 5 --warmup 1" for k, c in zip("ab", WAVE_COUNTERS))
-                    + " ; python3 bench.py --wave-report gpurun_out/pmc_a gpurun_out/pmc_b profiles/gemm_wave_states.md")
+                    " ; ".join(f"rocprofv3 --pmc {c} --kernel-trace -d {d} -o run --output-format csv "
+                               "-- python3 bench.py --only c4 --steps 5 --warmup 1"
+                               for d, c in zip(args.wave_report[:2], WAVE_COUNTERS))
+                    + f" ; python3 bench.py --wave-report {' '.join(args.wave_report)}")
         return
     if args.pmc_report:
         pmc_report(Path(args.pmc_report[0]), Path(args.pmc_report[1]),
